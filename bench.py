@@ -1,0 +1,291 @@
+"""Benchmark of diff-gpt's attention hot path on one MI355X.
+
+Default workload: 64 series x 100 trajectories =
+6400 concurrent sequences of the README GPT geometry (2 layers, 4 heads,
+head_dim 16), a shared 96-token prefix per series already broadcast into the
+KV cache, then 48 decode steps (L_kv 97..144).  One bench step = that whole
+decode job through the hot path: per decode step and layer, one fused
+RoPE + QK-norm + KV-append launch and one decode-attention launch, on
+synthetic q/k/v resident in HBM.
+
+    python bench.py [--steps K] [--warmup W] [--dtype fp32|bf16] [--no-prefill]
+                    [--no-cpu-baseline] [--traffic-json FILE]
+
+Prints ONE JSON line.  value = sequences*48*K / timed seconds (tokens/s).
+roofline = decode-attention kernel: algorithmic bytes per launch
+B*H*es*(2*L_kv*D + 2*D) over its mean launch time, timed with HIP events on
+the launch stream inside the timed region.  The prefill leg (configs[2]:
+B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s with
+FLOP = 2*B*H*D*T*(T+1).  cpu_baseline = the oracle's torch-CPU restatement of
+the reference decode path on a bounded sample, on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "diff-gpt_amd", REPO):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "decode attn tokens/s + % HBM roofline; prefill attn TFLOP/s, 1×MI355X"
+
+# configs[1] geometry
+SERIES, TRAJ, PREFIX, NEW = 64, 100, 96, 48
+LAYERS, HEADS, HEAD_DIM = 2, 4, 16
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_job(dtype_name: str, steps: int, warmup: int):
+    import torch
+
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    dev = torch.device("cuda:0")
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
+    es = 4 if dt == torch.float32 else 2
+    ops = _native.ops()
+    B, H, D, L = SERIES * TRAJ, HEADS, HEAD_DIM, LAYERS
+    cap = PREFIX + NEW
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    # KV cache (L,2,B,H,cap,D): per-series prefix broadcast to its 100 rows
+    # (KVCache.prefill), positions >= PREFIX written by the decode job.
+    cache = torch.empty((L, 2, B, H, cap, D), dtype=dt, device=dev)
+    prefix = torch.randn((L, 2, SERIES, 1, H, PREFIX, D), generator=g, device=dev).to(dt)
+    cache.view(L, 2, SERIES, TRAJ, H, cap, D)[..., :PREFIX, :] = prefix
+    table = precompute_freqs_cis(D, 2 * 138, 10000).to(dev).to(dt)
+    # synthetic projections for every (step, layer): q, k, v (B,1,H,D)
+    qkv = torch.randn((NEW, L, 3, B, 1, H, D), generator=g, device=dev).to(dt)
+    q_rot = torch.empty((B, 1, H, D), dtype=dt, device=dev)
+    y = torch.empty((B, 1, H, D), dtype=dt, device=dev)
+    torch.cuda.synchronize()
+
+    ev = []  # (start, end) events around each decode-attention launch
+
+    def run_job(record: bool):
+        for s in range(NEW):
+            t0 = PREFIX + s
+            fc = table[t0:t0 + 1].view(1, 1, 1, D // 2, 2)
+            for layer in range(L):
+                q, k, v = qkv[s, layer]
+                kd = cache[layer, 0, :, :, t0:t0 + 1].transpose(1, 2)
+                vd = cache[layer, 1, :, :, t0:t0 + 1].transpose(1, 2)
+                ops.rope_qknorm_append(q, k, v, fc, q_rot, kd, vd, True)
+                keys = cache[layer, 0, :, :, :t0 + 1].transpose(1, 2)
+                vals = cache[layer, 1, :, :, :t0 + 1].transpose(1, 2)
+                if record:
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    _native.attention_(q_rot, keys, vals, y, 0.25)
+                    b.record()
+                    ev.append((a, b))
+                else:
+                    _native.attention_(q_rot, keys, vals, y, 0.25)
+
+    for _ in range(warmup):
+        run_job(False)
+    torch.cuda.synchronize()
+    log(f"decode {dtype_name}: warmup done, timing {steps} jobs")
+    t_start = time.perf_counter()
+    for _ in range(steps):
+        run_job(True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t_start
+
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    launches = len(kern_ms)
+    mean_kernel_s = sum(kern_ms) / launches / 1e3
+    # algorithmic bytes per launch, averaged over the job's L_kv = 97..144
+    bytes_job = sum(B * H * es * (2 * (PREFIX + s + 1) * D + 2 * D) for s in range(NEW)) * L
+    bytes_per_launch = bytes_job / (NEW * L)
+    achieved = bytes_per_launch / mean_kernel_s / 1e9
+    tokens = B * NEW * steps
+    return {
+        "tokens_per_s": tokens / elapsed,
+        "ms_per_step": elapsed / steps * 1e3,
+        "kernel_mean_us": mean_kernel_s * 1e6,
+        "bytes_per_launch": bytes_per_launch,
+        "achieved_gbs": achieved,
+        "launches": launches,
+        "attn_only_tokens_per_s": B * NEW / (sum(kern_ms) / steps / 1e3),
+    }
+
+
+def prefill_leg(reps: int = 5):
+    """B=256, T=1024, H=8, D=64 bf16, q/k/v in (B,T,H,D) projection
+    layout, RoPE base 1e4 + QK-norm fused in the first launch, causal attention
+    in the second."""
+    import torch
+
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    dev = torch.device("cuda:0")
+    B, T, H, D = 256, 1024, 8, 64
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn((B, T, H, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    fc = precompute_freqs_cis(D, 2 * T, 10000).to(dev).to(torch.bfloat16)[:T].view(1, T, 1, D // 2, 2)
+    q_rot, k_rot, y = (torch.empty_like(q) for _ in range(3))
+    ops = _native.ops()
+    flop = 2.0 * B * H * D * T * (T + 1)
+
+    def once(evs=None):
+        ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
+        if evs is not None:
+            evs[0].record()
+        _native.attention_(q_rot, k_rot, v, y, 1.0 / D**0.5)
+        if evs is not None:
+            evs[1].record()
+
+    once()
+    torch.cuda.synchronize()
+    times, attn = [], []
+    for _ in range(reps):
+        evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        t0 = time.perf_counter()
+        once(evs)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+        attn.append(evs[0].elapsed_time(evs[1]) / 1e3)
+    t_attn = sorted(attn)[len(attn) // 2]
+    t_all = sorted(times)[len(times) // 2]
+    tf = flop / t_attn / 1e12
+    return {
+        "workload": "configs[2] causal prefill B=256 H=8 T=1024 D=64 bf16, RoPE+QK-norm",
+        "tflops": tf,
+        "attn_ms": t_attn * 1e3,
+        "with_rope_ms": t_all * 1e3,
+        "tflops_with_rope": flop / t_all / 1e12,
+        "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS, "traffic": None},
+    }
+
+
+def cpu_baseline(dtype_name: str, budget_s: float = 12.0):
+    """The oracle's torch-CPU restatement of the reference decode path
+    (rope.py, rms_norm.py, kv_cache.py insert, mha.py:68 SDPA) on the same
+    configs[1] shapes, for as many of the 48 decode steps as fit the budget."""
+    import torch
+
+    from oracle import torch_ref as tr
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
+    B, H, D, L = SERIES * TRAJ, HEADS, HEAD_DIM, LAYERS
+    g = torch.Generator().manual_seed(0)
+    cache = tr.RefCache(B, H, PREFIX + NEW, D, L)
+    cache.data = torch.randn((L, 2, B, H, PREFIX + NEW, D), generator=g).to(dt)
+    cache.pos = PREFIX
+    table = tr.freqs_table(D, 2 * 138, 10000).to(dt)
+    done, t0 = 0, time.perf_counter()
+    with torch.no_grad():
+        for s in range(NEW):
+            fc = table[PREFIX + s:PREFIX + s + 1].view(1, 1, 1, -1, 2)
+            for layer in range(L):
+                q, k, v = (torch.randn((B, 1, H, D), generator=g).to(dt) for _ in range(3))
+                q, k = tr.rms(tr.rope(q, fc)), tr.rms(tr.rope(k, fc))
+                kk, vv = cache.insert(layer, k.transpose(1, 2), v.transpose(1, 2))
+                tr.sdpa(q.transpose(1, 2), kk, vv).transpose(1, 2).contiguous()
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    el = time.perf_counter() - t0
+    return {
+        "value": B * done / el,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"configs[1] {dtype_name}: decode steps 1..{done} of 48 (both layers, 6400 seqs), "
+                  "torch CPU restatement (oracle.torch_ref)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--dtype", default="fp32", choices=["fp32", "bf16"])
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--traffic-json", default=str(REPO / "profiles" / "decode_attn_cfg1_traffic.json"))
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (no multi-GPU path); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    res = decode_job(args.dtype, args.steps, args.warmup)
+    log(f"decode: {res}")
+    other = "bf16" if args.dtype == "fp32" else "fp32"
+    res_other = decode_job(other, max(1, args.steps // 2), 1)
+    log(f"decode {other}: {res_other}")
+    traffic = None
+    tp = Path(args.traffic_json)
+    if tp.exists():
+        tj = json.loads(tp.read_text())
+        traffic = tj.get(args.dtype)
+    roof = {
+        "bound": "hbm",
+        "achieved": res["achieved_gbs"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": res["achieved_gbs"] / HBM_PEAK_GBS,
+        "traffic": traffic,
+    }
+    prefill = None if args.no_prefill else prefill_leg()
+    if prefill:
+        log(f"prefill: {prefill}")
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args.dtype)
+    out = {
+        "metric": METRIC,
+        "value": res["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if args.dtype == "fp32" else "bf16",
+        "data": "synthetic (seeded randn q/k/v and KV prefix, resident in HBM)",
+        "config": {
+            "workload": "configs[1]: 6400 seqs (64 series x 100 trajectories), 96-token prefix, "
+                        "48 decode steps, 2 layers, H=4, D=16; step = whole 48-token decode job "
+                        "(fused RoPE+QK-norm+append + decode attention per layer-step)",
+            "sequences": SERIES * TRAJ,
+            "decode_steps": NEW,
+            "kv_len": [PREFIX + 1, PREFIX + NEW],
+        },
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "decode_kernel": {"mean_us": res["kernel_mean_us"], "bytes_per_launch": res["bytes_per_launch"],
+                          "attn_only_tokens_per_s": res["attn_only_tokens_per_s"]},
+        "decode_other_dtype": {"dtype": other, "tokens_per_s": res_other["tokens_per_s"],
+                               "achieved_gbs": res_other["achieved_gbs"],
+                               "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
+        "prefill": prefill,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,79 @@
+"""Build libdgattn.so for gfx950 with hipcc (in-tree, no torch involvement).
+
+    python diff-gpt_amd/csrc/build.py            # incremental
+    python diff-gpt_amd/csrc/build.py --force    # rebuild every object
+
+Objects go to diff-gpt_amd/csrc/_build/, the library to diff-gpt_amd/lib/.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG = HERE.parent
+REPO = PKG.parent
+BUILD = HERE / "_build"
+LIB = PKG / "lib" / "libdgattn.so"
+SOURCES = ["dg_abi.hip", "dg_rope.hip", "dg_attn_vec.hip", "dg_attn_mfma.hip"]
+HEADERS = ["dg_common.h", str(REPO / "include" / "dgattn.h")]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+CFLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # packed fp32 ops are kept out of every kernel of this library
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def _newest(paths) -> float:
+    return max(Path(p).stat().st_mtime for p in paths)
+
+
+def _compile(src: str, force: bool) -> Path:
+    s = HERE / src
+    o = BUILD / (Path(src).stem + ".o")
+    deps = [s] + [HERE / h if not os.path.isabs(h) else Path(h) for h in HEADERS]
+    if not force and o.exists() and o.stat().st_mtime >= _newest(deps):
+        return o
+    cmd = [HIPCC, *CFLAGS, "-c", str(s), "-o", str(o)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise SystemExit(f"hipcc failed on {src}")
+    return o
+
+
+def build(force: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    LIB.parent.mkdir(exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+        objs = list(ex.map(lambda s: _compile(s, force), SOURCES))
+    if force or not LIB.exists() or LIB.stat().st_mtime < _newest(objs):
+        tmp = LIB.with_suffix(".so.tmp")
+        cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            sys.stderr.write(r.stdout + r.stderr)
+            raise SystemExit("link failed")
+        os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--force", action="store_true")
+    args = ap.parse_args()
+    print(build(force=args.force))

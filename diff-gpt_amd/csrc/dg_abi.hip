@@ -1,0 +1,130 @@
+// C entry points that are not a single kernel family: version, error slot,
+// attention dispatch (MFMA prefill vs. vector kernel) and the strided copy.
+#include "dg_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace dg {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return DG_ELAUNCH;
+  }
+  return DG_OK;
+}
+
+// dg_attn_vec.hip
+int vec_attention_splits(int B, int H, int Tq, int Tk, int D);
+size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D);
+int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                  const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
+                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
+                  void* workspace, size_t workspace_bytes, hipStream_t s);
+// dg_attn_mfma.hip
+bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                             const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
+                             const void* v, const dg_stride3* v_st, const void* y,
+                             const dg_stride3* y_st);
+int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                 const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
+                 const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
+                 hipStream_t s);
+
+// ---------------------------------------------------------------------------
+// Strided 4-D copy (exact), element size 2 or 4 bytes.
+// ---------------------------------------------------------------------------
+struct CopyArgs {
+  const void* src;
+  void* dst;
+  int64_t n0, n1, n2, n3;
+  int64_t s0, s1, s2, s3;
+  int64_t d0, d1, d2, d3;
+  int64_t total;
+};
+
+template <typename E>
+__global__ __launch_bounds__(256) void copy4d_kernel(const CopyArgs a) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < a.total; idx += stride) {
+    int64_t r = idx;
+    const int64_t i3 = r % a.n3;
+    r /= a.n3;
+    const int64_t i2 = r % a.n2;
+    r /= a.n2;
+    const int64_t i1 = r % a.n1;
+    const int64_t i0 = r / a.n1;
+    const E* s = static_cast<const E*>(a.src) + i0 * a.s0 + i1 * a.s1 + i2 * a.s2 + i3 * a.s3;
+    E* d = static_cast<E*>(a.dst) + i0 * a.d0 + i1 * a.d1 + i2 * a.d2 + i3 * a.d3;
+    *d = *s;
+  }
+}
+
+}  // namespace dg
+
+using namespace dg;
+
+extern "C" int dg_abi_version(void) { return DG_ABI_VERSION; }
+
+extern "C" const char* dg_last_error(void) { return g_err; }
+
+extern "C" size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int D, int dtype) {
+  (void)dtype;
+  if (B <= 0 || H <= 0 || Tq <= 0 || Tk <= 0 || D <= 0) return 0;
+  return vec_attention_workspace(B, H, Tq, Tk, D);
+}
+
+extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                            const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
+                            const void* v, const dg_stride3* v_st, void* y,
+                            const dg_stride3* y_st, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  DG_REQUIRE(B >= 0 && H >= 0 && Tq >= 0 && Tk >= 0, DG_EINVAL, "attention: negative size");
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "attention: dtype %d unsupported", dtype);
+  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention: head_dim must be even (got %d)", D);
+  if ((int64_t)B * H * Tq == 0) return DG_OK;
+  DG_REQUIRE(Tk >= Tq, DG_EINVAL, "attention: Tk (%d) < Tq (%d)", Tk, Tq);
+  DG_REQUIRE(q && k && v && y && q_st && k_st && v_st && y_st, DG_EINVAL, "attention: NULL argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st))
+    return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
+  return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, workspace,
+                       workspace_bytes, s);
+}
+
+extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const int64_t* src_st,
+                         void* dst, const int64_t* dst_st, void* stream) {
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "copy4d: dtype %d unsupported", dtype);
+  DG_REQUIRE(shape && src_st && dst_st, DG_EINVAL, "copy4d: NULL shape/strides");
+  for (int i = 0; i < 4; ++i) DG_REQUIRE(shape[i] >= 0, DG_EINVAL, "copy4d: negative extent");
+  CopyArgs a{};
+  a.total = shape[0] * shape[1] * shape[2] * shape[3];
+  if (a.total == 0) return DG_OK;
+  DG_REQUIRE(src && dst, DG_EINVAL, "copy4d: NULL pointer");
+  a.src = src;
+  a.dst = dst;
+  a.n0 = shape[0]; a.n1 = shape[1]; a.n2 = shape[2]; a.n3 = shape[3];
+  a.s0 = src_st[0]; a.s1 = src_st[1]; a.s2 = src_st[2]; a.s3 = src_st[3];
+  a.d0 = dst_st[0]; a.d1 = dst_st[1]; a.d2 = dst_st[2]; a.d3 = dst_st[3];
+  int64_t blocks = (a.total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == DG_F32)
+    hipLaunchKernelGGL(copy4d_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(copy4d_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return check_launch("copy4d_kernel");
+}

@@ -1,0 +1,173 @@
+// Shared device helpers of libdgattn: element conversion, 64-lane butterfly
+// reductions and the error slot used by every C entry point.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dgattn.h"
+
+namespace dg {
+
+// ---------------------------------------------------------------------------
+// Element types.  bf16 is held as its 16-bit pattern so loads/stores are plain
+// integer moves; conversion to fp32 is exact (append 16 zero bits) and the
+// conversion back rounds to nearest-even, matching torch's Tensor.to(bfloat16)
+// and the single rounding of type_as() in rope.py:27.
+// ---------------------------------------------------------------------------
+struct bf16_t {
+  uint16_t bits;
+};
+struct f16_t {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x.bits) << 16);
+}
+__device__ __forceinline__ float to_f32(f16_t x) {
+  _Float16 h = __builtin_bit_cast(_Float16, x.bits);
+  return static_cast<float>(h);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) {
+  return x;
+}
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
+  uint32_t u = __float_as_uint(x);
+  bf16_t r;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep sign, force a quiet NaN
+    r.bits = static_cast<uint16_t>((u >> 16) | 0x0040u);
+    return r;
+  }
+  // round to nearest, ties to even, on the 16 discarded bits
+  u += 0x7fffu + ((u >> 16) & 1u);
+  r.bits = static_cast<uint16_t>(u >> 16);
+  return r;
+}
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float x) {
+  _Float16 h = static_cast<_Float16>(x);  // v_cvt_f16_f32: round to nearest even
+  f16_t r;
+  r.bits = __builtin_bit_cast(uint16_t, h);
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Vector loads of EPL consecutive elements (EPL*sizeof(T) bytes, naturally
+// aligned by the host-side checks) converted to fp32.
+// ---------------------------------------------------------------------------
+template <int BYTES>
+struct raw_vec;
+template <>
+struct raw_vec<4> {
+  using type = uint32_t;
+};
+template <>
+struct raw_vec<8> {
+  using type = uint2;
+};
+template <>
+struct raw_vec<16> {
+  using type = uint4;
+};
+
+template <typename T, int EPL>
+__device__ __forceinline__ void load_vec(const T* __restrict__ p, float (&out)[EPL]) {
+  constexpr int BYTES = EPL * (int)sizeof(T);
+  T e[EPL];
+  if constexpr (BYTES > 16) {
+    static_assert(BYTES % 16 == 0, "vector width");
+#pragma unroll
+    for (int c = 0; c < BYTES / 16; ++c) {
+      uint4 r = reinterpret_cast<const uint4*>(p)[c];
+      __builtin_memcpy(reinterpret_cast<char*>(e) + 16 * c, &r, 16);
+    }
+  } else {
+    static_assert(BYTES == 4 || BYTES == 8 || BYTES == 16, "vector width");
+    using R = typename raw_vec<BYTES>::type;
+    R r = *reinterpret_cast<const R*>(p);
+    __builtin_memcpy(e, &r, BYTES);
+  }
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) out[i] = to_f32(e[i]);
+}
+
+template <typename T, int EPL>
+__device__ __forceinline__ void store_vec(T* __restrict__ p, const float (&in)[EPL]) {
+  constexpr int BYTES = EPL * (int)sizeof(T);
+  T e[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) e[i] = from_f32<T>(in[i]);
+  if constexpr (BYTES > 16) {
+    static_assert(BYTES % 16 == 0, "vector width");
+#pragma unroll
+    for (int c = 0; c < BYTES / 16; ++c) {
+      uint4 r;
+      __builtin_memcpy(&r, reinterpret_cast<const char*>(e) + 16 * c, 16);
+      reinterpret_cast<uint4*>(p)[c] = r;
+    }
+  } else {
+    static_assert(BYTES == 4 || BYTES == 8 || BYTES == 16, "vector width");
+    using R = typename raw_vec<BYTES>::type;
+    R r;
+    __builtin_memcpy(&r, e, BYTES);
+    *reinterpret_cast<R*>(p) = r;
+  }
+}
+
+// Pairwise-tree sum of N (power of two) values held by one lane: adjacent
+// pairs first, then pairs of pairs.  Together with group_sum over the lanes
+// of a row this is the canonical reduction order of the row norms.
+template <int N>
+__device__ __forceinline__ float tree_sum(float (&v)[N]) {
+#pragma unroll
+  for (int w = 1; w < N; w <<= 1) {
+#pragma unroll
+    for (int i = 0; i < N; i += 2 * w) v[i] = v[i] + v[i + w];
+  }
+  return v[0];
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane exchange inside a 64-wide wavefront.  ds_swizzle / DPP are picked
+// by the compiler for __shfl_xor with constant offsets.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor(float v, int off) { return __shfl_xor(v, off, 64); }
+
+// Butterfly sum over groups of G consecutive lanes (G a power of two).  Every
+// lane of a group ends with the same value: IEEE addition is commutative, so
+// partners compute bit-identical sums.  The pairing order (xor 1, 2, 4, ...)
+// is the tail of a pairwise tree over the lanes' partial sums.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = 1; off < G; off <<= 1) v = v + shfl_xor(v, off);
+  return v;
+}
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+}  // namespace dg
+
+// ---------------------------------------------------------------------------
+// Host side: thread-local error slot and launch checking.
+// ---------------------------------------------------------------------------
+namespace dg {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace dg
+
+#define DG_REQUIRE(cond, code, ...) \
+  do {                              \
+    if (!(cond)) {                  \
+      ::dg::set_error(__VA_ARGS__); \
+      return (code);                \
+    }                               \
+  } while (0)

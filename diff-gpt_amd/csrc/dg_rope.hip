@@ -1,0 +1,374 @@
+// Fused RoPE + QK-norm + KV append, and the standalone row RMSNorm.
+//
+// Reference semantics (fxeqxmulfx/diff-gpt):
+//   rope.py:20-27   x.float() split into interleaved pairs (x[2j], x[2j+1]);
+//                   out = (re*cos - im*sin, re*sin + im*cos) in fp32, then one
+//                   rounding back to x's dtype (type_as).
+//   rms_norm.py:7   F.rms_norm(x, (D,)) with eps=None: x * rsqrt(mean(x^2) + eps)
+//                   in fp32 with eps = FLT_EPSILON, one rounding to x's dtype.
+//   mha.py:44-56    q,k -> rope -> QK-norm -> transpose -> KVCache.insert_kv.
+//
+// Arithmetic contract (what makes the cache contents reproducible bit for bit):
+//   * RoPE: two separately rounded products and one rounded add/sub, never an
+//     FMA (contraction is switched off below), cos/sin read from the caller's
+//     table -- never recomputed on the device.
+//   * Norm: squares rounded, summed by a pairwise tree over the row padded with
+//     zeros to a power of two (adjacent pairs, then pairs of pairs ...),
+//     mean = sum / D, r = 1 / sqrt(mean + FLT_EPSILON) with correctly rounded
+//     sqrt and divide, y = x * r.
+//   * The V half of the append is an exact copy.
+#include "dg_common.h"
+
+#include <float.h>
+
+namespace dg {
+
+struct RopeArgs {
+  const void* src[3];
+  void* dst[3];
+  int64_t sb[3], st[3], sh[3];  // source strides (b, t, h)
+  int64_t db[3], dt[3], dh[3];  // destination strides (b, t, h)
+  const void* freqs;
+  int64_t fb, ft, fh;
+  int64_t rows;  // B*T*H
+  int T, H, D;
+  int qknorm;
+};
+
+// One row (b,t,h) of D elements is owned by LPK = DPAD/EPL consecutive lanes,
+// each holding EPL consecutive elements (EPL even, so a (re, im) pair never
+// straddles lanes).  Lanes whose slice starts at or beyond D (only when D is
+// not a power of two) hold zeros and store nothing.
+template <typename T, typename FT, int DPAD, int EPL>
+__global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int LPK = DPAD / EPL;
+  static_assert(LPK >= 1 && LPK <= 64 && (EPL % 2) == 0, "row mapping");
+  constexpr int ROWS_PER_BLOCK = 256 / LPK;
+
+  const int sub = threadIdx.x % LPK;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / LPK;
+  if (row >= a.rows) return;  // a whole lane group leaves together; no barriers follow
+
+  const int h = (int)(row % a.H);
+  const int64_t bt = row / a.H;
+  const int t = (int)(bt % a.T);
+  const int64_t b = bt / a.T;
+  const int d0 = sub * EPL;
+  const bool active = d0 < a.D;
+
+  float cs[EPL];  // (cos, sin) of the EPL/2 pairs of this lane, interleaved
+  if (active) {
+    const FT* f = static_cast<const FT*>(a.freqs) + b * a.fb + (int64_t)t * a.ft +
+                  (int64_t)h * a.fh + d0;
+    load_vec<FT, EPL>(f, cs);
+  }
+
+#pragma unroll
+  for (int w = 0; w < 3; ++w) {
+    if (a.src[w] == nullptr) continue;  // uniform over the grid
+    float x[EPL];
+    if (active) {
+      const T* s = static_cast<const T*>(a.src[w]) + b * a.sb[w] + (int64_t)t * a.st[w] +
+                   (int64_t)h * a.sh[w] + d0;
+      load_vec<T, EPL>(s, x);
+    } else {
+#pragma unroll
+      for (int i = 0; i < EPL; ++i) x[i] = 0.f;
+    }
+    if (w < 2) {
+#pragma unroll
+      for (int p = 0; p < EPL / 2; ++p) {
+        const float re = x[2 * p], im = x[2 * p + 1];
+        const float c = cs[2 * p], sn = cs[2 * p + 1];
+        const float a0 = re * c, a1 = im * sn;
+        const float b0 = re * sn, b1 = im * c;
+        // rounding to the storage dtype happens here (type_as), before the norm
+        x[2 * p] = to_f32(from_f32<T>(a0 - a1));
+        x[2 * p + 1] = to_f32(from_f32<T>(b0 + b1));
+      }
+      if (a.qknorm) {
+        float sq[EPL];
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) sq[i] = x[i] * x[i];
+        float ss = tree_sum<EPL>(sq);
+        ss = group_sum<LPK>(ss);
+        const float mean = ss / (float)a.D;
+        const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) x[i] = x[i] * r;
+      }
+    }
+    if (active) {
+      T* d = static_cast<T*>(a.dst[w]) + b * a.db[w] + (int64_t)t * a.dt[w] +
+             (int64_t)h * a.dh[w] + d0;
+      store_vec<T, EPL>(d, x);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Row RMSNorm over N elements (rms_norm.py:5-7).  G = NPAD/CH lanes per row,
+// each lane owns CH consecutive elements; same canonical tree as above.
+// ---------------------------------------------------------------------------
+struct RowNormArgs {
+  const void* x;
+  void* out;
+  int64_t x_ld, out_ld, M;
+  int N;
+  int vec;  // 1 when every lane slice is aligned for CH-element vector access
+};
+
+template <typename T, int NPAD, int CH>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const RowNormArgs a) {
+#pragma clang fp contract(off)
+  constexpr int G = NPAD / CH;
+  static_assert(G >= 1 && G <= 64, "row mapping");
+  constexpr int ROWS_PER_BLOCK = 256 / G;
+  const int sub = threadIdx.x % G;
+  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / G;
+  if (row >= a.M) return;
+  const int c0 = sub * CH;
+  const T* xs = static_cast<const T*>(a.x) + row * a.x_ld + c0;
+  float x[CH];
+  if (a.vec && c0 + CH <= a.N) {
+    load_vec<T, CH>(xs, x);
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) x[i] = (c0 + i < a.N) ? to_f32(xs[i]) : 0.f;
+  }
+  float sq[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) sq[i] = x[i] * x[i];
+  float ss = tree_sum<CH>(sq);
+  ss = group_sum<G>(ss);
+  const float mean = ss / (float)a.N;
+  const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) x[i] = x[i] * r;
+  T* os = static_cast<T*>(a.out) + row * a.out_ld + c0;
+  if (a.vec && c0 + CH <= a.N) {
+    store_vec<T, CH>(os, x);
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (c0 + i < a.N) os[i] = from_f32<T>(x[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch
+// ---------------------------------------------------------------------------
+namespace {
+
+int elem_size(int dtype) { return dtype == DG_F32 ? 4 : 2; }
+
+bool aligned(const void* p, int64_t bytes) {
+  return p == nullptr || (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
+}
+bool strides_multiple(const dg_stride3* s, int64_t m) {
+  return s == nullptr || (s->b % m == 0 && s->t % m == 0 && s->h % m == 0);
+}
+
+int next_pow2(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+template <typename T, typename FT, int DPAD, int EPL>
+int launch_rope(const RopeArgs& a, hipStream_t s) {
+  constexpr int LPK = DPAD / EPL;
+  constexpr int RPB = 256 / LPK;
+  const int64_t blocks = (a.rows + RPB - 1) / RPB;
+  DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "rope: too many rows (%lld)", (long long)a.rows);
+  hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL>), dim3((unsigned)blocks), dim3(256), 0,
+                     s, a);
+  return check_launch("rope_qknorm_kernel");
+}
+
+template <typename T, typename FT, int DPAD>
+int rope_pick_epl(int epl, const RopeArgs& a, hipStream_t s) {
+  constexpr int PREF = (16 / (int)sizeof(T)) < DPAD ? (16 / (int)sizeof(T)) : DPAD;
+  if constexpr (PREF != 2) {
+    if (epl == PREF) return launch_rope<T, FT, DPAD, PREF>(a, s);
+  }
+  if constexpr (DPAD / 2 <= 64) {
+    if (epl == 2) return launch_rope<T, FT, DPAD, 2>(a, s);
+  }
+  set_error("rope: no kernel for D pad %d with %d elements per lane", DPAD, epl);
+  return DG_EUNSUPPORTED;
+}
+
+template <typename T, typename FT>
+int rope_pick_d(int dpad, int epl, const RopeArgs& a, hipStream_t s) {
+  switch (dpad) {
+    case 2: return rope_pick_epl<T, FT, 2>(epl, a, s);
+    case 4: return rope_pick_epl<T, FT, 4>(epl, a, s);
+    case 8: return rope_pick_epl<T, FT, 8>(epl, a, s);
+    case 16: return rope_pick_epl<T, FT, 16>(epl, a, s);
+    case 32: return rope_pick_epl<T, FT, 32>(epl, a, s);
+    case 64: return rope_pick_epl<T, FT, 64>(epl, a, s);
+    case 128: return rope_pick_epl<T, FT, 128>(epl, a, s);
+    case 256: return rope_pick_epl<T, FT, 256>(epl, a, s);
+  }
+  set_error("rope: head_dim %d unsupported", a.D);
+  return DG_EUNSUPPORTED;
+}
+
+template <typename T, int NPAD>
+int launch_rms(const RowNormArgs& a, hipStream_t s) {
+  constexpr int PREF = 16 / (int)sizeof(T);
+  constexpr int CH0 = NPAD / 64 > PREF ? NPAD / 64 : PREF;
+  constexpr int CH = CH0 < NPAD ? CH0 : NPAD;
+  constexpr int G = NPAD / CH;
+  constexpr int RPB = 256 / G;
+  const int64_t blocks = (a.M + RPB - 1) / RPB;
+  DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "rms_norm: too many rows (%lld)", (long long)a.M);
+  RowNormArgs b = a;
+  const int64_t vb = (int64_t)CH * (int64_t)sizeof(T);
+  const bool pow2_vec = (vb == 4 || vb == 8 || vb % 16 == 0);
+  b.vec = pow2_vec && aligned(a.x, vb) && aligned(a.out, vb) &&
+          (a.x_ld * (int64_t)sizeof(T)) % vb == 0 && (a.out_ld * (int64_t)sizeof(T)) % vb == 0 &&
+          (CH * (int)sizeof(T)) >= 4;
+  hipLaunchKernelGGL((rms_norm_kernel<T, NPAD, CH>), dim3((unsigned)blocks), dim3(256), 0, s, b);
+  return check_launch("rms_norm_kernel");
+}
+
+template <typename T>
+int rms_pick(int npad, const RowNormArgs& a, hipStream_t s) {
+  switch (npad) {
+    case 1: return launch_rms<T, 2>(a, s);
+    case 2: return launch_rms<T, 2>(a, s);
+    case 4: return launch_rms<T, 4>(a, s);
+    case 8: return launch_rms<T, 8>(a, s);
+    case 16: return launch_rms<T, 16>(a, s);
+    case 32: return launch_rms<T, 32>(a, s);
+    case 64: return launch_rms<T, 64>(a, s);
+    case 128: return launch_rms<T, 128>(a, s);
+    case 256: return launch_rms<T, 256>(a, s);
+    case 512: return launch_rms<T, 512>(a, s);
+    case 1024: return launch_rms<T, 1024>(a, s);
+    case 2048: return launch_rms<T, 2048>(a, s);
+    case 4096: return launch_rms<T, 4096>(a, s);
+    case 8192: return launch_rms<T, 8192>(a, s);
+  }
+  set_error("rms_norm: N=%d unsupported (max 8192)", a.N);
+  return DG_EUNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace dg
+
+using namespace dg;
+
+extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, const void* q,
+                                     const dg_stride3* q_st, void* q_out, const dg_stride3* qo_st,
+                                     const void* k, const dg_stride3* k_st, void* k_out,
+                                     const dg_stride3* ko_st, const void* v,
+                                     const dg_stride3* v_st, void* v_out,
+                                     const dg_stride3* vo_st, const void* freqs,
+                                     const dg_stride3* f_st, int freqs_dtype, int flags,
+                                     void* stream) {
+  DG_REQUIRE(B >= 0 && T >= 0 && H >= 0, DG_EINVAL, "rope: negative size");
+  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "rope: head_dim must be even and >= 2 (got %d)", D);
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "rope: dtype %d unsupported", dtype);
+  DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == dtype, DG_EUNSUPPORTED,
+             "rope: freqs dtype must be fp32 or equal to the data dtype");
+  if ((int64_t)B * T * H == 0) return DG_OK;
+  const void* src[3] = {q, k, v};
+  void* dst[3] = {q_out, k_out, v_out};
+  const dg_stride3* sst[3] = {q_st, k_st, v_st};
+  const dg_stride3* dst_st[3] = {qo_st, ko_st, vo_st};
+  bool any = false;
+  for (int w = 0; w < 3; ++w) {
+    DG_REQUIRE((src[w] == nullptr) == (dst[w] == nullptr), DG_EINVAL,
+               "rope: input %d and its output must both be given or both be NULL", w);
+    if (src[w]) {
+      DG_REQUIRE(sst[w] && dst_st[w], DG_EINVAL, "rope: missing strides for tensor %d", w);
+      any = true;
+    }
+  }
+  if (!any) return DG_OK;
+  const bool need_freqs = (q != nullptr) || (k != nullptr);
+  DG_REQUIRE(!need_freqs || (freqs != nullptr && f_st != nullptr), DG_EINVAL,
+             "rope: freqs table required");
+
+  const int es = elem_size(dtype);
+  const int fes = elem_size(freqs_dtype);
+  const int dpad = next_pow2(D);
+  DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "rope: head_dim %d > 256", D);
+
+  // Preferred vector width: 16 bytes of data per lane when D is a power of two
+  // and every pointer / stride allows it; otherwise one (re, im) pair per lane.
+  int pref = 16 / es;
+  if (pref > dpad) pref = dpad;
+  auto fits = [&](int epl) {
+    if (epl != 2 && dpad != D) return false;
+    if (dpad / epl > 64) return false;
+    for (int w = 0; w < 3; ++w) {
+      if (!src[w]) continue;
+      if (!aligned(src[w], (int64_t)epl * es) || !aligned(dst[w], (int64_t)epl * es)) return false;
+      if (!strides_multiple(sst[w], epl) || !strides_multiple(dst_st[w], epl)) return false;
+    }
+    if (need_freqs) {
+      if (!aligned(freqs, (int64_t)epl * fes) || !strides_multiple(f_st, epl)) return false;
+    }
+    return true;
+  };
+  int epl = 0;
+  if (fits(pref)) epl = pref;
+  else if (fits(2)) epl = 2;
+  DG_REQUIRE(epl != 0, DG_EINVAL,
+             "rope: pointers/strides not aligned to an element pair (D=%d); pass contiguous rows", D);
+
+  RopeArgs a{};
+  for (int w = 0; w < 3; ++w) {
+    a.src[w] = src[w];
+    a.dst[w] = dst[w];
+    if (src[w]) {
+      a.sb[w] = sst[w]->b;  a.st[w] = sst[w]->t;  a.sh[w] = sst[w]->h;
+      a.db[w] = dst_st[w]->b; a.dt[w] = dst_st[w]->t; a.dh[w] = dst_st[w]->h;
+    }
+  }
+  a.freqs = freqs;
+  if (f_st) { a.fb = f_st->b; a.ft = f_st->t; a.fh = f_st->h; }
+  a.rows = (int64_t)B * T * H;
+  a.T = T;
+  a.H = H;
+  a.D = D;
+  a.qknorm = (flags & DG_QKNORM) ? 1 : 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+
+  if (dtype == DG_F32) return rope_pick_d<float, float>(dpad, epl, a, s);
+  if (dtype == DG_BF16) {
+    if (freqs_dtype == DG_F32) return rope_pick_d<bf16_t, float>(dpad, epl, a, s);
+    return rope_pick_d<bf16_t, bf16_t>(dpad, epl, a, s);
+  }
+  if (freqs_dtype == DG_F32) return rope_pick_d<f16_t, float>(dpad, epl, a, s);
+  return rope_pick_d<f16_t, f16_t>(dpad, epl, a, s);
+}
+
+extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
+                           int64_t out_ld, void* stream) {
+  DG_REQUIRE(M >= 0 && N >= 1, DG_EINVAL, "rms_norm: bad sizes M=%lld N=%d", (long long)M, N);
+  DG_REQUIRE(N <= 8192, DG_EUNSUPPORTED, "rms_norm: N=%d > 8192", N);
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "rms_norm: dtype %d unsupported", dtype);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(x != nullptr && out != nullptr, DG_EINVAL, "rms_norm: NULL pointer");
+  DG_REQUIRE(x_ld >= N && out_ld >= N, DG_EINVAL, "rms_norm: row stride smaller than N");
+  RowNormArgs a{};
+  a.x = x;
+  a.out = out;
+  a.x_ld = x_ld;
+  a.out_ld = out_ld;
+  a.M = M;
+  a.N = N;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int npad = next_pow2(N);
+  if (dtype == DG_F32) return rms_pick<float>(npad, a, s);
+  if (dtype == DG_BF16) return rms_pick<bf16_t>(npad, a, s);
+  return rms_pick<f16_t>(npad, a, s);
+}

@@ -1,0 +1,331 @@
+"""Binding of libdgattn.so (the gfx950 HIP library behind include/dgattn.h).
+
+The C entry points are reached through ctypes and exposed to PyTorch as custom
+operators in the ``dgattn`` namespace (``torch.ops.dgattn.*``), registered for
+the CUDA (= HIP on ROCm) dispatch key only.  There is deliberately no CPU
+kernel: a CPU tensor, a missing library or an autograd-tracked input raises
+instead of silently computing somewhere else.
+
+Each wrapper passes raw data pointers, element strides and the current HIP
+stream of the tensor's device; the library enqueues its kernels on that stream
+and returns immediately.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(
+    os.environ.get(
+        "DGATTN_LIB", Path(__file__).resolve().parent.parent / "lib" / "libdgattn.so"
+    )
+)
+
+DG_F32, DG_BF16, DG_F16 = 0, 1, 2
+DG_QKNORM = 1
+_DTYPE_CODE = {torch.float32: DG_F32, torch.bfloat16: DG_BF16, torch.float16: DG_F16}
+
+
+class Stride3(ctypes.Structure):
+    """``dg_stride3``: element strides of a (B,T,H,D) view."""
+
+    _fields_ = [("b", ctypes.c_int64), ("t", ctypes.c_int64), ("h", ctypes.c_int64)]
+
+
+_lib: ctypes.CDLL | None = None
+
+_SIGNATURES = {
+    "dg_abi_version": (ctypes.c_int, []),
+    "dg_last_error": (ctypes.c_char_p, []),
+    "dg_rope_qknorm_append": (
+        ctypes.c_int,
+        [ctypes.c_int] * 5
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 7  # q, q_out, k, k_out, v, v_out, freqs
+        + [ctypes.c_int, ctypes.c_int, ctypes.c_void_p],
+    ),
+    "dg_attention_workspace_size": (ctypes.c_size_t, [ctypes.c_int] * 6),
+    "dg_attention": (
+        ctypes.c_int,
+        [ctypes.c_int] * 6
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4
+        + [ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+    ),
+    "dg_rms_norm": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
+    "dg_copy4d": (
+        ctypes.c_int,
+        [ctypes.c_int, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
+         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
+         ctypes.c_void_p],
+    ),
+}
+
+ABI_VERSION = 1
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdgattn.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"libdgattn.so not found at {LIB_PATH}; build it with "
+                "`python diff-gpt_amd/csrc/build.py` (or __graft_entry__.build())"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        got = handle.dg_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"libdgattn ABI {got} != expected {ABI_VERSION}")
+        _lib = handle
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().dg_last_error().decode(errors="replace")
+        raise RuntimeError(f"dgattn.{what} failed (status {rc}): {msg}")
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise TypeError(
+            f"dgattn supports float32/bfloat16/float16 tensors, got {t.dtype}"
+        ) from None
+
+
+def require_device(what: str, *tensors: torch.Tensor | None) -> None:
+    """The HIP path has no CPU implementation: insist on ROCm device tensors."""
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"{what}: the MI355X attention path runs on ROCm devices only; got a "
+                f"tensor on '{t.device}'. Move the model/cache with .to('cuda')."
+            )
+
+
+def require_device_type(what: str, device) -> None:
+    if torch.device(device).type != "cuda":
+        raise RuntimeError(
+            f"{what}: the MI355X attention path runs on ROCm devices only; got '{device}'"
+        )
+
+
+def require_inference(what: str, *tensors: torch.Tensor | None) -> None:
+    if not torch.is_grad_enabled():
+        return
+    for t in tensors:
+        if t is not None and t.requires_grad:
+            raise RuntimeError(
+                f"{what}: the HIP kernels are inference-only (no backward); call under "
+                "torch.no_grad() / torch.inference_mode()"
+            )
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _bthd_strides(t: torch.Tensor) -> Stride3:
+    """Strides of a 4-D (B,T,H,D) view with a unit D stride."""
+    if t.dim() != 4:
+        raise ValueError(f"expected a 4-D (B,T,H,D) tensor, got shape {tuple(t.shape)}")
+    if t.stride(3) != 1 and t.size(3) > 1:
+        raise ValueError("the last (head_dim) dimension must be contiguous")
+    return Stride3(t.stride(0), t.stride(1), t.stride(2))
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+# ---------------------------------------------------------------------------
+# Raw launchers (operate in place on caller-provided outputs)
+# ---------------------------------------------------------------------------
+
+
+def rope_qknorm_append_(
+    q: torch.Tensor | None,
+    k: torch.Tensor | None,
+    v: torch.Tensor | None,
+    freqs: torch.Tensor,
+    q_out: torch.Tensor | None,
+    k_out: torch.Tensor | None,
+    v_out: torch.Tensor | None,
+    qknorm: bool,
+) -> None:
+    """dg_rope_qknorm_append on (B,T,H,D) views; freqs is (B|1,T,H|1,D/2,2)."""
+    ref = next(t for t in (q, k, v) if t is not None)
+    B, T, H, D = ref.shape
+    for a, b in ((q, q_out), (k, k_out), (v, v_out)):
+        if (a is None) != (b is None):
+            raise ValueError("each input needs an output (and vice versa)")
+        if a is not None:
+            if a.shape != (B, T, H, D) or b.shape != (B, T, H, D):
+                raise ValueError(f"shape mismatch: {tuple(a.shape)} -> {tuple(b.shape)}")
+            if a.dtype != ref.dtype or b.dtype != ref.dtype:
+                raise TypeError("q/k/v and outputs must share one dtype")
+    need_f = q is not None or k is not None
+    if need_f:
+        if freqs.dim() != 5 or freqs.shape[-2:] != (D // 2, 2):
+            raise ValueError(f"freqs must be (B,T,H,D/2,2)-broadcastable, got {tuple(freqs.shape)}")
+        if freqs.stride(-1) != 1 or freqs.stride(-2) != 2:
+            freqs = freqs.contiguous()
+        if freqs.size(1) not in (1, T) or freqs.size(0) not in (1, B) or freqs.size(2) not in (1, H):
+            raise ValueError("freqs does not broadcast against (B,T,H)")
+        fb = 0 if freqs.size(0) == 1 else freqs.stride(0)
+        ft = 0 if freqs.size(1) == 1 else freqs.stride(1)
+        fh = 0 if freqs.size(2) == 1 else freqs.stride(2)
+        f_st = Stride3(fb, ft, fh)
+        f_code = _dtype_code(freqs)
+    else:
+        f_st = Stride3(0, 0, 0)
+        f_code = _dtype_code(ref)
+
+    def st(t):
+        return None if t is None else ctypes.pointer(_bthd_strides(t))
+
+    rc = lib().dg_rope_qknorm_append(
+        B, T, H, D, _dtype_code(ref),
+        _ptr(q), st(q), _ptr(q_out), st(q_out),
+        _ptr(k), st(k), _ptr(k_out), st(k_out),
+        _ptr(v), st(v), _ptr(v_out), st(v_out),
+        _ptr(freqs if need_f else None), ctypes.pointer(f_st), f_code,
+        DG_QKNORM if qknorm else 0, _stream(ref),
+    )
+    _check(rc, "rope_qknorm_append")
+
+
+def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
+               scale: float) -> None:
+    """dg_attention: q,y (B,Tq,H,D) views; k,v (B,Tk,H,D) views."""
+    B, Tq, H, D = q.shape
+    Tk = k.size(1)
+    if k.shape != (B, Tk, H, D) or v.shape != (B, Tk, H, D) or y.shape != q.shape:
+        raise ValueError("attention: inconsistent q/k/v/y shapes")
+    if not (q.dtype == k.dtype == v.dtype == y.dtype):
+        raise TypeError("attention: q/k/v/y must share one dtype")
+    code = _dtype_code(q)
+    L = lib()
+    ws_bytes = L.dg_attention_workspace_size(B, H, Tq, Tk, D, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    rc = L.dg_attention(
+        B, H, Tq, Tk, D, code,
+        _ptr(q), ctypes.pointer(_bthd_strides(q)),
+        _ptr(k), ctypes.pointer(_bthd_strides(k)),
+        _ptr(v), ctypes.pointer(_bthd_strides(v)),
+        _ptr(y), ctypes.pointer(_bthd_strides(y)),
+        float(scale), _ptr(ws), ws_bytes, _stream(q),
+    )
+    _check(rc, "attention")
+
+
+def rms_norm_(x: torch.Tensor, out: torch.Tensor) -> None:
+    N = x.size(-1)
+    x2 = x.reshape(-1, N) if x.dim() != 2 else x
+    o2 = out.view(-1, N)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    rc = lib().dg_rms_norm(
+        x2.size(0), N, _dtype_code(x2), _ptr(x2), x2.stride(0), _ptr(o2), o2.stride(0), _stream(x2)
+    )
+    _check(rc, "rms_norm")
+
+
+def copy4d_(src: torch.Tensor, dst: torch.Tensor) -> None:
+    """dst[...] = src[...] over 4-D views (src may broadcast with 0 strides)."""
+    if src.dim() != 4 or dst.dim() != 4:
+        raise ValueError("copy4d expects 4-D views")
+    if src.dtype != dst.dtype:
+        raise TypeError("copy4d: dtype mismatch")
+    shape = (ctypes.c_int64 * 4)(*dst.shape)
+    s_st = (ctypes.c_int64 * 4)(*[0 if src.size(i) == 1 and dst.size(i) != 1 else src.stride(i)
+                                  for i in range(4)])
+    d_st = (ctypes.c_int64 * 4)(*dst.stride())
+    for i in range(4):
+        if src.size(i) not in (1, dst.size(i)):
+            raise ValueError(f"copy4d: {tuple(src.shape)} does not broadcast to {tuple(dst.shape)}")
+    rc = lib().dg_copy4d(_dtype_code(dst), shape, _ptr(src), s_st, _ptr(dst), d_st, _stream(dst))
+    _check(rc, "copy4d")
+
+
+# ---------------------------------------------------------------------------
+# torch.ops.dgattn registration (CUDA/HIP kernels + Meta shape functions)
+# ---------------------------------------------------------------------------
+
+_DEF = torch.library.Library("dgattn", "DEF")
+_DEF.define(
+    "rope_qknorm_append(Tensor? q, Tensor? k, Tensor? v, Tensor freqs, Tensor(a!)? q_out, "
+    "Tensor(b!)? k_out, Tensor(c!)? v_out, bool qknorm) -> ()"
+)
+_DEF.define("attention(Tensor q, Tensor k, Tensor v, float scale) -> Tensor")
+_DEF.define("rms_norm(Tensor x) -> Tensor")
+_DEF.define("rope(Tensor x, Tensor freqs) -> Tensor")
+_DEF.define("copy4d(Tensor src, Tensor(a!) dst) -> ()")
+
+_IMPL = torch.library.Library("dgattn", "IMPL")
+
+
+def _attention_impl(q, k, v, scale):
+    y = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    attention_(q, k, v, y, scale)
+    return y
+
+
+def _rms_norm_impl(x):
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    rms_norm_(x, out)
+    return out
+
+
+def _rope_impl(x, freqs):
+    # x (..., D) and freqs (..., D/2, 2) broadcast over the leading dims; the
+    # kernel sees both as (B,T,H,D) views.
+    D = x.size(-1)
+    lead = torch.broadcast_shapes(x.shape[:-1], freqs.shape[:-2])
+    if tuple(lead) != tuple(x.shape[:-1]):
+        raise ValueError("apply_rotary_emb: freqs broadcasts x to a larger shape")
+    n = len(lead)
+    fexp = freqs.expand(*lead, D // 2, 2)  # 0-stride view over broadcast dims
+    if n <= 3:
+        pad = (1,) * (3 - n)
+        x4 = x.reshape(*pad, *x.shape)
+        f5 = fexp.reshape(*pad, *fexp.shape)
+    else:
+        head = math.prod(lead[:-2])
+        x4 = x.reshape(head, *x.shape[-3:])
+        f5 = fexp.reshape(head, *lead[-2:], D // 2, 2)
+    out = torch.empty(x4.shape, dtype=x.dtype, device=x.device)
+    rope_qknorm_append_(x4, None, None, f5, out, None, None, qknorm=False)
+    return out.view(x.shape)
+
+
+_IMPL.impl("rope_qknorm_append", rope_qknorm_append_, "CUDA")
+_IMPL.impl("attention", _attention_impl, "CUDA")
+_IMPL.impl("rms_norm", _rms_norm_impl, "CUDA")
+_IMPL.impl("rope", _rope_impl, "CUDA")
+_IMPL.impl("copy4d", copy4d_, "CUDA")
+
+_IMPL.impl("attention", lambda q, k, v, scale: torch.empty_like(q), "Meta")
+_IMPL.impl("rms_norm", lambda x: torch.empty_like(x), "Meta")
+_IMPL.impl("rope", lambda x, freqs: torch.empty_like(x), "Meta")
+
+
+def ops():
+    """The registered operator namespace (torch.ops.dgattn)."""
+    return torch.ops.dgattn

@@ -1,0 +1,76 @@
+"""Transformer block with Block Attention Residuals (src/diff_gpt/model/block.py:10-107).
+
+Each sub-layer (attention, MLP) reads a per-token softmax mixture over the
+committed block states plus the running partial sum, weighted by a learned
+pseudo-query; a block boundary every ``layers_per_block`` layers commits the
+partial sum.  The mixture is small torch math; its RMSNorm is dg_rms_norm and
+the attention sub-layer is the HIP path of MultiHeadAttention.
+"""
+
+import torch
+from torch import nn
+
+from diff_gpt.model.feed_forward import FeedForward
+from diff_gpt.model.kv_cache import KVCache
+from diff_gpt.model.mha import MultiHeadAttention
+from diff_gpt.model.rms_norm import rms_norm
+
+
+def block_attn_res(
+    blocks: tuple[torch.Tensor, ...],
+    partial_block: torch.Tensor,
+    proj: nn.Linear,
+) -> torch.Tensor:
+    """softmax_n(rms_norm(V_n) . w) weighted sum of V_n over V = (*blocks, partial),
+    per token (block.py:10-44).  With a single committed block that *is* the
+    partial sum (layer 0) the mixture is that tensor itself."""
+    if len(blocks) == 1 and partial_block is blocks[0]:
+        return partial_block
+    V = torch.stack((*blocks, partial_block), dim=0)  # (N+1, B, T, C)
+    scores = rms_norm(V).matmul(proj.weight.view(-1))  # (N+1, B, T)
+    weights = scores.softmax(dim=0).unsqueeze(-1)
+    return (weights * V).sum(dim=0)
+
+
+class Block(nn.Module):
+    def __init__(
+        self,
+        n_embd: int,
+        n_head: int,
+        swiglu_alpha: float,
+        swiglu_limit: float,
+        layer_idx: int,
+        layers_per_block: int = 1,
+    ) -> None:
+        super().__init__()
+        assert layers_per_block >= 1
+        self.layer_idx = layer_idx
+        self.layers_per_block = layers_per_block
+        self.sa = MultiHeadAttention(n_embd=n_embd, n_head=n_head, layer_idx=layer_idx)
+        self.ffwd = FeedForward(
+            n_embd=n_embd, swiglu_alpha=swiglu_alpha, swiglu_limit=swiglu_limit
+        )
+        # one (1, C) pseudo-query per sub-layer
+        self.attn_res_proj = nn.Linear(n_embd, 1, bias=False)
+        self.mlp_res_proj = nn.Linear(n_embd, 1, bias=False)
+
+    def _at_boundary(self) -> bool:
+        return (self.layer_idx + 1) % self.layers_per_block == 0
+
+    def forward(
+        self,
+        blocks: tuple[torch.Tensor, ...],
+        partial_block: torch.Tensor,
+        freqs_cis: torch.Tensor,
+        kv_cache: KVCache | None,
+    ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
+        h = block_attn_res(blocks, partial_block, self.attn_res_proj)
+        committed = self._at_boundary()
+        if committed:
+            blocks = (*blocks, partial_block)
+        attn_out = self.sa(rms_norm(h), freqs_cis=freqs_cis, kv_cache=kv_cache)
+        partial_block = attn_out if committed else partial_block + attn_out
+
+        h = block_attn_res(blocks, partial_block, self.mlp_res_proj)
+        partial_block = partial_block + self.ffwd(rms_norm(h))
+        return blocks, partial_block

@@ -1,0 +1,210 @@
+"""GPT over the MI355X attention path (src/diff_gpt/model/gpt.py:15-242).
+
+Same constructor, parameter names (state_dicts load both ways), parameter
+creation order (so a seeded construction gives the same weights), forward
+signature and generation API as the reference.  Inference only: the HIP
+kernels have no backward, so a forward that would need autograd raises.
+"""
+
+from abc import ABC, abstractmethod
+
+import torch
+import torch.nn as nn
+from torch.nn import functional as F
+
+from diff_gpt.model.block import Block
+from diff_gpt.model.kv_cache import KVCache
+from diff_gpt.model.rms_norm import rms_norm
+from diff_gpt.model.rope import precompute_freqs_cis
+from diff_gpt.sampler.sampler import Sampler
+
+
+def _gaussian_soft_ce(
+    logits: torch.Tensor,
+    targets: torch.Tensor,
+    sigma: float,
+    ignore_index: int = -100,
+) -> torch.Tensor:
+    """Cross-entropy against a Gaussian over bin indices, N(target, sigma^2),
+    normalised over the vocabulary; ignore_index rows are skipped
+    (gpt.py:15-35)."""
+    keep = targets != ignore_index
+    if not keep.any():
+        return logits.sum() * 0.0
+    lg = logits[keep]
+    tg = targets[keep].to(lg.dtype)
+    bins = torch.arange(logits.shape[-1], device=logits.device, dtype=lg.dtype)
+    dist2 = (bins[None, :] - tg[:, None]).pow(2)
+    soft = F.softmax(-dist2 / (2.0 * sigma * sigma), dim=-1)
+    return -(soft * F.log_softmax(lg, dim=-1)).sum(dim=-1).mean()
+
+
+class BaseGPT(nn.Module, ABC):
+    def __init__(
+        self,
+        block_size: int,
+        vocab_size: int,
+        n_embd: int,
+        n_head: int,
+        n_layer: int,
+    ) -> None:
+        super().__init__()
+        self.block_size = block_size
+        self.vocab_size = vocab_size
+        self.n_embd = n_embd
+        self.n_head = n_head
+        self.n_layer = n_layer
+
+    @abstractmethod
+    def forward(
+        self,
+        idx: torch.Tensor,
+        targets: torch.Tensor | None = None,
+        kv_cache: KVCache | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        pass
+
+    @abstractmethod
+    def generate(
+        self,
+        idx: torch.Tensor,
+        max_new_tokens: int,
+        sampler: Sampler | None,
+        seed: int | None = None,
+    ) -> torch.Tensor:
+        pass
+
+    @property
+    @abstractmethod
+    def device_type(self) -> str:
+        pass
+
+
+class GPT(BaseGPT):
+    def __init__(
+        self,
+        vocab_size: int,
+        n_embd: int = 64,
+        block_size: int = 32,
+        n_head: int = 4,
+        n_layer: int = 4,
+        rope_theta: float = 10000,
+        swiglu_alpha: float = 1.702,
+        swiglu_limit: float = 7.0,
+        use_checkpoint: bool = True,
+        logit_softcap: float = 15.0,
+        pad_vocab_size_to: int = 64,
+        attn_res_layers_per_block: int = 1,
+        label_smoothing_sigma: float = 0.0,
+    ) -> None:
+        super().__init__(
+            block_size=block_size,
+            vocab_size=vocab_size,
+            n_embd=n_embd,
+            n_head=n_head,
+            n_layer=n_layer,
+        )
+        assert logit_softcap >= 0, "logit_softcap must be non-negative (0 disables it)"
+        assert label_smoothing_sigma >= 0, (
+            "label_smoothing_sigma must be non-negative (0 disables it)"
+        )
+        assert pad_vocab_size_to >= 1, "pad_vocab_size_to must be >= 1"
+        assert attn_res_layers_per_block >= 1, "attn_res_layers_per_block must be >= 1"
+        assert vocab_size % pad_vocab_size_to == 0, (
+            f"vocab_size ({vocab_size}) must be a multiple of "
+            f"pad_vocab_size_to ({pad_vocab_size_to}); pad it in the encoder"
+        )
+        self.token_embedding_table = nn.Embedding(vocab_size, n_embd)
+        self.blocks = nn.ModuleList(
+            Block(
+                n_embd=n_embd,
+                n_head=n_head,
+                swiglu_alpha=swiglu_alpha,
+                swiglu_limit=swiglu_limit,
+                layer_idx=i,
+                layers_per_block=attn_res_layers_per_block,
+            )
+            for i in range(n_layer)
+        )
+        # lm_head is created (consuming the seeded RNG) and then tied
+        self.lm_head = nn.Linear(n_embd, vocab_size, bias=False)
+        self.lm_head.weight = self.token_embedding_table.weight
+        # RoPE table for 2*block_size positions; not saved in the state_dict
+        self.register_buffer(
+            "freqs_cis",
+            precompute_freqs_cis(n_embd // n_head, block_size * 2, theta=rope_theta),
+            persistent=False,
+        )
+        self.use_checkpoint = use_checkpoint
+        self.logit_softcap = logit_softcap
+        self.label_smoothing_sigma = label_smoothing_sigma
+
+    def forward(
+        self,
+        idx: torch.Tensor,
+        targets: torch.Tensor | None = None,
+        kv_cache: KVCache | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        B, T = idx.shape
+        start = 0 if kv_cache is None else kv_cache.get_pos()
+        end = start + T
+        assert end <= self.freqs_cis.shape[0]
+        freqs_cis = self.freqs_cis[start:end].view(1, T, 1, -1, 2)
+
+        x = rms_norm(self.token_embedding_table(idx))
+        # Block-AttnRes state: the normalised embedding is block 0 and also the
+        # first partial sum
+        blocks: tuple[torch.Tensor, ...] = (x,)
+        partial = x
+        for block in self.blocks:
+            blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache)
+
+        logits = self.lm_head(rms_norm(partial))
+        if self.logit_softcap > 0:
+            cap = self.logit_softcap
+            logits = cap * torch.tanh(logits / cap)
+
+        loss = None
+        if targets is not None:
+            flat_logits = logits.view(B * T, -1)
+            flat_targets = targets.view(B * T)
+            if self.label_smoothing_sigma > 0:
+                loss = _gaussian_soft_ce(
+                    flat_logits, flat_targets, sigma=self.label_smoothing_sigma
+                )
+            else:
+                loss = F.cross_entropy(flat_logits, flat_targets)
+        return logits, loss
+
+    @torch.inference_mode()
+    def generate(
+        self,
+        idx: torch.Tensor,
+        max_new_tokens: int,
+        sampler: Sampler | None,
+        seed: int | None = None,
+    ) -> torch.Tensor:
+        """Cache-free sliding-window sampling (gpt.py:202-237): every step
+        re-runs the last block_size tokens through the causal prefill path."""
+        device = idx.device
+        rng = None
+        if seed is not None:
+            rng = torch.Generator(device=device)
+            rng.manual_seed(seed)
+        B, T = idx.shape
+        out = torch.zeros((B, T + max_new_tokens), dtype=torch.int64, device=device)
+        out[:, :T] = idx
+        for cur in range(T, T + max_new_tokens):
+            window = out[:, max(0, cur - self.block_size) : cur]
+            logits, _ = self(window)
+            last = logits[:, -1]
+            if sampler is not None:
+                nxt = sampler(last, rng=rng)
+            else:
+                nxt = torch.multinomial(F.softmax(last, dim=-1), num_samples=1, generator=rng)
+            out[:, cur] = nxt.squeeze()
+        return out
+
+    @property
+    def device_type(self) -> str:
+        return str(self.freqs_cis.device.type)

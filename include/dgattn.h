@@ -1,0 +1,145 @@
+/*
+ * dgattn.h -- C-ABI of the MI355X (gfx950) attention hot path of diff-gpt.
+ *
+ * The library (libdgattn.so) exports plain C entry points over raw device
+ * pointers, element strides and sizes.  No torch or HIP types appear in the
+ * signatures: a stream is passed as `void*` (a hipStream_t; NULL = the null
+ * stream).  Every entry point only enqueues work on that stream; none
+ * synchronises the host, none allocates device memory.  Buffers are owned by
+ * the caller.  Entry points return DG_OK (0) or a negative dg_status; the
+ * calling thread's last error message is available from dg_last_error().
+ *
+ * Layout vocabulary: a "(B,T,H,D) view" is addressed as
+ *     base + b*st.b + t*st.t + h*st.h + d          (element strides, d stride 1)
+ * The KV cache of the reference (kv_cache.py:25) is (L, 2, B, H, Tcap, D),
+ * i.e. for one layer and one of K/V the strides are b = H*Tcap*D, h = Tcap*D,
+ * t = D: one contiguous page of Tcap*D elements per (layer, K|V, row, head).
+ *
+ * Reference interfaces replaced (paths relative to fxeqxmulfx/diff-gpt):
+ *   src/diff_gpt/model/rope.py:4-27       apply_rotary_emb
+ *   src/diff_gpt/model/rms_norm.py:5-7    rms_norm (QK-norm at mha.py:48 and the
+ *                                         residual-stream norms of gpt.py/block.py)
+ *   src/diff_gpt/model/kv_cache.py:77-79  KVCache.prefill broadcast copy
+ *   src/diff_gpt/model/kv_cache.py:100-109 KVCache.insert_kv growth copy + append
+ *   src/diff_gpt/model/mha.py:44-56       RoPE x2, QK-norm x2, transpose, insert_kv
+ *   src/diff_gpt/model/mha.py:61-83       the three scaled_dot_product_attention
+ *                                         branches and the head re-assembly
+ */
+#ifndef DGATTN_H
+#define DGATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DG_ABI_VERSION 1
+
+#if defined(__GNUC__)
+#define DG_API __attribute__((visibility("default")))
+#else
+#define DG_API
+#endif
+
+/* Element types.  The reference computes in the model's dtype (fp32, or bf16
+ * after GPT.to(torch.bfloat16)); fp16 is accepted as well. */
+enum dg_dtype { DG_F32 = 0, DG_BF16 = 1, DG_F16 = 2 };
+
+enum dg_status {
+  DG_OK = 0,
+  DG_EINVAL = -1,       /* bad size, stride, alignment or pointer            */
+  DG_EUNSUPPORTED = -2, /* dtype / head_dim combination not built            */
+  DG_ELAUNCH = -3,      /* hipLaunchKernel / hipGetLastError reported failure */
+  DG_EWORKSPACE = -4    /* workspace missing or smaller than required        */
+};
+
+/* Flags of dg_rope_qknorm_append. */
+#define DG_QKNORM 1 /* apply the parameter-free RMSNorm after RoPE (mha.py:48) */
+
+/* Element strides of a (B,T,H,D) view; the D stride is always 1. */
+typedef struct dg_stride3 {
+  int64_t b, t, h;
+} dg_stride3;
+
+/* Returns DG_ABI_VERSION of the built library. */
+DG_API int dg_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+DG_API const char* dg_last_error(void);
+
+/*
+ * Fused RoPE + QK-norm + KV append.  Replaces mha.py:44-56: apply_rotary_emb on
+ * q and k (rope.py:4-27), rms_norm on both (rms_norm.py:5-7, eps = FLT_EPSILON,
+ * fp32 arithmetic), the (B,T,H,D)->(B,H,T,D) transposes and the two cache
+ * copies of KVCache.insert_kv (kv_cache.py:108-109).
+ *
+ * For every (b,t,h) row:
+ *   q_out[b,t,h,:] = norm(rope(q[b,t,h,:], freqs[b,t,h]))     if q != NULL
+ *   k_out[b,t,h,:] = norm(rope(k[b,t,h,:], freqs[b,t,h]))     if k != NULL
+ *   v_out[b,t,h,:] = v[b,t,h,:]                                if v != NULL
+ * norm() is applied only with DG_QKNORM.  freqs points at the (cos, sin) pairs
+ * of the row (the reference's (T, D/2, 2) table, kv_cache-position slice,
+ * gpt.py:150-153); f_st gives its element strides over (b,t,h) -- 0 for the
+ * broadcast dims -- and the D/2 pairs of a row are contiguous.  Pass k_out /
+ * v_out as the cache page at position `pos` (e.g. &cache[l,0,0,0,pos,0] with
+ * cache strides) to append.  Output dtype = input dtype (rope.py:27 type_as).
+ * Supported: D even, D <= 256 (powers of two) or D <= 128 (other even D).
+ */
+DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
+                          const void* q, const dg_stride3* q_st,
+                          void* q_out, const dg_stride3* qo_st,
+                          const void* k, const dg_stride3* k_st,
+                          void* k_out, const dg_stride3* ko_st,
+                          const void* v, const dg_stride3* v_st,
+                          void* v_out, const dg_stride3* vo_st,
+                          const void* freqs, const dg_stride3* f_st,
+                          int freqs_dtype, int flags, void* stream);
+
+/*
+ * Scaled dot-product attention of mha.py:61-81 with the head re-assembly of
+ * mha.py:83.  q is a (B,Tq,H,D) view, k and v are (B,Tk,H,D) views (for the
+ * KV cache: strides b=H*Tcap*D, t=D, h=Tcap*D), y a (B,Tq,H,D) view.  Query i
+ * sees key j iff j <= i + (Tk - Tq): this is is_causal=True when Tq == Tk
+ * (mha.py:64), the unmasked single-query decode when Tq == 1 (mha.py:68) and
+ * the bottom-right chunk mask otherwise (mha.py:69-81).  Softmax in fp32.
+ * scale is the SDPA scale (the reference uses the default 1/sqrt(D)).
+ *
+ * workspace: split-KV partials; dg_attention_workspace_size() gives the bytes
+ * needed for these sizes (0 when no split is used).  With workspace == NULL
+ * the library uses no split (always correct, slower for few long rows).
+ */
+DG_API size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int D, int dtype);
+
+DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
+                 const void* q, const dg_stride3* q_st,
+                 const void* k, const dg_stride3* k_st,
+                 const void* v, const dg_stride3* v_st,
+                 void* y, const dg_stride3* y_st, float scale,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with
+ * eps=None, i.e. FLT_EPSILON, computed in fp32 and rounded once to dtype).
+ * x and out are M rows of N elements with row strides x_ld / out_ld.
+ * Supported: N <= 8192.
+ */
+DG_API int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x_ld,
+                void* out, int64_t out_ld, void* stream);
+
+/*
+ * Strided 4-D copy dst[i0,i1,i2,i3] = src[i0,i1,i2,i3] over shape[4], element
+ * strides per tensor (a 0 src stride broadcasts).  Serves KVCache.insert_kv's
+ * append (kv_cache.py:108-109) and growth copy (kv_cache.py:100-106) and
+ * KVCache.prefill's batch broadcast (kv_cache.py:77-79).  Exact copy.
+ */
+DG_API int dg_copy4d(int dtype, const int64_t* shape, const void* src,
+              const int64_t* src_st, void* dst, const int64_t* dst_st,
+              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DGATTN_H */

@@ -1,0 +1,75 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry point
+include/dgattn.h declares, reports its ABI version, and rejects bad arguments
+with a status code and a message before touching the device."""
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import REPO
+
+
+def _declared_symbols():
+    text = (REPO / "include" / "dgattn.h").read_text()
+    return sorted(set(re.findall(r"DG_API\s+[\w\s\*]+?\b(dg_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    syms = _declared_symbols()
+    assert {"dg_abi_version", "dg_last_error", "dg_rope_qknorm_append", "dg_attention",
+            "dg_attention_workspace_size", "dg_rms_norm", "dg_copy4d"} <= set(syms)
+
+
+def test_library_exports_every_declared_symbol():
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), f"libdgattn.so does not export {name}"
+    assert lib.dg_abi_version() == _native.ABI_VERSION
+
+
+def _s3(b=0, t=0, h=0):
+    from diff_gpt._native import Stride3
+
+    return ctypes.pointer(Stride3(b, t, h))
+
+
+def test_argument_errors_return_status_and_message():
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    nul = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)
+    # odd head_dim
+    rc = lib.dg_rope_qknorm_append(1, 1, 1, 5, 0, fake, _s3(), fake, _s3(), nul, None, nul, None,
+                                   nul, None, nul, None, fake, _s3(), 0, 1, nul)
+    assert rc == -1 and b"even" in lib.dg_last_error()
+    # unsupported dtype
+    rc = lib.dg_attention(1, 1, 1, 1, 16, 7, fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(),
+                          1.0, nul, 0, nul)
+    assert rc == -2 and b"dtype" in lib.dg_last_error()
+    # Tk < Tq
+    rc = lib.dg_attention(1, 1, 4, 2, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(),
+                          1.0, nul, 0, nul)
+    assert rc == -1 and b"Tk" in lib.dg_last_error()
+    # rms_norm row too long
+    rc = lib.dg_rms_norm(1, 10000, 0, fake, 10000, fake, 10000, nul)
+    assert rc == -2
+    # empty work is a no-op success
+    assert lib.dg_attention(0, 1, 1, 1, 16, 0, nul, _s3(), nul, _s3(), nul, _s3(), nul, _s3(),
+                            1.0, nul, 0, nul) == 0
+
+
+def test_workspace_sizes():
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    # many rows: no split, no workspace
+    assert lib.dg_attention_workspace_size(6400, 4, 1, 144, 16, 0) == 0
+    # few long rows (cfg4 decode): split partials of (D + 2) fp32 per unit
+    ws = lib.dg_attention_workspace_size(64, 8, 1, 3680, 128, 1)
+    assert ws > 0 and ws % (130 * 4) == 0
+    # prefill never splits
+    assert lib.dg_attention_workspace_size(1, 1, 512, 512, 64, 1) == 0

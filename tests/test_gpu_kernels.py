@@ -1,0 +1,199 @@
+"""Kernel parity on the GPU through the C-ABI (libdgattn via diff_gpt._native).
+
+Bars:
+  * RoPE / QK-norm / KV append: bit-exact against oracle.numerics (same
+    canonical fp32 operation order); V and plain copies exact.
+  * attention: fp32 max-abs error <= 1e-5 * max|ref|; bf16 / fp16 within
+    2e-2 * max|ref| -- against float64 brute force on the same inputs.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import numerics as on
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+TOL = {"f32": 1e-5, "bf16": 2e-2, "f16": 2e-2}
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().view(np.uint32)
+
+
+def _randn(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(TDT[dtype])
+
+
+# ------------------------------------------------------------------ RoPE + QK-norm + append
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", [8, 16, 64, 128, 256, 12])
+def test_rope_qknorm_append_bit_exact(dev, dtype, D):
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, T, H, pos, cap = 3, 5, 4, 7, 16
+    q = _randn((B, T, H, D), 10 + D, dtype, 2.0)
+    k = _randn((B, T, H, D), 20 + D, dtype, 2.0)
+    v = _randn((B, T, H, D), 30 + D, dtype)
+    table = precompute_freqs_cis(D, 64, 10000).to(TDT[dtype])
+    fc = table[pos:pos + T].view(1, T, 1, D // 2, 2)
+
+    cache = torch.full((2, 2, B, H, cap, D), 7.0, dtype=TDT[dtype])
+    layer = 1
+    qd, kd, vd, fd = (t.to(dev) for t in (q, k, v, fc))
+    cd = cache.to(dev)
+    q_out = torch.empty_like(qd)
+    k_dst = cd[layer, 0, :, :, pos:pos + T].transpose(1, 2)
+    v_dst = cd[layer, 1, :, :, pos:pos + T].transpose(1, 2)
+    _native.ops().rope_qknorm_append(qd, kd, vd, fd, q_out, k_dst, v_dst, True)
+    torch.cuda.synchronize()
+
+    fcn = fc.float().numpy()
+    exp_q = on.rope_qknorm(q.float().numpy(), fcn, dtype)
+    exp_k = on.rope_qknorm(k.float().numpy(), fcn, dtype)
+    got = cd.cpu()
+    assert np.array_equal(_bits(q_out), exp_q.view(np.uint32))
+    assert np.array_equal(_bits(got[layer, 0, :, :, pos:pos + T].transpose(1, 2)),
+                          exp_k.view(np.uint32))
+    assert torch.equal(got[layer, 1, :, :, pos:pos + T].transpose(1, 2), v)
+    # nothing outside the window was touched
+    untouched = got.clone()
+    untouched[layer, :, :, :, pos:pos + T] = 7.0
+    assert (untouched == 7.0).all()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_rope_only_bit_exact_with_broadcast_table(dev, dtype):
+    from diff_gpt.model.rope import apply_rotary_emb
+
+    x = _randn((2, 4, 8, 10), 3, dtype)  # D = 10: not a power of two
+    g = torch.Generator().manual_seed(4)
+    th = torch.randn(1, 1, 8, 5, generator=g)
+    fc = torch.stack([th.cos(), th.sin()], -1).to(TDT[dtype])
+    out = apply_rotary_emb(x.to(dev), fc.to(dev))
+    exp = on.rope(x.float().numpy(), np.broadcast_to(fc.float().numpy(), (2, 4, 8, 5, 2)), dtype)
+    assert out.shape == x.shape and out.dtype == x.dtype
+    assert np.array_equal(_bits(out), exp.view(np.uint32))
+
+
+# ------------------------------------------------------------------ row RMSNorm
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("N", [5, 16, 64, 100, 1024, 4096])
+def test_rms_norm_bit_exact(dev, dtype, N):
+    from diff_gpt.model.rms_norm import rms_norm
+
+    x = _randn((3, 37, N), N, dtype, 3.0)
+    y = rms_norm(x.to(dev))
+    exp = on.rms_norm(x.float().numpy(), dtype)
+    assert y.dtype == x.dtype and y.shape == x.shape
+    assert np.array_equal(_bits(y), exp.view(np.uint32))
+
+
+# ------------------------------------------------------------------ attention
+
+
+def _attention_case(dev, dtype, B, H, Tq, Tk, D, cache_layout, seed):
+    from diff_gpt import _native
+
+    q = _randn((B, Tq, H, D), seed, dtype)
+    k = _randn((B, Tk, H, D), seed + 1, dtype)
+    v = _randn((B, Tk, H, D), seed + 2, dtype)
+    ref = on.attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    if cache_layout:
+        cap = Tk + 5
+        kc = torch.zeros((B, H, cap, D), dtype=TDT[dtype], device=dev)
+        vc = torch.zeros_like(kc)
+        kc[:, :, :Tk] = k.transpose(1, 2).to(dev)
+        vc[:, :, :Tk] = v.transpose(1, 2).to(dev)
+        kd, vd = kc[:, :, :Tk].transpose(1, 2), vc[:, :, :Tk].transpose(1, 2)
+    else:
+        kd, vd = k.to(dev), v.to(dev)
+    y = _native.ops().attention(q.to(dev), kd, vd, 1.0 / np.sqrt(D))
+    got = y.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    return err
+
+
+DECODE = [  # (B, H, Tk, D): cfg1 rows, cfg3 / cfg4 rows (few, long: key splits)
+    (64, 4, 144, 16),
+    (8, 8, 1536, 64),
+    (4, 8, 3680, 128),
+    (3, 2, 97, 32),
+    (2, 3, 33, 10),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", DECODE, ids=lambda s: "x".join(map(str, s)))
+def test_decode_attention_parity(dev, dtype, shape):
+    B, H, Tk, D = shape
+    err = _attention_case(dev, dtype, B, H, 1, Tk, D, cache_layout=True, seed=Tk + D)
+    assert err <= TOL[dtype], err
+
+
+PREFILL = [  # (B, H, Tq, Tk, D)
+    (2, 4, 96, 96, 16),   # cfg0/1 prefill
+    (2, 8, 256, 256, 64),
+    (1, 8, 300, 300, 128),
+    (2, 3, 5, 17, 32),    # chunked: bottom-right mask (mha.py:69-81)
+    (1, 2, 1, 1, 16),     # first token with a cache: Tq == Tk == 1
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", PREFILL, ids=lambda s: "x".join(map(str, s)))
+def test_prefill_attention_parity(dev, dtype, shape):
+    B, H, Tq, Tk, D = shape
+    err = _attention_case(dev, dtype, B, H, Tq, Tk, D, cache_layout=(Tq != Tk), seed=Tq + D)
+    assert err <= TOL[dtype], err
+
+
+def test_decode_without_workspace_matches_split(dev):
+    """A NULL workspace forces the single-pass path; both agree with fp64."""
+    from diff_gpt import _native
+
+    B, H, Tk, D = 4, 8, 2048, 64
+    q = _randn((B, 1, H, D), 1, "bf16").to(dev)
+    k = _randn((B, Tk, H, D), 2, "bf16").to(dev)
+    v = _randn((B, Tk, H, D), 3, "bf16").to(dev)
+    lib = _native.lib()
+    assert lib.dg_attention_workspace_size(B, H, 1, Tk, D, 1) > 0
+    y_split = _native.ops().attention(q, k, v, 0.125)
+    y_single = torch.empty_like(q)
+    st = [ctypes.pointer(_native._bthd_strides(t)) for t in (q, k, v, y_single)]
+    rc = lib.dg_attention(B, H, 1, Tk, D, 1, ctypes.c_void_p(q.data_ptr()), st[0],
+                          ctypes.c_void_p(k.data_ptr()), st[1], ctypes.c_void_p(v.data_ptr()), st[2],
+                          ctypes.c_void_p(y_single.data_ptr()), st[3], 0.125, None, 0,
+                          ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    ref = on.attention_f64(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), 0.125)
+    for y in (y_split, y_single):
+        err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+        assert err <= 2e-2
+
+
+# ------------------------------------------------------------------ strided copy
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_copy4d_exact_with_broadcast(dev, dtype):
+    from diff_gpt import _native
+
+    src = _randn((1, 3, 5, 7), 9, dtype).to(dev)
+    dst = torch.zeros((4, 3, 5, 7), dtype=TDT[dtype], device=dev)
+    _native.ops().copy4d(src.expand(4, 3, 5, 7), dst)
+    assert torch.equal(dst.cpu(), src.cpu().expand(4, 3, 5, 7))
+    # transposed destination view
+    dst2 = torch.zeros((3, 4, 7, 5), dtype=TDT[dtype], device=dev)
+    _native.ops().copy4d(src.expand(4, 3, 5, 7).transpose(0, 1).transpose(2, 3), dst2)
+    assert torch.equal(dst2.cpu(), src.cpu().expand(4, 3, 5, 7).transpose(0, 1).transpose(2, 3))

@@ -1,0 +1,412 @@
+"""The reference's model-level tests, run on the GPU through the HIP path, plus
+end-to-end parity with the CPU oracle (oracle.torch_ref).
+
+Ported in spirit from fxeqxmulfx/diff-gpt tests/diff_gpt/model/:
+test_rope.py, test_kv_cache.py, test_mha.py, test_block.py, test_gpt.py,
+test_engine.py (file:line cited per test).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+from torch.testing import assert_close
+
+from oracle import torch_ref as tr
+
+pytestmark = pytest.mark.gpu
+
+
+def _fc(seq_len, head_dim, dev, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    th = torch.randn(1, seq_len, 1, head_dim // 2, generator=g)
+    return torch.stack([th.cos(), th.sin()], dim=-1).to(dev)
+
+
+# ------------------------------------------------------------------ rope (test_rope.py)
+
+
+def test_rope_pi_over_2(dev):
+    from diff_gpt.model.rope import apply_rotary_emb
+
+    x = torch.tensor([[[[1.0, 0.0]]]], device=dev)
+    th = torch.tensor([[[[math.pi / 2]]]])
+    fc = torch.stack([th.cos(), th.sin()], -1).to(dev)
+    assert_close(apply_rotary_emb(x, fc).cpu(), torch.tensor([[[[0.0, 1.0]]]]), atol=1e-6, rtol=1e-6)
+
+
+def test_rope_explicit_formula(dev):
+    # test_rope.py:38-69 with a full (B,H,S,D/2,2) table
+    from diff_gpt.model.rope import apply_rotary_emb
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 4, 8, 16, generator=g)
+    th = torch.randn(2, 4, 8, 8, generator=g)
+    fc = torch.stack([th.cos(), th.sin()], -1)
+    out = apply_rotary_emb(x.to(dev), fc.to(dev)).cpu()
+    xr, xi = x[..., 0::2], x[..., 1::2]
+    exp = torch.stack([xr * th.cos() - xi * th.sin(), xr * th.sin() + xi * th.cos()], -1).flatten(3)
+    assert_close(out, exp)
+
+
+# ------------------------------------------------------------------ KV cache (test_kv_cache.py)
+
+
+def test_kv_cache_resize_keeps_contents(dev):
+    # test_kv_cache.py:7-81 (head_dim 5, growth on the 5th token)
+    from diff_gpt.model.kv_cache import KVCache
+
+    B, H, T, D, L = 2, 3, 4, 5, 6
+    c = KVCache(batch_size=B, num_heads=H, seq_len=T, head_dim=D, num_layers=L)
+
+    def put(tok):
+        for layer in range(L):
+            k = torch.full((B, H, 1, D), float(tok), device=dev)
+            c.insert_kv(layer, k, k * 100)
+
+    for i in range(4):
+        put(i)
+    before = c.kv_cache.clone()
+    put(4)
+    assert c.kv_cache.shape[4] > before.shape[4]
+    for layer in range(L):
+        for tok in range(4):
+            assert (c.kv_cache[layer, 0, :, :, tok] == tok).all()
+            assert (c.kv_cache[layer, 1, :, :, tok] == tok * 100).all()
+            assert torch.equal(c.kv_cache[layer, :, :, :, tok], before[layer, :, :, :, tok])
+
+
+def test_kv_cache_lazy_init_pos_and_chunks(dev):
+    # test_kv_cache.py:98-148
+    from diff_gpt.model.kv_cache import KVCache
+
+    c = KVCache(1, 2, 10, 8, 2)
+    k = torch.randn(1, 2, 1, 8, device=dev)
+    c.insert_kv(0, k, k)
+    assert c.get_pos() == 0
+    k_out, _ = c.insert_kv(1, k, k)
+    assert c.get_pos() == 1
+    assert_close(k_out[..., 0:1, :], k)
+    c2 = KVCache(1, 1, 20, 4, 1)
+    kk = torch.randn(1, 1, 5, 4, device=dev)
+    out_k, out_v = c2.insert_kv(0, kk, kk * 2)
+    assert c2.get_pos() == 5 and out_k.shape[-2] == 5
+    assert torch.equal(out_k, kk) and torch.equal(out_v, kk * 2)
+
+
+def test_kv_cache_growth_rounding(dev):
+    # test_kv_cache.py:151-178
+    from diff_gpt.model.kv_cache import KVCache
+
+    c = KVCache(1, 1, 10, 4, 1)
+    k0 = torch.randn(1, 1, 1, 4, device=dev)
+    c.insert_kv(0, k0, k0)
+    assert c.kv_cache.shape[4] == 10
+    kb = torch.randn(1, 1, 20, 4, device=dev)
+    c.insert_kv(0, kb, kb)
+    assert c.kv_cache.shape[4] == 2048 and c.get_pos() == 21
+    assert torch.equal(c.kv_cache[0, 0, 0, 0, 0], k0[0, 0, 0])
+    assert torch.equal(c.kv_cache[0, 0, :, :, 1:21], kb)
+
+
+def test_kv_cache_prefill_broadcast_and_reset(dev):
+    # test_kv_cache.py:181-227
+    from diff_gpt.model.kv_cache import KVCache
+
+    src = KVCache(1, 2, 10, 4, 1)
+    k = torch.randn(1, 2, 5, 4, device=dev)
+    src.insert_kv(0, k, k)
+    dst = KVCache(3, 2, 20, 4, 1)
+    dst.prefill(src)
+    assert dst.get_pos() == 5
+    for b in range(3):
+        assert torch.equal(dst.kv_cache[0, 0, b, :, :5], k[0])
+    src.reset()
+    assert src.get_pos() == 0
+    one = torch.ones(1, 2, 1, 4, device=dev)
+    out_k, _ = src.insert_kv(0, one, one)
+    assert torch.equal(out_k, one)
+
+
+# ------------------------------------------------------------------ MHA (test_mha.py)
+
+
+def test_mha_causality(dev):
+    # test_mha.py:48-77
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(0)
+    m = MultiHeadAttention(16, 2, 0).to(dev).eval()
+    x = torch.randn(1, 5, 16, device=dev)
+    fc = _fc(5, 8, dev)
+    with torch.no_grad():
+        y0 = m(x, fc, kv_cache=None)
+        xp = x.clone()
+        xp[:, -1] += 1.0
+        y1 = m(xp, fc, kv_cache=None)
+    assert_close(y0[:, :-1], y1[:, :-1])
+    assert not torch.allclose(y0[:, -1], y1[:, -1])
+
+
+def test_mha_kv_step_equals_batch(dev):
+    # test_mha.py:80-119
+    from diff_gpt.model.kv_cache import KVCache
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(1)
+    m = MultiHeadAttention(16, 2, 0).to(dev).eval()
+    x = torch.randn(1, 4, 16, device=dev)
+    fc = _fc(4, 8, dev, seed=1)
+    kv = KVCache(batch_size=1, num_heads=2, seq_len=10, head_dim=8, num_layers=1)
+    with torch.no_grad():
+        full = m(x, fc, kv_cache=None)
+        steps = [m(x[:, t:t + 1], fc[:, t:t + 1], kv_cache=kv) for t in range(4)]
+    assert_close(torch.cat(steps, 1), full, atol=1e-5, rtol=1e-5)
+
+
+def test_mha_chunked_prefill_then_decode(dev):
+    # test_mha.py:122-158, plus a genuine chunk (Tq=3 over Tk=5) that takes the
+    # bottom-right mask branch the reference test never reaches
+    from diff_gpt.model.kv_cache import KVCache
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(2)
+    m = MultiHeadAttention(16, 2, 0).to(dev).eval()
+    x = torch.randn(1, 6, 16, device=dev)
+    fc = _fc(6, 8, dev, seed=2)
+    kv = KVCache(batch_size=1, num_heads=2, seq_len=10, head_dim=8, num_layers=1)
+    with torch.no_grad():
+        full = m(x, fc, None)
+        a = m(x[:, :2], fc[:, :2], kv)
+        assert kv.get_pos() == 2
+        b = m(x[:, 2:5], fc[:, 2:5], kv)
+        assert kv.get_pos() == 5
+        c = m(x[:, 5:6], fc[:, 5:6], kv)
+        assert kv.get_pos() == 6
+    assert_close(torch.cat([a, b, c], 1), full, atol=1e-5, rtol=1e-5)
+
+
+def test_block_kv_step_consistency(dev):
+    # test_block.py:129-166 (AttnRes active, layers_per_block=2)
+    from diff_gpt.model.block import Block
+    from diff_gpt.model.kv_cache import KVCache
+
+    torch.manual_seed(3)
+    m = Block(16, 2, 1.0, 10.0, layer_idx=0, layers_per_block=2).to(dev).eval()
+    x = torch.randn(1, 6, 16, device=dev)
+    fc = _fc(6, 8, dev, seed=3)
+    kv = KVCache(batch_size=1, num_heads=2, seq_len=20, head_dim=8, num_layers=1)
+    with torch.no_grad():
+        _, full = m((x,), x, freqs_cis=fc, kv_cache=None)
+        outs = [m((x[:, t:t + 1],), x[:, t:t + 1], freqs_cis=fc[:, t:t + 1], kv_cache=kv)[1]
+                for t in range(6)]
+    assert_close(torch.cat(outs, 1), full, atol=1e-5, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ GPT (test_gpt.py)
+
+
+def _gpt(dev, seed=0, **kw):
+    from diff_gpt.model.gpt import GPT
+
+    torch.manual_seed(seed)
+    return GPT(**kw).to(dev).eval()
+
+
+def test_gpt_kv_cache_consistency(dev):
+    # test_gpt.py:34-76, with two layers and a batch of 3
+    from diff_gpt.model.kv_cache import KVCache
+
+    m = _gpt(dev, vocab_size=64, n_embd=16, block_size=20, n_layer=2, n_head=2, use_checkpoint=False)
+    idx = torch.randint(0, 64, (3, 5), generator=torch.Generator().manual_seed(0)).to(dev)
+    kv = KVCache(batch_size=3, num_heads=2, seq_len=20, head_dim=8, num_layers=2)
+    with torch.no_grad():
+        full, _ = m(idx)
+        steps = [m(idx[:, t:t + 1], kv_cache=kv)[0] for t in range(5)]
+    assert_close(full, torch.cat(steps, 1), atol=1e-5, rtol=1e-5)
+
+
+def test_gpt_generate_length_and_seed(dev):
+    # test_gpt.py:102-137
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    m = _gpt(dev, vocab_size=64, n_embd=32, block_size=16, n_layer=1)
+    idx = torch.randint(0, 64, (1, 5), generator=torch.Generator().manual_seed(1)).to(dev)
+    assert m.generate(idx, max_new_tokens=3, sampler=None).shape == (1, 8)
+    s = TemperatureSampler(temperature=20.0)
+    a = m.generate(idx, max_new_tokens=8, sampler=s, seed=7)
+    b = m.generate(idx, max_new_tokens=8, sampler=s, seed=7)
+    c = m.generate(idx, max_new_tokens=8, sampler=s, seed=99)
+    assert torch.equal(a, b) and not torch.equal(a, c)
+
+
+def test_gpt_softcap_bound(dev):
+    # test_gpt.py:188-218
+    m = _gpt(dev, vocab_size=64, n_embd=16, block_size=12, n_layer=2, n_head=2)
+    with torch.no_grad():
+        m.lm_head.weight.mul_(100.0)
+        logits, _ = m(torch.randint(0, 64, (2, 6), device=dev))
+    assert logits.abs().max().item() <= m.logit_softcap + 1e-5
+    assert logits.abs().max().item() >= m.logit_softcap - 1e-3
+
+
+def test_gpt_rejects_autograd(dev):
+    m = _gpt(dev, vocab_size=64, n_embd=16, block_size=12, n_layer=1, n_head=2).train()
+    with pytest.raises(RuntimeError, match="inference-only"):
+        m(torch.zeros(1, 4, dtype=torch.long, device=dev), torch.zeros(1, 4, dtype=torch.long, device=dev))
+
+
+# ------------------------------------------------------------------ Engine (test_engine.py)
+
+
+@pytest.fixture(scope="module")
+def engine_model(dev):
+    return _gpt(dev, vocab_size=64, n_embd=32, block_size=16, n_head=4, n_layer=2)
+
+
+def test_engine_shapes_and_determinism(engine_model):
+    # test_engine.py:35-121
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    e = Engine(engine_model)
+    r, m = e.generate_batch(tokens=[1, 2, 3], num_samples=4, max_tokens=5)
+    assert len(r) == 4 and all(len(x) == 8 for x in r) and all(len(x) == 8 for x in m)
+    hot = TemperatureSampler(temperature=20)
+    r1, _ = e.generate_batch(tokens=[5, 8, 12], num_samples=2, max_tokens=10, seed=42, sampler=hot)
+    r2, _ = e.generate_batch(tokens=[5, 8, 12], num_samples=2, max_tokens=10, seed=42, sampler=hot)
+    r3, _ = e.generate_batch(tokens=[5, 8, 12], num_samples=2, max_tokens=10, seed=99, sampler=hot)
+    assert r1 == r2 and r1 != r3
+
+
+def test_engine_streaming_equals_batch(engine_model):
+    # test_engine.py:124-166
+    from diff_gpt.model.engine import Engine
+
+    e = Engine(engine_model)
+    rb, mb = e.generate_batch(tokens=[10, 20], num_samples=3, max_tokens=4, seed=123)
+    rs = [[10, 20] for _ in range(3)]
+    ms = [[0, 0] for _ in range(3)]
+    for col, mcol in e.generate(tokens=[10, 20], num_samples=3, max_tokens=4, seed=123):
+        for i in range(3):
+            rs[i].append(col[i])
+            ms[i].append(mcol[i])
+    assert rb == rs and mb == ms
+
+
+def test_engine_ceiling_and_budget(engine_model):
+    # test_engine.py:212-247
+    from diff_gpt.model.engine import Engine
+
+    e = Engine(engine_model)
+    ceil = engine_model.block_size * 2
+    r, _ = e.generate_batch(tokens=[1, 2, 3], num_samples=1, max_tokens=ceil - 3 + 50)
+    assert len(r[0]) == ceil
+    r, _ = e.generate_batch(tokens=[1, 2, 3, 4], num_samples=1)
+    assert len(r[0]) == ceil
+
+
+def test_engine_force_schedule(engine_model):
+    # test_engine.py:249-285
+    from diff_gpt.model.engine import Engine
+
+    e = Engine(engine_model)
+    sched = [7, None, 11, None, 13, None]
+    r, m = e.generate_batch(tokens=[1, 2, 3], num_samples=2, max_tokens=6, force_schedule=sched)
+    for row, mask in zip(r, m):
+        tail = row[3:]
+        assert tail[0] == 7 and tail[2] == 11 and tail[4] == 13
+        assert mask[3:] == [0, 1, 0, 1, 0, 1]
+    r, _ = e.generate_batch(tokens=[1, 2], num_samples=3, max_tokens=4, force_schedule=[5, 6, 7, 8])
+    assert all(row[2:] == [5, 6, 7, 8] for row in r)
+
+
+def test_engine_prefill_clone_equivalence(engine_model):
+    # test_engine.py:301-347
+    from diff_gpt.model.engine import Engine
+
+    greedy = lambda logits, rng: torch.argmax(logits, dim=-1, keepdim=True)  # noqa: E731
+    e = Engine(engine_model)
+    many, _ = e.generate_batch(tokens=[1, 8, 4, 9], num_samples=4, max_tokens=6, sampler=greedy)
+    one, _ = e.generate_batch(tokens=[1, 8, 4, 9], num_samples=1, max_tokens=6, sampler=greedy)
+    assert all(row == many[0] for row in many)
+    assert many == one * 4
+
+
+# ------------------------------------------------------------------ end-to-end parity with the oracle
+
+
+def _cfg0_model(dev, dtype=torch.float32):
+    m = _gpt(dev, vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2,
+             use_checkpoint=False)
+    return m.to(dtype)
+
+
+def test_cfg0_greedy_ids_and_logits_match_oracle(dev):
+    """fp32, 32 prompts of 96 ids, 48 greedy KV-cache decode
+    steps.  Teacher-forced on the oracle's greedy tokens, every step's logits
+    agree within 1e-4 and the argmax equals the oracle's token wherever the
+    oracle's top-1/top-2 margin exceeds 1e-3 (ties aside, ids are identical)."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    model = _cfg0_model(dev)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2)
+    prompts = torch.randint(0, 256, (32, 96), generator=torch.Generator().manual_seed(1))
+    ref_tokens, ref_logits = tr.greedy_decode(params, cfg, prompts, 48)
+
+    kv = KVCache(batch_size=32, num_heads=4, seq_len=144, head_dim=16, num_layers=2)
+    with torch.no_grad():
+        logits, _ = model(prompts.to(dev), kv_cache=kv)
+        logits = logits[:, -1]
+        checked = 0
+        for s in range(48):
+            ref = ref_logits[s]
+            assert_close(logits.cpu(), ref, atol=1e-4, rtol=1e-4)
+            top2 = ref.topk(2, dim=-1).values
+            clear = (top2[:, 0] - top2[:, 1]) > 1e-3
+            ours = logits.argmax(-1).cpu()
+            assert torch.equal(ours[clear], ref_tokens[clear, s])
+            checked += int(clear.sum())
+            logits, _ = model(ref_tokens[:, s:s + 1].to(dev), kv_cache=kv)
+            logits = logits[:, -1]
+    assert checked > 0.95 * 32 * 48
+    assert kv.get_pos() == 96 + 48
+
+
+def test_cfg0_kv_cache_contents_match_oracle(dev):
+    """After the cfg0 prefill, the cache holds the oracle's rotated+normed K and
+    raw V (same model weights; the projections differ only by GEMM rounding)."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    model = _cfg0_model(dev)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2)
+    prompts = torch.randint(0, 256, (8, 96), generator=torch.Generator().manual_seed(2))
+    kv = KVCache(batch_size=8, num_heads=4, seq_len=96, head_dim=16, num_layers=2)
+    with torch.no_grad():
+        model(prompts.to(dev), kv_cache=kv)
+        ref = tr.RefCache(8, 4, 96, 16, 2)
+        tr.forward(params, cfg, prompts, ref)
+    assert_close(kv.kv_cache.cpu(), ref.data, atol=2e-5, rtol=1e-4)
+
+
+def test_bf16_model_logits_close_to_oracle(dev):
+    """cfg0/1 model cast to bf16 (freqs table included, gpt.py buffer .to()):
+    prefill + 8 decode steps against the oracle run in bf16 on the CPU."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    model = _cfg0_model(dev, torch.bfloat16)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2)
+    prompts = torch.randint(0, 256, (16, 96), generator=torch.Generator().manual_seed(3))
+    _, ref_logits = tr.greedy_decode(params, cfg, prompts, 8)
+    ref_tokens = torch.stack([l.argmax(-1) for l in ref_logits], 1)
+    kv = KVCache(batch_size=16, num_heads=4, seq_len=104, head_dim=16, num_layers=2)
+    with torch.no_grad():
+        logits = model(prompts.to(dev), kv_cache=kv)[0][:, -1]
+        for s in range(8):
+            err = (logits.float().cpu() - ref_logits[s].float()).abs().max().item()
+            assert err <= 0.25, (s, err)  # softcapped logits in [-15, 15], bf16 through 2 layers
+            logits = model(ref_tokens[:, s:s + 1].to(dev), kv_cache=kv)[0][:, -1]
