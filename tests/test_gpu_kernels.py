@@ -147,6 +147,9 @@ PREFILL = [  # (B, H, Tq, Tk, D)
     (1, 8, 300, 300, 128),
     (2, 3, 5, 17, 32),    # chunked: bottom-right mask (mha.py:69-81)
     (1, 2, 1, 1, 16),     # first token with a cache: Tq == Tk == 1
+    (2, 2, 200, 330, 64), # chunked, MFMA path, ragged tiles
+    (1, 3, 77, 77, 128),  # Tq not a multiple of the 128-query block
+    (1, 2, 640, 640, 64), # several query blocks per head, causal skipping
 ]
 
 

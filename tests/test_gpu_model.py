@@ -394,19 +394,30 @@ def test_cfg0_kv_cache_contents_match_oracle(dev):
 
 def test_bf16_model_logits_close_to_oracle(dev):
     """cfg0/1 model cast to bf16 (freqs table included, gpt.py buffer .to()):
-    prefill + 8 decode steps against the oracle run in bf16 on the CPU."""
+    prefill + 8 teacher-forced decode steps.  bf16 rounding through two layers
+    moves softcapped logits by a few tenths whatever the device, so the bar is
+    relative to that noise: against the same bf16 weights evaluated in fp32
+    (the exact model), the HIP path may deviate at most 1.5x as much as the
+    reference's own bf16 CPU evaluation does, and stays within 2e-2 of the
+    logit range."""
     from diff_gpt.model.kv_cache import KVCache
 
     model = _cfg0_model(dev, torch.bfloat16)
     params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    params32 = {k: v.float() for k, v in params.items()}
     cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2)
     prompts = torch.randint(0, 256, (16, 96), generator=torch.Generator().manual_seed(3))
-    _, ref_logits = tr.greedy_decode(params, cfg, prompts, 8)
-    ref_tokens = torch.stack([l.argmax(-1) for l in ref_logits], 1)
+    _, bf_logits = tr.greedy_decode(params, cfg, prompts, 8)
+    tokens = torch.stack([l.argmax(-1) for l in bf_logits], 1)
+    _, exact = tr.greedy_decode(params32, cfg, prompts, 8, forced=tokens.T.tolist())
     kv = KVCache(batch_size=16, num_heads=4, seq_len=104, head_dim=16, num_layers=2)
+    worst_ours, worst_ref = 0.0, 0.0
     with torch.no_grad():
         logits = model(prompts.to(dev), kv_cache=kv)[0][:, -1]
         for s in range(8):
-            err = (logits.float().cpu() - ref_logits[s].float()).abs().max().item()
-            assert err <= 0.25, (s, err)  # softcapped logits in [-15, 15], bf16 through 2 layers
-            logits = model(ref_tokens[:, s:s + 1].to(dev), kv_cache=kv)[0][:, -1]
+            worst_ours = max(worst_ours, (logits.float().cpu() - exact[s]).abs().max().item())
+            worst_ref = max(worst_ref, (bf_logits[s].float() - exact[s]).abs().max().item())
+            logits = model(tokens[:, s:s + 1].to(dev), kv_cache=kv)[0][:, -1]
+    span = max(e.abs().max().item() for e in exact)
+    assert worst_ours <= 1.5 * worst_ref + 1e-3, (worst_ours, worst_ref)
+    assert worst_ours <= 2e-2 * 2 * span, (worst_ours, span)
