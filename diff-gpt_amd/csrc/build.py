@@ -32,6 +32,9 @@ CFLAGS = [
     "-fPIC",
     "-fvisibility=hidden",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # MFMA accumulators in VGPRs: the softmax reads every score with VALU ops,
+    # and AGPR-resident accumulators would need a copy each way per tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     # packed fp32 ops are kept out of every kernel of this library
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",

@@ -36,7 +36,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                              const void* v, const dg_stride3* v_st, const void* y,
-                             const dg_stride3* y_st);
+                             const dg_stride3* y_st, float scale);
 int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                  const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
@@ -98,7 +98,7 @@ extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, cons
   DG_REQUIRE(Tk >= Tq, DG_EINVAL, "attention: Tk (%d) < Tq (%d)", Tk, Tq);
   DG_REQUIRE(q && k && v && y && q_st && k_st && v_st && y_st, DG_EINVAL, "attention: NULL argument");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st))
+  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
     return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
   return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, workspace,
                        workspace_bytes, s);

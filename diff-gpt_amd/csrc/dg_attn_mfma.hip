@@ -1,23 +1,37 @@
 // bf16 / fp16 MFMA prefill attention for gfx950 (the causal / chunked
 // branches of mha.py:61-81 when Tq is large and head_dim is 64 or 128).
 //
-// Workgroup = 4 wavefronts = 128 queries of one (b, h); each wavefront owns 32
-// queries.  Keys stream through LDS in tiles of 64.  Both products are issued
+// Workgroup = 4 wavefronts; each wavefront owns QW blocks of 32 queries of one
+// (b, h), so a workgroup covers BM = 128*QW queries.  Keys stream through a
+// double-buffered LDS ring in tiles of BN = 64 (one barrier per tile; the
+// global loads of tile t+2 are in flight while tile t is computed and tile t+1
+// is being written to the other buffer).  Both products are issued
 // transposed so that a lane's statistics all belong to ONE query:
 //
 //   S^T (64 keys x 32 queries) = K (64 x D) . Q^T (D x 32)
-//        A = K rows from LDS, B = Q^T held in registers for the whole loop
+//        A = K rows from LDS (shared by the QW query blocks of the wave),
+//        B = Q^T held in registers for the whole loop
 //   O^T (D x 32 queries)      = V^T (D x 64) . P^T (64 x 32)
 //        A = V^T from the transposed LDS copy of V, B = P^T straight from
-//        the S^T accumulators (converted to bf16, no lane exchange)
+//        the S^T accumulators (packed to bf16/fp16, no lane exchange)
 //
 // with v_mfma_f32_32x32x16_{bf16,f16}.  Lane l (half hh = l/32) holds, in a
 // 32x32 accumulator block, row 8*(r/4) + 4*hh + r%4 of column l%32 for
 // register r; the column is the lane's query for both S^T and O^T, so the
-// online-softmax max / sum / rescale of a query stay inside lanes l and l^32.
-// The contraction order of P^T.V^T follows that register order (keys
-// 16c + 4hh + {0..3} and 16c + 8 + 4hh + {0..3} for chunk c); V^T is read from
-// LDS in exactly that permuted order, so P^T needs no shuffling.
+// online-softmax statistics of a query live in lanes l and l^32 and meet
+// through one v_permlane32_swap.  The contraction order of P^T.V^T follows
+// that register order (keys 16c + 4hh + {0..3} and 16c + 8 + 4hh + {0..3} for
+// chunk c); V^T is read from LDS in exactly that permuted order.
+//
+// Softmax arithmetic per score: one max (v_max3), one FMA (scale and max
+// subtraction in log2 units), one exp2, half a bf16 pack and half a dot2 (the
+// row sum adds the packed bf16/fp16 probabilities that also feed the MFMA, so
+// numerator and denominator use the same rounded values).  The running max
+// used as the exponent offset is raised only when a row's new maximum exceeds
+// it by more than kLazyLog2 (log2 units); in between, probabilities up to
+// 2^kLazyLog2 are accumulated exactly as the online softmax would after a
+// rescale, so the result is the same function -- only the rescale of the
+// accumulators is skipped.
 //
 // Causality: query i sees key j iff j <= i + (Tk - Tq).  Tiles entirely above
 // a wavefront's diagonal are skipped by that wavefront; only tiles crossing
@@ -27,11 +41,22 @@
 // head start first.
 #include "dg_common.h"
 
+#ifndef DG_PREFILL_QW_D64
+#define DG_PREFILL_QW_D64 1
+#endif
+#ifndef DG_PREFILL_QW_D128
+#define DG_PREFILL_QW_D128 1
+#endif
+
 namespace dg {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+typedef _Float16 __attribute__((ext_vector_type(2))) f16x2_t;
 typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16_t;
+// plain clang vector (not HIP's uint4 wrapper class) so staging arrays stay in registers
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 struct PrefillArgs {
   const void* q;
@@ -45,7 +70,8 @@ struct PrefillArgs {
   int H, Tq, Tk, q_offset;
   int nqb;     // query blocks per (b, h)
   int nwg;     // total workgroups
-  float scale_log2;
+  float scale_log2;  // SDPA scale * log2(e)
+  float lazy_raw;    // kLazyLog2 / scale_log2: allowed growth of a row max in raw score units
 };
 
 template <typename T>
@@ -57,12 +83,17 @@ struct MfmaOps<bf16_t> {
   __device__ static floatx16_t mma(vec8 a, vec8 b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
-  // hardware round-to-nearest-even conversion (v_cvt_pk_bf16_f32)
-  __device__ static vec8 pack(const float* x) {
-    vec8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (__bf16)x[i];
-    return r;
+  // v_cvt_pk_bf16_f32: round to nearest even, two values per instruction
+  __device__ static uint32_t pack2(float a, float b) {
+    bf16x2_t r;
+    r[0] = (__bf16)a;
+    r[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 against (1, 1))
+  __device__ static float add_pair(uint32_t p, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, p),
+                                           __builtin_bit_cast(bf16x2_t, 0x3f803f80u), acc, false);
   }
 };
 template <>
@@ -71,31 +102,63 @@ struct MfmaOps<f16_t> {
   __device__ static floatx16_t mma(vec8 a, vec8 b, floatx16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  __device__ static vec8 pack(const float* x) {
-    vec8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = (_Float16)x[i];
-    return r;
+  __device__ static uint32_t pack2(float a, float b) {
+    f16x2_t r;
+    r[0] = (_Float16)a;
+    r[1] = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, r);
+  }
+  __device__ static float add_pair(uint32_t p, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, p),
+                                  __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
   }
 };
 
-constexpr int kBM = 128;  // queries per workgroup
-constexpr int kBN = 64;   // keys per tile
+constexpr int kBN = 64;             // keys per tile
+constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
-template <typename T, int D>
+// max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
+// value in both operands leaves every lane holding its own value in one
+// result and lane l^32's in the other (which one depends on the half), so a
+// commutative op over the pair gives both halves the same bits.
+__device__ __forceinline__ float half_pair_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_pair_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <typename T, int D, int QW>
+struct PrefillCfg {
+  static constexpr int BM = 128 * QW;       // queries per workgroup
+  static constexpr int KP = D + 8;          // padded K row (elements)
+  static constexpr int VP = kBN + 4;        // padded V^T row (elements)
+  static constexpr int K_ELEMS = kBN * KP;
+  static constexpr int V_ELEMS = D * VP;
+  static constexpr int BUF = K_ELEMS + V_ELEMS;  // one ring slot
+  static constexpr int LDS_BYTES = 2 * BUF * 2;
+  static constexpr int NC = D / 16;         // 16-wide contraction chunks of QK^T
+  static constexpr int NB = D / 32;         // 32-row blocks of O^T
+  static constexpr int CPR = D / 8;         // 16-byte chunks per K row
+  static constexpr int KCPT = kBN * CPR / 256;      // K chunks per thread per tile
+  static constexpr int VBPT = kBN * D / 16 / 256;   // 4x4 V blocks per thread per tile
+  static_assert(KCPT >= 1 && (kBN * CPR) % 256 == 0, "K tile mapping");
+  static_assert(VBPT >= 1 && (kBN * D / 16) % 256 == 0, "V tile mapping");
+};
+
+template <typename T, int D, int QW>
 __global__ __launch_bounds__(256) void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
-  constexpr int KP = D + 8;    // padded K row (elements): 16-byte aligned, bank-shifted
-  constexpr int VP = kBN + 8;  // padded V^T row
-  constexpr int NC = D / 16;   // 16-wide contraction chunks of QK^T
-  constexpr int NB = D / 32;   // 32-row blocks of O^T
-  constexpr int CPR = D / 8;   // 16-byte chunks per K/V row
-  constexpr int CPT = kBN * CPR / 256;  // chunks per thread per tile (K and V each)
-  static_assert(CPT >= 1 && (kBN * CPR) % 256 == 0, "tile mapping");
+  using C = PrefillCfg<T, D, QW>;
+  constexpr int KP = C::KP, VP = C::VP, NC = C::NC, NB = C::NB, CPR = C::CPR;
+  constexpr int KCPT = C::KCPT, VBPT = C::VBPT;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[D * VP];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * C::BUF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -111,9 +174,8 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const PrefillArgs a) 
   const int head = bh % a.H;
   const int64_t b = bh / a.H;
 
-  const int q0 = qblk * kBM;
-  const int qw = q0 + 32 * wv;  // first query of this wavefront
-  const int qi = qw + r32;      // this lane's query
+  const int q0 = qblk * C::BM;
+  const int qw = q0 + 32 * QW * wv;  // first query of this wavefront
   const int qoff = a.q_offset;
 
   const T* qp = static_cast<const T*>(a.q) + b * a.qb + (int64_t)head * a.qh;
@@ -121,164 +183,272 @@ __global__ __launch_bounds__(256) void prefill_mfma_kernel(const PrefillArgs a) 
   const T* vp = static_cast<const T*>(a.v) + b * a.vb + (int64_t)head * a.vh;
 
   // Q^T fragments (B operand): lane holds Q[qi][16c + 8hh .. +8]
-  vec8 qf[NC];
+  vec8 qf[QW][NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (qi < a.Tq) raw = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * a.qt + 16 * c + 8 * hh);
-    qf[c] = __builtin_bit_cast(vec8, raw);
+  for (int qb = 0; qb < QW; ++qb) {
+    const int qi = qw + 32 * qb + r32;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (qi < a.Tq) raw = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * a.qt + 16 * c + 8 * hh);
+      qf[qb][c] = __builtin_bit_cast(vec8, raw);
+    }
   }
 
-  const int kv_end = min(a.Tk, q0 + kBM + qoff);
+  const int kv_end = min(a.Tk, q0 + C::BM + qoff);
   const int ntiles = (kv_end + kBN - 1) / kBN;
   const bool wave_live = qw < a.Tq;
-  const int wave_last_key = qw + 31 + qoff;  // largest key any query of this wave sees
+  const int wave_last_key = qw + 32 * QW - 1 + qoff;  // largest key any query of this wave sees
 
-  floatx16_t o[NB];
+  floatx16_t o[QW][NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[nb][r] = 0.f;
-  float m = kNegInf, l = 0.f;
-
-  uint4 kreg[CPT], vreg[CPT];
-  auto gload = [&](int kt0) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int chunk = tid + 256 * i;
-      const int key = chunk / CPR, dc = chunk % CPR;
-      const int t = kt0 + key;
-      if (t < a.Tk) {
-        kreg[i] = *reinterpret_cast<const uint4*>(kp + (int64_t)t * a.kt + 8 * dc);
-        vreg[i] = *reinterpret_cast<const uint4*>(vp + (int64_t)t * a.vt + 8 * dc);
-      } else {
-        kreg[i] = make_uint4(0, 0, 0, 0);
-        vreg[i] = make_uint4(0, 0, 0, 0);
-      }
-    }
-  };
-
-  if (ntiles > 0) gload(0);
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int kt0 = tile * kBN;
-    __syncthreads();  // previous tile's LDS reads are done
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int chunk = tid + 256 * i;
-      const int key = chunk / CPR, dc = chunk % CPR;
-      *reinterpret_cast<uint4*>(&Ks[key * KP + 8 * dc]) = kreg[i];
-      uint16_t e[8];
-      __builtin_memcpy(e, &vreg[i], 16);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) Vt[(8 * dc + j) * VP + key] = e[j];
-    }
-    __syncthreads();
-    if (tile + 1 < ntiles) gload(kt0 + kBN);  // in flight while this tile computes
-
-    if (!wave_live || kt0 > wave_last_key) continue;  // tile entirely above this wave's diagonal
-
-    // S^T = K . Q^T for the two 32-key halves of the tile
-    floatx16_t s[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[mb][r] = 0.f;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * KP + 16 * c + 8 * hh]);
-        s[mb] = Ops::mma(__builtin_bit_cast(vec8, raw), qf[c], s[mb]);
-      }
-    }
-
-    // scale into log2 units, mask, tile max
-    const bool needs_mask = (kt0 + kBN - 1 > qw + qoff) || (kt0 + kBN > a.Tk);
-    float mt = kNegInf;
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[mb][r] * a.scale_log2;
-        if (needs_mask) {
-          const int key = kt0 + 32 * mb + 8 * (r >> 2) + 4 * hh + (r & 3);
-          if (key > qi + qoff || key >= a.Tk) x = kNegInf;
-        }
-        s[mb][r] = x;
-        mt = fmaxf(mt, x);
-      }
-    }
-    mt = fmaxf(mt, shfl_xor(mt, 32));
-    const float m_new = fmaxf(m, mt);
-    const float alpha = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
-    l *= alpha;
+  for (int qb = 0; qb < QW; ++qb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[nb][r] *= alpha;
-
-    // P^T fragments: chunk c = 2*mb + r/8, item r%8
-    vec8 pf[4];
-    float ls = 0.f;
+      for (int r = 0; r < 16; ++r) o[qb][nb][r] = 0.f;
+  float m[QW], l[QW];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        // m is finite here (key 0 is visible to every query and tile 0 is
-        // never skipped), so masked scores give exp2(-inf) = 0
-        const float p = __builtin_amdgcn_exp2f(s[mb][r] - m);
-        ls += p;
-        s[mb][r] = p;
-      }
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        float t8[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t8[i] = s[mb][8 * c2 + i];
-        pf[2 * mb + c2] = Ops::pack(t8);
-      }
-    }
-    l += ls;
-
-    // O^T += V^T . P^T
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const uint16_t* vrow = &Vt[(32 * nb + r32) * VP + 4 * hh];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * c);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * c + 8);
-        const uint4 raw = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        o[nb] = Ops::mma(__builtin_bit_cast(vec8, raw), pf[c], o[nb]);
-      }
-    }
+  for (int qb = 0; qb < QW; ++qb) {
+    m[qb] = kNegInf;
+    l[qb] = 0.f;
   }
 
-  if (!wave_live || qi >= a.Tq) return;
-  const float lt = l + shfl_xor(l, 32);
-  const float inv = 1.0f / lt;
-  T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)qi * a.yt + (int64_t)head * a.yh;
+  // ---- global -> registers -> LDS staging of one key tile ------------------
+  // Per-thread element offsets inside a tile (32-bit: the host guarantees
+  // Tk * stride < 2^31); the tile base kt0 * stride is wave-uniform.
+  int koff[KCPT], kkey[KCPT], kdst[KCPT];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+  for (int i = 0; i < KCPT; ++i) {
+    const int chunk = tid + 256 * i;
+    kkey[i] = chunk / CPR;
+    koff[i] = kkey[i] * (int)a.kt + 8 * (chunk % CPR);
+    kdst[i] = kkey[i] * KP + 8 * (chunk % CPR);
+  }
+  int vkey[VBPT], voff[VBPT], vdst[VBPT];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      T e[4];
+  for (int i = 0; i < VBPT; ++i) {
+    const int blk = tid + 256 * i;
+    const int dg = blk % (D / 4), kg = blk / (D / 4);
+    vkey[i] = 4 * kg;
+    voff[i] = 4 * kg * (int)a.vt + 4 * dg;
+    vdst[i] = (4 * dg) * VP + 4 * kg;
+  }
+  u32x4_t kreg[KCPT];
+  uint2 vreg[VBPT][4];
+
+#define DG_PREFILL_GLOAD(KT0)                                                              \
+  do {                                                                                     \
+    const int kt0_ = (KT0);                                                                \
+    const T* kbase = kp + (int64_t)kt0_ * a.kt;                                            \
+    const T* vbase = vp + (int64_t)kt0_ * a.vt;                                            \
+    if (kt0_ + kBN <= a.Tk) {                                                              \
+      _Pragma("unroll") for (int i = 0; i < KCPT; ++i)                                     \
+          kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + koff[i]);                      \
+      _Pragma("unroll") for (int i = 0; i < VBPT; ++i)                                     \
+          _Pragma("unroll") for (int j = 0; j < 4; ++j)                                    \
+              vreg[i][j] = *reinterpret_cast<const uint2*>(vbase + voff[i] + j * (int)a.vt); \
+    } else {                                                                               \
+      /* last, partial tile: rows past Tk re-read the last key; their scores are masked */ \
+      /* and their probabilities are 0, so only finiteness matters */                      \
+      const int last = a.Tk - 1 - kt0_;                                                    \
+      _Pragma("unroll") for (int i = 0; i < KCPT; ++i) {                                   \
+        const int shift = (min(kkey[i], last) - kkey[i]) * (int)a.kt;                      \
+        kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + koff[i] + shift);                \
+      }                                                                                    \
+      _Pragma("unroll") for (int i = 0; i < VBPT; ++i)                                     \
+          _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                  \
+        const int shift = (min(vkey[i] + j, last) - vkey[i]) * (int)a.vt;                  \
+        vreg[i][j] = *reinterpret_cast<const uint2*>(vbase + voff[i] + shift);             \
+      }                                                                                    \
+    }                                                                                      \
+  } while (0)
+
+  // 4 keys x 4 dims in registers -> 4 rows of V^T with 4 consecutive keys each
+  // (vreg[i][j].x = dims (0, 1) of key j, .y = dims (2, 3))
+#define DG_PREFILL_SSTORE(SLOT)                                                            \
+  do {                                                                                     \
+    uint16_t* Ks_ = lds + (SLOT) * C::BUF;                                                 \
+    uint16_t* Vt_ = Ks_ + C::K_ELEMS;                                                      \
+    _Pragma("unroll") for (int i = 0; i < KCPT; ++i)                                       \
+        *reinterpret_cast<u32x4_t*>(&Ks_[kdst[i]]) = kreg[i];                                \
+    _Pragma("unroll") for (int i = 0; i < VBPT; ++i) {                                     \
+      const uint2* e = vreg[i];                                                            \
+      const uint2 d0 = make_uint2((e[0].x & 0xffffu) | (e[1].x << 16),                     \
+                                  (e[2].x & 0xffffu) | (e[3].x << 16));                    \
+      const uint2 d1 = make_uint2((e[0].x >> 16) | (e[1].x & 0xffff0000u),                 \
+                                  (e[2].x >> 16) | (e[3].x & 0xffff0000u));                \
+      const uint2 d2 = make_uint2((e[0].y & 0xffffu) | (e[1].y << 16),                     \
+                                  (e[2].y & 0xffffu) | (e[3].y << 16));                    \
+      const uint2 d3 = make_uint2((e[0].y >> 16) | (e[1].y & 0xffff0000u),                 \
+                                  (e[2].y >> 16) | (e[3].y & 0xffff0000u));                \
+      uint16_t* vb_ = &Vt_[vdst[i]];                                                       \
+      *reinterpret_cast<uint2*>(vb_) = d0;                                                 \
+      *reinterpret_cast<uint2*>(vb_ + VP) = d1;                                            \
+      *reinterpret_cast<uint2*>(vb_ + 2 * VP) = d2;                                        \
+      *reinterpret_cast<uint2*>(vb_ + 3 * VP) = d3;                                        \
+    }                                                                                      \
+  } while (0)
+
+  if (ntiles > 0) {
+    DG_PREFILL_GLOAD(0);
+    DG_PREFILL_SSTORE(0);
+    if (ntiles > 1) DG_PREFILL_GLOAD(kBN);
+  }
+  __syncthreads();
+
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int kt0 = tile * kBN;
+    const int buf = tile & 1;
+    if (wave_live && kt0 <= wave_last_key) {
+      const uint16_t* Ks = lds + buf * C::BUF;
+      const uint16_t* Vt = Ks + C::K_ELEMS;
+
+      // S^T = K . Q^T for the two 32-key halves of the tile
+      floatx16_t s[QW][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) e[i] = from_f32<T>(o[nb][4 * g + i] * inv);
-      uint2 raw;
-      __builtin_memcpy(&raw, e, 8);
-      *reinterpret_cast<uint2*>(yp + 32 * nb + 8 * g + 4 * hh) = raw;
+      for (int qb = 0; qb < QW; ++qb)
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint4 raw = *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * KP + 16 * c + 8 * hh]);
+          const vec8 kf = __builtin_bit_cast(vec8, raw);
+#pragma unroll
+          for (int qb = 0; qb < QW; ++qb) s[qb][mb] = Ops::mma(kf, qf[qb][c], s[qb][mb]);
+        }
+      }
+
+      // mask (only on tiles that cross the diagonal or the end of the keys)
+      const bool needs_mask = (kt0 + kBN - 1 > qw + qoff) || (kt0 + kBN > a.Tk);
+      if (needs_mask) {
+#pragma unroll
+        for (int qb = 0; qb < QW; ++qb) {
+          const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
+#pragma unroll
+          for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
+              if (rel > lim) s[qb][mb][r] = kNegInf;
+            }
+        }
+      }
+
+      vec8 pf[QW][4];
+#pragma unroll
+      for (int qb = 0; qb < QW; ++qb) {
+        // tile max of the raw scores (scale > 0, so it commutes with the max)
+        float mt = s[qb][0][0];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
+        mt = half_pair_max(mt);
+        // raise the exponent offset only when some row of the wave would
+        // otherwise produce probabilities above 2^kLazyLog2
+        const float mnew = fmaxf(m[qb], mt);
+        if (__builtin_amdgcn_ballot_w64(mnew > m[qb] + a.lazy_raw) != 0) {
+          // m == -inf only before the first tile; key 0 is visible to every
+          // query, so mnew is finite from then on
+          const float alpha = (m[qb] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m[qb] - mnew) * a.scale_log2);
+          m[qb] = mnew;
+          l[qb] *= alpha;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qb][nb][r] *= alpha;
+        }
+        const float moff = m[qb] * a.scale_log2;
+        float ls = l[qb];
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i], a.scale_log2, -moff));
+              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i + 1], a.scale_log2, -moff));
+              w[i] = Ops::pack2(p0, p1);
+              ls = Ops::add_pair(w[i], ls);
+            }
+            pf[qb][2 * mb + c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+          }
+        }
+        l[qb] = ls;
+      }
+
+      // O^T += V^T . P^T
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint16_t* vrow = &Vt[(32 * nb + r32) * VP + 4 * hh];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * c);
+          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * c + 8);
+          const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+          for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c], o[qb][nb]);
+        }
+      }
+    }
+    if (tile + 1 < ntiles) {
+      DG_PREFILL_SSTORE(buf ^ 1);  // tile + 1, loaded one iteration ago
+      if (tile + 2 < ntiles) DG_PREFILL_GLOAD(kt0 + 2 * kBN);
+    }
+    __syncthreads();
+  }
+
+  if (!wave_live) return;
+#pragma unroll
+  for (int qb = 0; qb < QW; ++qb) {
+    const int qi = qw + 32 * qb + r32;
+    const float lt = half_pair_sum(l[qb]);
+    if (qi >= a.Tq) continue;
+    const float inv = 1.0f / lt;
+    T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)qi * a.yt + (int64_t)head * a.yh;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        T e[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = from_f32<T>(o[qb][nb][4 * g + i] * inv);
+        uint2 raw;
+        __builtin_memcpy(&raw, e, 8);
+        *reinterpret_cast<uint2*>(yp + 32 * nb + 8 * g + 4 * hh) = raw;
+      }
     }
   }
 }
+
+#undef DG_PREFILL_GLOAD
+#undef DG_PREFILL_SSTORE
 
 namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool strides8(const dg_stride3* s) { return s->b % 8 == 0 && s->t % 8 == 0 && s->h % 8 == 0; }
 
+template <int D>
+constexpr int qw_for() {
+  return D == 64 ? DG_PREFILL_QW_D64 : DG_PREFILL_QW_D128;
+}
+
 template <typename T, int D>
-int launch_prefill(const PrefillArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D>), dim3((unsigned)a.nwg), dim3(256), 0, s, a);
+int launch_prefill(PrefillArgs a, hipStream_t s) {
+  constexpr int QW = qw_for<D>();
+  constexpr int BM = PrefillCfg<T, D, QW>::BM;
+  a.nqb = (a.Tq + BM - 1) / BM;
+  const int64_t nwg = (int64_t)(a.nwg) * a.nqb;  // a.nwg holds B*H on entry
+  DG_REQUIRE(nwg <= 0x7fffffffLL, DG_EINVAL, "prefill: too many workgroups");
+  a.nwg = (int)nwg;
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW>), dim3((unsigned)a.nwg), dim3(256), 0, s, a);
   return check_launch("prefill_mfma_kernel");
 }
 
@@ -287,12 +457,17 @@ int launch_prefill(const PrefillArgs& a, hipStream_t s) {
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                              const void* v, const dg_stride3* v_st, const void* y,
-                             const dg_stride3* y_st) {
+                             const dg_stride3* y_st, float scale) {
+  (void)Tk;
+  if (!(scale > 0.f)) return false;  // the tile max of raw scores needs a positive scale
   if (dtype != DG_BF16 && dtype != DG_F16) return false;
   if (D != 64 && D != 128) return false;
   if (Tq < 16) return false;  // decode and tiny chunks: vector kernel
-  const int64_t nwg = (int64_t)B * H * ((Tq + kBM - 1) / kBM);
+  const int64_t nwg = (int64_t)B * H * ((Tq + 127) / 128);
   if (nwg <= 0 || nwg > 0x7fffffffLL) return false;
+  // per-head row offsets are 32-bit inside the kernel
+  const int64_t span = (int64_t)Tk * (k_st->t > v_st->t ? k_st->t : v_st->t);
+  if (span >= (int64_t)1 << 31 || k_st->t < 0 || v_st->t < 0) return false;
   return aligned16(q) && aligned16(k) && aligned16(v) && aligned16(y) && strides8(q_st) &&
          strides8(k_st) && strides8(v_st) && strides8(y_st);
 }
@@ -309,9 +484,9 @@ int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.yb = y_st->b; a.yt = y_st->t; a.yh = y_st->h;
   a.H = H; a.Tq = Tq; a.Tk = Tk;
   a.q_offset = Tk - Tq;
-  a.nqb = (Tq + kBM - 1) / kBM;
-  a.nwg = B * H * a.nqb;
+  a.nwg = B * H;
   a.scale_log2 = scale * 1.44269504088896340736f;
+  a.lazy_raw = kLazyLog2 / a.scale_log2;
   if (dtype == DG_BF16) return D == 64 ? launch_prefill<bf16_t, 64>(a, s) : launch_prefill<bf16_t, 128>(a, s);
   return D == 64 ? launch_prefill<f16_t, 64>(a, s) : launch_prefill<f16_t, 128>(a, s);
 }
