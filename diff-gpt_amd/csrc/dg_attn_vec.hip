@@ -6,11 +6,24 @@
 // the wave, LPK = DPAD/EPL lanes hold one key row (EPL consecutive elements
 // each, 16 bytes when the layout allows), so one wave instruction touches
 // KPI = 64/LPK consecutive cache rows: a contiguous, fully coalesced stretch of
-// the (b,h) page.  Each lane group keeps its own online-softmax state (running
-// max m, running sum l, the group's EPL-slice of sum p*v); the KPI groups are
-// merged with xor-butterflies at the end.  Scores use exp2 with log2(e) folded
-// into the scale.  With several key splits, unnormalised partials (acc, m, l)
-// go to the caller's workspace and attn_combine_kernel merges them.
+// the (b,h) page.  Keys are processed in trips of U slots (U*KPI keys); the
+// K/V registers of the next trip are loaded while the current trip computes
+// (two register sets, loop unrolled by two), so every wave keeps 2*U*2
+// sixteen-byte loads per lane in flight.
+//
+// Arithmetic per key slot and lane: the partial q.k over the lane's EPL
+// elements (fp32 FMAs, or v_dot2_f32_{bf16,f16} straight on the packed
+// 16-bit data -- products of two 16-bit floats are exact in fp32), a
+// register-only sum over the LPK lanes of the key (DPP / permlane, no LDS),
+// then the online softmax in log2 units with the SDPA scale folded into one
+// FMA: p = exp2(s*c - m*c), c = scale*log2(e), on raw scores s.  The offset m
+// is shared by the whole wave (a DPP max over the trip's scores): it is raised
+// only when a score exceeds it by more than kLazyLog2/c, so probabilities stay
+// <= 2^kLazyLog2 and the rescale of (l, acc) is skipped on most trips; the
+// result is the same function.  Because m is common to all KPI lane groups,
+// they merge at the end by plain register sums of l and acc.  With several
+// key splits the unnormalised partials (acc, m, l) go to the caller's
+// workspace and attn_combine_kernel merges them.
 #include "dg_common.h"
 
 namespace dg {
@@ -30,114 +43,211 @@ struct AttnArgs {
   int q_offset;  // Tk - Tq: query i sees keys j <= i + q_offset
   int nsplit, split_len;
   float scale_log2;  // scale * log2(e)
+  float lazy_raw;    // kLazyLog2 / scale_log2
 };
+
+constexpr float kVecLazyLog2 = 8.0f;
+
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
+typedef _Float16 __attribute__((ext_vector_type(2))) f16x2v_t;
+
+// EPL elements of one row as raw 32-bit words (EPL*sizeof(T) bytes).
+template <typename T, int EPL>
+struct RowRegs {
+  static constexpr int BYTES = EPL * (int)sizeof(T);
+  static constexpr int WORDS = BYTES / 4;
+  static_assert(BYTES % 4 == 0, "row slice must be whole 32-bit words");
+  uint32_t w[WORDS];
+};
+
+template <typename T, int EPL>
+__device__ __forceinline__ void load_row(RowRegs<T, EPL>& r, const T* p) {
+  constexpr int W = RowRegs<T, EPL>::WORDS;
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < W / 4; ++c) {
+      const u32x4_t x = reinterpret_cast<const u32x4_t*>(p)[c];
+      r.w[4 * c] = x[0];
+      r.w[4 * c + 1] = x[1];
+      r.w[4 * c + 2] = x[2];
+      r.w[4 * c + 3] = x[3];
+    }
+  } else if constexpr (W == 2) {
+    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
+    r.w[0] = x[0];
+    r.w[1] = x[1];
+  } else {
+    static_assert(W == 1, "row slice width");
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// Element e of the slice as fp32.
+template <typename T, int EPL>
+__device__ __forceinline__ float elem(const RowRegs<T, EPL>& r, int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(r.w[e]);
+  } else if constexpr (__is_same(T, bf16_t)) {
+    const uint32_t w = r.w[e >> 1];
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    const uint32_t w = r.w[e >> 1];
+    const uint16_t hbits = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return (float)__builtin_bit_cast(_Float16, hbits);
+  }
+}
+
+// Partial dot product of the lane's slices of q and k.
+template <typename T, int EPL>
+__device__ __forceinline__ float slice_dot(const RowRegs<T, EPL>& q, const RowRegs<T, EPL>& k) {
+  float d = 0.f;
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(__uint_as_float(q.w[e]), __uint_as_float(k.w[e]), d);
+  } else if constexpr (__is_same(T, bf16_t)) {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w)
+      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, q.w[w]),
+                                          __builtin_bit_cast(bf16x2v_t, k.w[w]), d, false);
+  } else {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w)
+      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v_t, q.w[w]),
+                                 __builtin_bit_cast(f16x2v_t, k.w[w]), d, false);
+  }
+  return d;
+}
 
 template <typename T, int DPAD, int EPL, int U>
 __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   constexpr int LPK = DPAD / EPL;
   constexpr int KPI = 64 / LPK;
+  constexpr int STEP = KPI * U;  // keys per trip
   static_assert(LPK >= 1 && LPK <= 64, "lane mapping");
+  using Row = RowRegs<T, EPL>;
 
   const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // wave-uniform unit index (the host keeps units below 2^31)
+  const int unit = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (unit >= a.units) return;  // whole wave exits; kernel has no barriers
 
   const int sub = lane % LPK;
   const int grp = lane / LPK;
-  int64_t r = unit;
-  const int split = (int)(r % a.nsplit);
+  int r = unit;
+  const int split = r % a.nsplit;
   r /= a.nsplit;
-  const int i = (int)(r % a.Tq);
+  const int i = r % a.Tq;
   r /= a.Tq;
-  const int h = (int)(r % a.H);
+  const int h = r % a.H;
   const int64_t b = r / a.H;
 
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
+  const int dl = active ? d0 : 0;  // inactive lanes (D not a power of two) read a valid slice
   const int kvis = min(a.Tk, i + a.q_offset + 1);
   const int kbeg = split * a.split_len;
   const int kend = min(kvis, kbeg + a.split_len);
+  const float c = a.scale_log2;
 
-  float qf[EPL];
-  if (active) {
-    load_vec<T, EPL>(static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + d0,
-                     qf);
-  } else {
+  Row qr;
+  load_row<T, EPL>(qr, static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + dl);
+  if (!active) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qf[e] = 0.f;
+    for (int w = 0; w < Row::WORDS; ++w) qr.w[w] = 0u;  // contributes 0 to every dot
   }
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) qf[e] *= a.scale_log2;
 
-  const T* kp = static_cast<const T*>(a.k) + b * a.kb + (int64_t)h * a.kh + d0;
-  const T* vp = static_cast<const T*>(a.v) + b * a.vb + (int64_t)h * a.vh + d0;
+  // wave-uniform page bases; per-lane offsets of slot u inside a trip
+  const T* kbase = static_cast<const T*>(a.k) + b * a.kb + (int64_t)h * a.kh;
+  const T* vbase = static_cast<const T*>(a.v) + b * a.vb + (int64_t)h * a.vh;
+  const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
+  int koff[U], voff[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    koff[u] = (u * KPI + grp) * kt + dl;
+    voff[u] = (u * KPI + grp) * vt + dl;
+  }
 
   float m = kNegInf, l = 0.f;
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
 
-  for (int t0 = kbeg; t0 < kend; t0 += KPI * U) {
+  Row kA[U], vA[U], kB[U], vB[U];
+  auto load_trip = [&](Row (&kr)[U], Row (&vr)[U], int t0) __attribute__((always_inline)) {
+    if (t0 + STEP <= kend) {
+      const T* kb = kbase + (int64_t)t0 * kt;
+      const T* vb = vbase + (int64_t)t0 * vt;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        load_row<T, EPL>(kr[u], kb + koff[u]);
+        load_row<T, EPL>(vr[u], vb + voff[u]);
+      }
+    } else {
+      // last, partial trip: slots wholly past kend are skipped (wave-uniform);
+      // inside the straddling slot, rows past kend re-read row kend-1 (always
+      // valid) and their scores are masked
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t0 + u * KPI >= kend) break;
+        const int t = min(t0 + u * KPI + grp, kend - 1);
+        load_row<T, EPL>(kr[u], kbase + t * kt + dl);
+        load_row<T, EPL>(vr[u], vbase + t * vt + dl);
+      }
+    }
+  };
+  auto process = [&](const Row (&kr)[U], const Row (&vr)[U], int t0) __attribute__((always_inline)) {
     float s[U];
-    float vv[U][EPL];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * KPI + grp;
-      const bool valid = t < kend;
-      float kk[EPL];
-      if (valid && active) {
-        load_vec<T, EPL>(kp + (int64_t)t * a.kt, kk);
-        load_vec<T, EPL>(vp + (int64_t)t * a.vt, vv[u]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-          kk[e] = 0.f;
-          vv[u][e] = 0.f;
-        }
-      }
-      float dot = 0.f;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) dot += qf[e] * kk[e];
-      dot = group_sum<LPK>(dot);
-      s[u] = valid ? dot : kNegInf;
+      s[u] = kNegInf;
+      if (t0 + u * KPI >= kend) continue;  // slot not loaded (wave-uniform)
+      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qr, kr[u]));
+      s[u] = (t0 + u * KPI + grp < kend) ? dot : kNegInf;
     }
-    float mloc = s[0];
+    float mt = s[0];
 #pragma unroll
-    for (int u = 1; u < U; ++u) mloc = fmaxf(mloc, s[u]);
-    const float mnew = fmaxf(m, mloc);
-    if (mnew != kNegInf) {
-      const float alpha = exp2f(m - mnew);
+    for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u]);
+    // every trip holds at least one visible key, so mt is finite
+    mt = wave_max(mt);
+    if (mt > m + a.lazy_raw) {  // wave-uniform
+      const float alpha = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - mt) * c);
+      m = mt;
       l *= alpha;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+    }
+    const float moff = m * c;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float p = exp2f(s[u] - mnew);
-        l += p;
+    for (int u = 0; u < U; ++u) {
+      if (t0 + u * KPI >= kend) continue;
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u], c, -moff));
+      l += p;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] += p * vv[u][e];
-      }
-      m = mnew;
+      for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr[u], e), acc[e]);
+    }
+  };
+
+  int t0 = kbeg;
+  if (t0 < kend) {
+    load_trip(kA, vA, t0);
+    while (true) {
+      if (t0 + STEP < kend) load_trip(kB, vB, t0 + STEP);
+      process(kA, vA, t0);
+      t0 += STEP;
+      if (t0 >= kend) break;
+      if (t0 + STEP < kend) load_trip(kA, vA, t0 + STEP);
+      process(kB, vB, t0);
+      t0 += STEP;
+      if (t0 >= kend) break;
     }
   }
 
-  // merge the KPI lane groups (xor over the group index keeps the d-slice)
+  // the KPI lane groups share m: their partials add up
+  l = sum_over_groups<LPK>(l);
 #pragma unroll
-  for (int off = LPK; off < 64; off <<= 1) {
-    const float mo = shfl_xor(m, off);
-    const float lo = shfl_xor(l, off);
-    float ao[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) ao[e] = shfl_xor(acc[e], off);
-    const float mn = fmaxf(m, mo);
-    if (mn != kNegInf) {
-      const float c1 = exp2f(m - mn), c2 = exp2f(mo - mn);
-      l = l * c1 + lo * c2;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] = acc[e] * c1 + ao[e] * c2;
-      m = mn;
-    }
-  }
+  for (int e = 0; e < EPL; ++e) acc[e] = sum_over_groups<LPK>(acc[e]);
 
   if (grp != 0 || !active) return;
   if (a.nsplit == 1) {
@@ -185,10 +295,10 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
     const float* pp = base + s * (DPAD + 2);
     const float ms = pp[DPAD];
     if (ms == kNegInf) continue;
-    const float c = exp2f(ms - M);
-    L += c * pp[DPAD + 1];
+    const float w = __builtin_amdgcn_exp2f((ms - M) * a.scale_log2);
+    L += w * pp[DPAD + 1];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += c * pp[d0 + e];
+    for (int e = 0; e < EPL; ++e) acc[e] += w * pp[d0 + e];
   }
   const float inv = 1.0f / L;
 #pragma unroll
@@ -201,7 +311,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int kUnroll = 4;        // key slots per lane group per loop trip
 constexpr int64_t kTargetWaves = 8192;  // 256 CUs x 32 resident waves
 constexpr int kMinSplitKeys = 128;
 constexpr int kMaxSplits = 64;
@@ -230,12 +339,29 @@ int pick_splits(int64_t base_units, int Tk) {
   return (int)n;
 }
 
+// Key slots per trip: 16-byte lane slices keep 4 slots (8 loads of K and V in
+// flight per register set); narrower slices take more slots per trip.
+// Key slots per trip.  16-byte lane slices: 2 slots for short rows (fewer
+// registers, more resident waves; the rows end within one or two trips) and
+// 4 for long ones (more loads in flight per wave).  Narrower slices double
+// both.
+constexpr int kShortRowKeys = 512;
+template <typename T, int EPL>
+constexpr int slots_for(bool long_rows) {
+  const int wide = EPL * (int)sizeof(T) >= 16 ? 1 : 2;
+  return (long_rows ? 4 : 2) * wide;
+}
+
 template <typename T, int DPAD, int EPL>
 int launch_attn(AttnArgs a, hipStream_t s) {
   const int64_t blocks = (a.units + 3) / 4;
   DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, kUnroll>), dim3((unsigned)blocks), dim3(256), 0,
-                     s, a);
+  if (a.split_len > kShortRowKeys)
+    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(true)>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(false)>), dim3((unsigned)blocks),
+                       dim3(256), 0, s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
   constexpr int LPK = DPAD / EPL;
@@ -297,6 +423,12 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
   DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "attention: head_dim %d > 256", D);
+  DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
+  // row offsets inside one (b, h) page are 32-bit in the kernel
+  const int64_t span_k = (int64_t)Tk * (k_st->t < 0 ? -k_st->t : k_st->t);
+  const int64_t span_v = (int64_t)Tk * (v_st->t < 0 ? -v_st->t : v_st->t);
+  DG_REQUIRE(span_k < ((int64_t)1 << 31) && span_v < ((int64_t)1 << 31) && k_st->t >= 0 && v_st->t >= 0,
+             DG_EINVAL, "attention: Tk * key/value row stride must be below 2^31 elements");
   int pref = 16 / es;
   if (pref > dpad) pref = dpad;
   auto fits = [&](int epl) {
@@ -322,6 +454,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.H = H; a.Tq = Tq; a.Tk = Tk; a.D = D;
   a.q_offset = Tk - Tq;
   a.scale_log2 = scale * 1.44269504088896340736f;
+  a.lazy_raw = kVecLazyLog2 / a.scale_log2;
 
   int ns = vec_attention_splits(B, H, Tq, Tk, D);
   const size_t need = vec_attention_workspace(B, H, Tq, Tk, D);
@@ -335,6 +468,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.part = ns == 1 ? nullptr : static_cast<float*>(workspace);
   DG_REQUIRE(ns == 1 || aligned(workspace, 16), DG_EINVAL, "attention: workspace must be 16-byte aligned");
   a.units = (int64_t)B * H * Tq * ns;
+  DG_REQUIRE(a.units < ((int64_t)1 << 31), DG_EINVAL, "attention: B*H*Tq*splits must be below 2^31");
 
   if (dtype == DG_F32) return attn_pick_d<float>(dpad, epl, a, s);
   if (dtype == DG_BF16) return attn_pick_d<bf16_t>(dpad, epl, a, s);

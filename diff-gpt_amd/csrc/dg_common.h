@@ -154,6 +154,97 @@ __device__ __forceinline__ float group_sum(float v) {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
+// ---------------------------------------------------------------------------
+// Register-only cross-lane sums (no LDS traffic): DPP quad permutes and row
+// mirrors inside a 16-lane row, v_permlane16/32_swap across rows.  The
+// pairings are those of group_sum (partner = lane ^ 1, ^ 2, then the other
+// half of each 8-, 16-, 32- and 64-lane group), every pair adds the same two
+// values in both lanes, so all G lanes of a group end with identical bits.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i inside each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i inside each 16
+
+// {own value, value of the partner row / half} in some order (which one comes
+// first depends on the lane); combine them with a commutative operation.
+__device__ __forceinline__ void pair16(float x, float& a, float& b) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float x, float& a, float& b) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+constexpr int kDppRowRor4 = 0x124;    // rotate each 16-lane row by 4
+constexpr int kDppRowRor8 = 0x128;    // rotate each 16-lane row by 8
+
+// Maximum over the 64 lanes of the wave (identical in every lane).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<kDppQuadXor1>(v));
+  v = fmaxf(v, dpp<kDppQuadXor2>(v));
+  v = fmaxf(v, dpp<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp<kDppMirror>(v));
+  float a, b;
+  pair16(v, a, b);
+  v = fmaxf(a, b);
+  pair32(v, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum over the 64/LPK groups of LPK consecutive lanes, element-wise for lanes
+// of equal index inside their group (lane offsets that are multiples of
+// LPK).  Every lane receives the full sum; the addition order may differ
+// between lanes of one group, so only one group's result should be used.
+template <int LPK>
+__device__ __forceinline__ float sum_over_groups(float v) {
+  static_assert(LPK >= 1 && LPK <= 64 && (LPK & (LPK - 1)) == 0, "group size");
+  if constexpr (LPK <= 1) v = v + dpp<kDppQuadXor1>(v);
+  if constexpr (LPK <= 2) v = v + dpp<kDppQuadXor2>(v);
+  if constexpr (LPK <= 4) v = v + dpp<kDppRowRor4>(v);
+  if constexpr (LPK <= 8) v = v + dpp<kDppRowRor8>(v);
+  if constexpr (LPK <= 16) {
+    float a, b;
+    pair16(v, a, b);
+    v = a + b;
+  }
+  if constexpr (LPK <= 32) {
+    float a, b;
+    pair32(v, a, b);
+    v = a + b;
+  }
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum_dpp(float v) {
+  static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group size");
+  if constexpr (G >= 2) v = v + dpp<kDppQuadXor1>(v);
+  if constexpr (G >= 4) v = v + dpp<kDppQuadXor2>(v);
+  if constexpr (G >= 8) v = v + dpp<kDppHalfMirror>(v);
+  if constexpr (G >= 16) v = v + dpp<kDppMirror>(v);
+  if constexpr (G >= 32) {
+    float a, b;
+    pair16(v, a, b);
+    v = a + b;
+  }
+  if constexpr (G >= 64) {
+    float a, b;
+    pair32(v, a, b);
+    v = a + b;
+  }
+  return v;
+}
+
 }  // namespace dg
 
 // ---------------------------------------------------------------------------
