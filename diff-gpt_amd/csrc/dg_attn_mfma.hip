@@ -150,8 +150,16 @@ struct PrefillCfg {
   static_assert(VBPT >= 1 && (kBN * D / 16) % 256 == 0, "V tile mapping");
 };
 
+// Resident workgroups per CU the register allocation must allow: D = 64 fits
+// 4 (LDS 35 KB each, <= 128 VGPRs -> 4 waves per SIMD to overlap one wave's
+// MFMAs with another's softmax); D = 128 is LDS-limited to 2.
+template <int D>
+constexpr int prefill_wgs_per_cu() {
+  return D == 64 ? 4 : 2;
+}
+
 template <typename T, int D, int QW>
-__global__ __launch_bounds__(256) void prefill_mfma_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(256, prefill_wgs_per_cu<D>()) void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
   using C = PrefillCfg<T, D, QW>;
