@@ -48,7 +48,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def decode_job(dtype_name: str, steps: int, warmup: int):
+def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
     import torch
 
     from diff_gpt import _native
@@ -99,12 +99,15 @@ def decode_job(dtype_name: str, steps: int, warmup: int):
                          _native._ptr(fc), P(_native.Stride3(0, 0, 0)), code, _native.DG_QKNORM, stream)
             ws = lib.dg_attention_workspace_size(B, H, 1, t0 + 1, D, code)
             assert ws == 0, "configs[1] decode runs without key splits"
+            # shared: the 96-token prefix of each series is read from the
+            # series' first row (all 100 rows hold it, KVCache.prefill)
+            prefix, group = (PREFIX, TRAJ) if shared else (0, 1)
             attn_args = (B, H, 1, t0 + 1, D, code,
                          _native._ptr(q_rot), P(S3(q_rot)), _native._ptr(keys), P(S3(keys)),
                          _native._ptr(vals), P(S3(vals)), _native._ptr(y), P(S3(y)),
-                         0.25, None, 0, stream)
+                         0.25, prefix, group, None, 0, stream)
             packs.append((rope_args, attn_args))
-    rope_fn, attn_fn = lib.dg_rope_qknorm_append, lib.dg_attention
+    rope_fn, attn_fn = lib.dg_rope_qknorm_append, lib.dg_attention_grouped
 
     ev = []  # (start, end) events around each decode-attention launch
 
@@ -137,7 +140,13 @@ def decode_job(dtype_name: str, steps: int, warmup: int):
     launches = len(kern_ms)
     mean_kernel_s = sum(kern_ms) / launches / 1e3
     # algorithmic bytes per launch, averaged over the job's L_kv = 97..144
-    bytes_job = sum(B * H * es * (2 * (PREFIX + s + 1) * D + 2 * D) for s in range(NEW)) * L
+    # algorithmic bytes per launch: K+V rows of every visible position, q, y;
+    # with a shared prefix the prefix rows count once per series (unique bytes)
+    if shared:
+        bytes_job = sum(H * es * (2 * D * (PREFIX * SERIES + (s + 1) * B) + 2 * D * B)
+                        for s in range(NEW)) * L
+    else:
+        bytes_job = sum(B * H * es * (2 * (PREFIX + s + 1) * D + 2 * D) for s in range(NEW)) * L
     bytes_per_launch = bytes_job / (NEW * L)
     achieved = bytes_per_launch / mean_kernel_s / 1e9
     tokens = B * NEW * steps
@@ -265,6 +274,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--traffic-json", default=str(REPO / "profiles" / "decode_attn_cfg1_traffic.json"))
     ap.add_argument("--single-dtype", action="store_true", help="skip the other-dtype decode leg")
+    ap.add_argument("--decode-mode", default="shared", choices=["shared", "plain"],
+                    help="shared: each series' prefix is read from its first row (what KVCache.prefill "
+                         "+ MultiHeadAttention do); plain: every row reads its own copy")
+    ap.add_argument("--single-mode", action="store_true", help="skip the other decode-mode leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -278,18 +291,23 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
     if args.calib_copy:
         calib_copy()
-    res = decode_job(args.dtype, args.steps, args.warmup)
-    log(f"decode: {res}")
+    shared = args.decode_mode == "shared"
+    res = decode_job(args.dtype, args.steps, args.warmup, shared)
+    log(f"decode {args.dtype} {args.decode_mode}: {res}")
+    res_mode = None
+    if not args.single_mode:
+        res_mode = decode_job(args.dtype, max(1, args.steps // 2), 1, not shared)
+        log(f"decode {args.dtype} {'plain' if shared else 'shared'}: {res_mode}")
     other = "bf16" if args.dtype == "fp32" else "fp32"
     res_other = None
     if not args.single_dtype:
-        res_other = decode_job(other, max(1, args.steps // 2), 1)
-        log(f"decode {other}: {res_other}")
+        res_other = decode_job(other, max(1, args.steps // 2), 1, shared)
+        log(f"decode {other} {args.decode_mode}: {res_other}")
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():
         tj = json.loads(tp.read_text())
-        traffic = tj.get(args.dtype)
+        traffic = tj.get(args.dtype + ("_shared" if shared else ""))
     roof = {
         "bound": "hbm",
         "achieved": res["achieved_gbs"],
@@ -327,8 +345,14 @@ def main():
         "cpu_baseline": cpu,
         "decode_kernel": {"mean_us": res["kernel_mean_us"], "bytes_per_launch": res["bytes_per_launch"],
                           "attn_only_tokens_per_s": res["attn_only_tokens_per_s"]},
+        "decode_mode": args.decode_mode,
+        "decode_other_mode": None if res_mode is None else {
+            "mode": "plain" if shared else "shared", "tokens_per_s": res_mode["tokens_per_s"],
+            "kernel_mean_us": res_mode["kernel_mean_us"],
+            "achieved_gbs": res_mode["achieved_gbs"], "frac": res_mode["achieved_gbs"] / HBM_PEAK_GBS},
         "decode_other_dtype": None if res_other is None else {
             "dtype": other, "tokens_per_s": res_other["tokens_per_s"],
+            "kernel_mean_us": res_other["kernel_mean_us"],
             "achieved_gbs": res_other["achieved_gbs"],
             "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill": prefill,

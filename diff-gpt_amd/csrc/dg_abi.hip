@@ -31,7 +31,8 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D);
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  void* workspace, size_t workspace_bytes, hipStream_t s);
+                  int prefix_len, int group, void* workspace, size_t workspace_bytes,
+                  hipStream_t s);
 // dg_attn_mfma.hip
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
@@ -85,23 +86,38 @@ extern "C" size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int 
   return vec_attention_workspace(B, H, Tq, Tk, D);
 }
 
+extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                                    const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
+                                    const void* v, const dg_stride3* v_st, void* y,
+                                    const dg_stride3* y_st, float scale, int prefix_len, int group,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  DG_REQUIRE(B >= 0 && H >= 0 && Tq >= 0 && Tk >= 0, DG_EINVAL, "attention: negative size");
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "attention: dtype %d unsupported", dtype);
+  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention: head_dim must be even (got %d)", D);
+  DG_REQUIRE(group >= 1, DG_EINVAL, "attention: group must be >= 1 (got %d)", group);
+  DG_REQUIRE(prefix_len >= 0 && prefix_len <= Tk, DG_EINVAL,
+             "attention: prefix_len %d outside [0, Tk=%d]", prefix_len, Tk);
+  if ((int64_t)B * H * Tq == 0) return DG_OK;
+  DG_REQUIRE(Tk >= Tq, DG_EINVAL, "attention: Tk (%d) < Tq (%d)", Tk, Tq);
+  DG_REQUIRE(q && k && v && y && q_st && k_st && v_st && y_st, DG_EINVAL, "attention: NULL argument");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The MFMA prefill kernel reads every row's own keys: equal results, since
+  // the rows of a group hold identical prefixes.
+  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
+    return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
+  if (group == 1) prefix_len = 0;
+  return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
+                       group, workspace, workspace_bytes, s);
+}
+
 extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                             const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                             const void* v, const dg_stride3* v_st, void* y,
                             const dg_stride3* y_st, float scale, void* workspace,
                             size_t workspace_bytes, void* stream) {
-  DG_REQUIRE(B >= 0 && H >= 0 && Tq >= 0 && Tk >= 0, DG_EINVAL, "attention: negative size");
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
-             "attention: dtype %d unsupported", dtype);
-  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention: head_dim must be even (got %d)", D);
-  if ((int64_t)B * H * Tq == 0) return DG_OK;
-  DG_REQUIRE(Tk >= Tq, DG_EINVAL, "attention: Tk (%d) < Tq (%d)", Tk, Tq);
-  DG_REQUIRE(q && k && v && y && q_st && k_st && v_st && y_st, DG_EINVAL, "attention: NULL argument");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
-    return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
-  return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, workspace,
-                       workspace_bytes, s);
+  return dg_attention_grouped(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, 0, 1,
+                              workspace, workspace_bytes, stream);
 }
 
 extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const int64_t* src_st,

@@ -42,6 +42,8 @@ struct AttnArgs {
   int H, Tq, Tk, D;
   int q_offset;  // Tk - Tq: query i sees keys j <= i + q_offset
   int nsplit, split_len;
+  int prefix_len;    // keys j < prefix_len of row b are read from row (b / group) * group
+  int group;
   float scale_log2;  // scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2
 };
@@ -129,8 +131,12 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   using Row = RowRegs<T, EPL>;
 
   const int lane = threadIdx.x & 63;
+  // Consecutive blocks (rows of one group, heads of one row) go to one XCD:
+  // workgroups are dealt round-robin over the 8 XCDs, each with its own L2.
+  int blk = blockIdx.x;
+  if ((gridDim.x & 7) == 0) blk = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   // wave-uniform unit index (the host keeps units below 2^31)
-  const int unit = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int unit = blk * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (unit >= a.units) return;  // whole wave exits; kernel has no barriers
 
   const int sub = lane % LPK;
@@ -161,6 +167,11 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   // wave-uniform page bases; per-lane offsets of slot u inside a trip
   const T* kbase = static_cast<const T*>(a.k) + b * a.kb + (int64_t)h * a.kh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.vb + (int64_t)h * a.vh;
+  // shared prefix: keys below prefix_len come from the group's first row
+  const int64_t b0 = (b / a.group) * a.group;
+  const T* kpre = static_cast<const T*>(a.k) + b0 * a.kb + (int64_t)h * a.kh;
+  const T* vpre = static_cast<const T*>(a.v) + b0 * a.vb + (int64_t)h * a.vh;
+  const int P = a.prefix_len;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
   int koff[U], voff[U];
 #pragma unroll
@@ -176,24 +187,28 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
 
   Row kA[U], vA[U], kB[U], vB[U];
   auto load_trip = [&](Row (&kr)[U], Row (&vr)[U], int t0) __attribute__((always_inline)) {
-    if (t0 + STEP <= kend) {
-      const T* kb = kbase + (int64_t)t0 * kt;
-      const T* vb = vbase + (int64_t)t0 * vt;
+    if (t0 + STEP <= kend && (t0 >= P || t0 + STEP <= P)) {
+      // full trip inside one source page (own rows, or the shared prefix)
+      const bool pre = t0 < P;
+      const T* kb = (pre ? kpre : kbase) + (int64_t)t0 * kt;
+      const T* vb = (pre ? vpre : vbase) + (int64_t)t0 * vt;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         load_row<T, EPL>(kr[u], kb + koff[u]);
         load_row<T, EPL>(vr[u], vb + voff[u]);
       }
     } else {
-      // last, partial trip: slots wholly past kend are skipped (wave-uniform);
-      // inside the straddling slot, rows past kend re-read row kend-1 (always
-      // valid) and their scores are masked
+      // trip straddling the end of the prefix or the end of the keys: slots
+      // wholly past kend are skipped (wave-uniform); inside the last slot,
+      // rows past kend re-read row kend-1 (always valid) and their scores
+      // are masked
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (t0 + u * KPI >= kend) break;
         const int t = min(t0 + u * KPI + grp, kend - 1);
-        load_row<T, EPL>(kr[u], kbase + t * kt + dl);
-        load_row<T, EPL>(vr[u], vbase + t * vt + dl);
+        const bool pre = t < P;
+        load_row<T, EPL>(kr[u], (pre ? kpre : kbase) + t * kt + dl);
+        load_row<T, EPL>(vr[u], (pre ? vpre : vbase) + t * vt + dl);
       }
     }
   };
@@ -419,7 +434,8 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  void* workspace, size_t workspace_bytes, hipStream_t s) {
+                  int prefix_len, int group, void* workspace, size_t workspace_bytes,
+                  hipStream_t s) {
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
   DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "attention: head_dim %d > 256", D);
@@ -455,6 +471,8 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.q_offset = Tk - Tq;
   a.scale_log2 = scale * 1.44269504088896340736f;
   a.lazy_raw = kVecLazyLog2 / a.scale_log2;
+  a.prefix_len = prefix_len;
+  a.group = group;
 
   int ns = vec_attention_splits(B, H, Tq, Tk, D);
   const size_t need = vec_attention_workspace(B, H, Tq, Tk, D);

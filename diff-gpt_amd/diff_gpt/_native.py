@@ -55,6 +55,13 @@ _SIGNATURES = {
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4
         + [ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
+    "dg_attention_grouped": (
+        ctypes.c_int,
+        [ctypes.c_int] * 6
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4
+        + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+           ctypes.c_void_p],
+    ),
     "dg_rms_norm": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
@@ -212,8 +219,10 @@ def rope_qknorm_append_(
 
 
 def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
-               scale: float) -> None:
-    """dg_attention: q,y (B,Tq,H,D) views; k,v (B,Tk,H,D) views."""
+               scale: float, prefix_len: int = 0, group: int = 1) -> None:
+    """dg_attention_grouped: q,y (B,Tq,H,D) views; k,v (B,Tk,H,D) views.  With
+    group > 1 the first prefix_len keys of row b are read from row
+    (b // group) * group (rows of a group must hold identical prefixes)."""
     B, Tq, H, D = q.shape
     Tk = k.size(1)
     if k.shape != (B, Tk, H, D) or v.shape != (B, Tk, H, D) or y.shape != q.shape:
@@ -224,13 +233,13 @@ def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tenso
     L = lib()
     ws_bytes = L.dg_attention_workspace_size(B, H, Tq, Tk, D, code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
-    rc = L.dg_attention(
+    rc = L.dg_attention_grouped(
         B, H, Tq, Tk, D, code,
         _ptr(q), ctypes.pointer(_bthd_strides(q)),
         _ptr(k), ctypes.pointer(_bthd_strides(k)),
         _ptr(v), ctypes.pointer(_bthd_strides(v)),
         _ptr(y), ctypes.pointer(_bthd_strides(y)),
-        float(scale), _ptr(ws), ws_bytes, _stream(q),
+        float(scale), int(prefix_len), int(group), _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "attention")
 
@@ -273,7 +282,9 @@ _DEF.define(
     "rope_qknorm_append(Tensor? q, Tensor? k, Tensor? v, Tensor freqs, Tensor(a!)? q_out, "
     "Tensor(b!)? k_out, Tensor(c!)? v_out, bool qknorm) -> ()"
 )
-_DEF.define("attention(Tensor q, Tensor k, Tensor v, float scale) -> Tensor")
+_DEF.define(
+    "attention(Tensor q, Tensor k, Tensor v, float scale, int prefix_len=0, int group=1) -> Tensor"
+)
 _DEF.define("rms_norm(Tensor x) -> Tensor")
 _DEF.define("rope(Tensor x, Tensor freqs) -> Tensor")
 _DEF.define("copy4d(Tensor src, Tensor(a!) dst) -> ()")
@@ -281,9 +292,9 @@ _DEF.define("copy4d(Tensor src, Tensor(a!) dst) -> ()")
 _IMPL = torch.library.Library("dgattn", "IMPL")
 
 
-def _attention_impl(q, k, v, scale):
+def _attention_impl(q, k, v, scale, prefix_len=0, group=1):
     y = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    attention_(q, k, v, y, scale)
+    attention_(q, k, v, y, scale, prefix_len, group)
     return y
 
 
@@ -321,7 +332,7 @@ _IMPL.impl("rms_norm", _rms_norm_impl, "CUDA")
 _IMPL.impl("rope", _rope_impl, "CUDA")
 _IMPL.impl("copy4d", copy4d_, "CUDA")
 
-_IMPL.impl("attention", lambda q, k, v, scale: torch.empty_like(q), "Meta")
+_IMPL.impl("attention", lambda q, k, v, scale, prefix_len=0, group=1: torch.empty_like(q), "Meta")
 _IMPL.impl("rms_norm", lambda x: torch.empty_like(x), "Meta")
 _IMPL.impl("rope", lambda x, freqs: torch.empty_like(x), "Meta")
 

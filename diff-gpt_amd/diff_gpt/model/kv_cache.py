@@ -39,6 +39,7 @@ class KVCache:
         "kv_shape",
         "kv_cache",
         "pos",
+        "shared_prefix",
     )
 
     def __init__(
@@ -52,9 +53,15 @@ class KVCache:
         self.kv_shape = (num_layers, 2, batch_size, num_heads, seq_len, head_dim)
         self.kv_cache = torch.zeros(0)
         self.pos = 0
+        # (length, group) when rows come in groups of `group` consecutive rows
+        # whose first `length` positions are identical (a batch-broadcast
+        # prefill); decode attention then reads that prefix from the group's
+        # first row only.  None otherwise.
+        self.shared_prefix: tuple[int, int] | None = None
 
     def reset(self) -> None:
         self.pos = 0
+        self.shared_prefix = None
 
     def get_pos(self) -> int:
         return self.pos
@@ -85,6 +92,7 @@ class KVCache:
                 src4 = src4.expand(dst4.shape)  # batch broadcast: 0 stride on B
             _native.ops().copy4d(src4, dst4)
         self.pos = n
+        self.shared_prefix = (n, sb) if (ob == 1 and sb > 1 and n > 0) else None
 
     # -- capacity management shared by insert_kv and the fused MHA path --
     def ensure_window(
@@ -95,6 +103,9 @@ class KVCache:
             _native.require_device_type("KVCache", device)
             self.kv_cache = torch.empty(self.kv_shape, dtype=dtype, device=device)
         t0, t1 = self.pos, self.pos + T_add
+        if self.shared_prefix is not None and t0 < self.shared_prefix[0]:
+            # rows diverge from position t0 on: only the part before it stays shared
+            self.shared_prefix = (t0, self.shared_prefix[1]) if t0 > 0 else None
         cap = self.kv_cache.size(4)
         if t1 > cap:
             new_cap = _grown_capacity(t1)

@@ -82,9 +82,12 @@ class MultiHeadAttention(nn.Module):
             k_all, v_all = kv_cache.layer_views(self.layer_idx, t1)
             keys, values = k_all.transpose(1, 2), v_all.transpose(1, 2)
             kv_cache.advance(self.layer_idx, t1)
+            shared = kv_cache.shared_prefix
 
-        # SDPA default scale 1/sqrt(head_dim); the mask follows from Tq vs Tk
-        y = ops.attention(q_rot, keys, values, 1.0 / math.sqrt(D))
+        # SDPA default scale 1/sqrt(head_dim); the mask follows from Tq vs Tk.
+        # A broadcast prefix (KVCache.prefill) is read once per row group.
+        prefix_len, group = (0, 1) if kv_cache is None or shared is None else shared
+        y = ops.attention(q_rot, keys, values, 1.0 / math.sqrt(D), prefix_len, group)
         y = y.view(B, T, H * D)
         y = y * torch.sigmoid(g)
         return self.c_proj(y)

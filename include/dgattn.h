@@ -120,6 +120,26 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * dg_attention over a batch whose rows come in groups sharing a prefix: for
+ * row b, keys j < prefix_len are read from row (b / group) * group of k and v
+ * instead of row b; keys j >= prefix_len from row b itself.  This is the
+ * decode attention of mha.py:65-68 over the cache that KVCache.prefill's
+ * batch broadcast (kv_cache.py:77-79) leaves behind: every row of a group
+ * holds the same first prefix_len positions, so the result is exactly
+ * dg_attention's, while the prefix is fetched from HBM about once per group
+ * (rows of one group run on one XCD and hit its L2).  The caller guarantees
+ * the identical prefixes.  group = 1 (or prefix_len = 0) is dg_attention.
+ * Prefill launches that take the MFMA kernel read every row's own keys.
+ */
+DG_API int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype,
+                                const void* q, const dg_stride3* q_st,
+                                const void* k, const dg_stride3* k_st,
+                                const void* v, const dg_stride3* v_st,
+                                void* y, const dg_stride3* y_st, float scale,
+                                int prefix_len, int group,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with
  * eps=None, i.e. FLT_EPSILON, computed in fp32 and rounded once to dtype).
  * x and out are M rows of N elements with row strides x_ld / out_ld.

@@ -18,7 +18,8 @@ def _declared_symbols():
 def test_header_declares_the_entry_points():
     syms = _declared_symbols()
     assert {"dg_abi_version", "dg_last_error", "dg_rope_qknorm_append", "dg_attention",
-            "dg_attention_workspace_size", "dg_rms_norm", "dg_copy4d"} <= set(syms)
+            "dg_attention_grouped", "dg_attention_workspace_size", "dg_rms_norm",
+            "dg_copy4d"} <= set(syms)
 
 
 def test_library_exports_every_declared_symbol():
@@ -57,6 +58,13 @@ def test_argument_errors_return_status_and_message():
     # rms_norm row too long
     rc = lib.dg_rms_norm(1, 10000, 0, fake, 10000, fake, 10000, nul)
     assert rc == -2
+    # grouped attention: group < 1 and a prefix longer than the keys
+    rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake,
+                                  _s3(), 1.0, 4, 0, nul, 0, nul)
+    assert rc == -1 and b"group" in lib.dg_last_error()
+    rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake,
+                                  _s3(), 1.0, 9, 2, nul, 0, nul)
+    assert rc == -1 and b"prefix_len" in lib.dg_last_error()
     # empty work is a no-op success
     assert lib.dg_attention(0, 1, 1, 1, 16, 0, nul, _s3(), nul, _s3(), nul, _s3(), nul, _s3(),
                             1.0, nul, 0, nul) == 0

@@ -185,6 +185,43 @@ def test_decode_without_workspace_matches_split(dev):
         assert err <= 2e-2
 
 
+GROUPED = [  # (B, group, H, prefix, Tk, D): cfg1 series of 100 rows, ragged last group
+    (300, 100, 4, 96, 144, 16),
+    (10, 4, 2, 33, 70, 16),
+    (12, 6, 8, 600, 1100, 64),
+    (4, 2, 8, 1500, 2600, 128),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", GROUPED, ids=lambda s: "x".join(map(str, s)))
+def test_grouped_prefix_attention_equals_plain(dev, dtype, shape):
+    """Rows of a group share their first `prefix` cache positions (a broadcast
+    prefill, kv_cache.py:77-79): reading the prefix from the group's first row
+    gives the very bits of the plain decode, and both match fp64."""
+    from diff_gpt import _native
+
+    B, G, H, P, Tk, D = shape
+    cap = Tk + 3
+    groups = (B + G - 1) // G
+    pre = _randn((groups, 2, H, P, D), 70 + D, dtype)
+    own = _randn((B, 2, H, Tk - P, D), 71 + D, dtype)
+    cache = torch.empty((2, B, H, cap, D), dtype=TDT[dtype])
+    cache[:, :, :, :P] = pre.repeat_interleave(G, dim=0)[:B].transpose(0, 1)
+    cache[:, :, :, P:Tk] = own.transpose(0, 1)
+    q = _randn((B, 1, H, D), 72 + D, dtype)
+    cd, qd = cache.to(dev), q.to(dev)
+    keys = cd[0, :, :, :Tk].transpose(1, 2)
+    vals = cd[1, :, :, :Tk].transpose(1, 2)
+    ops = _native.ops()
+    y_plain = ops.attention(qd, keys, vals, 1.0 / np.sqrt(D))
+    y_grp = ops.attention(qd, keys, vals, 1.0 / np.sqrt(D), P, G)
+    assert torch.equal(y_grp, y_plain)
+    ref = on.attention_f64(q.float().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy())
+    err = np.abs(y_grp.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= TOL[dtype], err
+
+
 # ------------------------------------------------------------------ strided copy
 
 

@@ -129,6 +129,30 @@ def test_kv_cache_prefill_broadcast_and_reset(dev):
     assert torch.equal(out_k, one)
 
 
+def test_kv_cache_shared_prefix_bookkeeping(dev):
+    """A batch-1 -> N prefill records the shared prefix (read once per group by
+    decode attention); an insert below it shrinks it, reset() clears it."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    src = KVCache(1, 2, 10, 4, 1)
+    k = torch.randn(1, 2, 5, 4, device=dev)
+    src.insert_kv(0, k, k)
+    dst = KVCache(3, 2, 20, 4, 1)
+    dst.prefill(src)
+    assert dst.shared_prefix == (5, 3)
+    step = torch.randn(3, 2, 1, 4, device=dev)
+    dst.insert_kv(0, step, step)  # decode step at position 5: prefix untouched
+    assert dst.shared_prefix == (5, 3) and dst.get_pos() == 6
+    dst.pos = 2  # a rewind (as after a partial reset) makes rows diverge from 2 on
+    dst.insert_kv(0, step, step)
+    assert dst.shared_prefix == (2, 3)
+    dst.reset()
+    assert dst.shared_prefix is None
+    same = KVCache(1, 2, 20, 4, 1)  # batch 1 -> 1: nothing to share
+    same.prefill(src)
+    assert same.shared_prefix is None
+
+
 # ------------------------------------------------------------------ MHA (test_mha.py)
 
 
