@@ -31,8 +31,8 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D);
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  int prefix_len, int group, void* workspace, size_t workspace_bytes,
-                  hipStream_t s);
+                  int prefix_len, int group, const int* pos_dev, void* workspace,
+                  size_t workspace_bytes, hipStream_t s);
 // dg_attn_mfma.hip
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
@@ -108,7 +108,37 @@ extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dty
     return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
   if (group == 1) prefix_len = 0;
   return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
-                       group, workspace, workspace_bytes, s);
+                       group, nullptr, workspace, workspace_bytes, s);
+}
+
+extern "C" size_t dg_decode_attention_at_workspace_size(int B, int H, int max_keys, int D, int dtype) {
+  return dg_attention_workspace_size(B, H, 1, max_keys, D, dtype);
+}
+
+extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void* q,
+                                      const dg_stride3* q_st, const void* k_cache,
+                                      const dg_stride3* kc_st, const void* v_cache,
+                                      const dg_stride3* vc_st, void* y, const dg_stride3* y_st,
+                                      float scale, int prefix_len, int group, const int32_t* pos,
+                                      int max_keys, void* workspace, size_t workspace_bytes,
+                                      void* stream) {
+  DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "attention_at: negative size");
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "attention_at: dtype %d unsupported", dtype);
+  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention_at: head_dim must be even (got %d)", D);
+  DG_REQUIRE(max_keys >= 1, DG_EINVAL, "attention_at: max_keys must be >= 1 (got %d)", max_keys);
+  DG_REQUIRE(group >= 1, DG_EINVAL, "attention_at: group must be >= 1 (got %d)", group);
+  DG_REQUIRE(prefix_len >= 0 && prefix_len <= max_keys, DG_EINVAL,
+             "attention_at: prefix_len %d outside [0, max_keys=%d]", prefix_len, max_keys);
+  if ((int64_t)B * H == 0) return DG_OK;
+  DG_REQUIRE(pos && q && k_cache && v_cache && y && q_st && kc_st && vc_st && y_st, DG_EINVAL,
+             "attention_at: NULL argument");
+  if (group == 1) prefix_len = 0;
+  // The kernel reads at most max_keys keys (Tk = min(*pos + 1, max_keys)); key
+  // splits and the workspace are sized for max_keys.
+  return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
+                       scale, prefix_len, group, pos, workspace, workspace_bytes,
+                       static_cast<hipStream_t>(stream));
 }
 
 extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,

@@ -46,6 +46,10 @@ struct AttnArgs {
   int group;
   float scale_log2;  // scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2
+  // Decode-step form (graph-replayable, Tq == 1): when pos_dev is set, the
+  // keys are positions 0 .. *pos_dev (the token of this step was appended at
+  // *pos_dev), at most Tk of them; split_len follows from that count.
+  const int* pos_dev;
 };
 
 constexpr float kVecLazyLog2 = 8.0f;
@@ -152,9 +156,15 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
   const int dl = active ? d0 : 0;  // inactive lanes (D not a power of two) read a valid slice
-  const int kvis = min(a.Tk, i + a.q_offset + 1);
-  const int kbeg = split * a.split_len;
-  const int kend = min(kvis, kbeg + a.split_len);
+  int Tk = a.Tk, q_offset = a.q_offset, split_len = a.split_len;
+  if (a.pos_dev != nullptr) {  // uniform over the grid
+    Tk = min(*a.pos_dev + 1, a.Tk);
+    q_offset = Tk - 1;
+    split_len = a.nsplit == 1 ? Tk : (((Tk + a.nsplit - 1) / a.nsplit + 15) / 16) * 16;
+  }
+  const int kvis = min(Tk, i + q_offset + 1);
+  const int kbeg = split * split_len;
+  const int kend = min(kvis, kbeg + split_len);
   const float c = a.scale_log2;
 
   Row qr;
@@ -434,8 +444,8 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  int prefix_len, int group, void* workspace, size_t workspace_bytes,
-                  hipStream_t s) {
+                  int prefix_len, int group, const int* pos_dev, void* workspace,
+                  size_t workspace_bytes, hipStream_t s) {
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
   DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "attention: head_dim %d > 256", D);
@@ -473,6 +483,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.lazy_raw = kVecLazyLog2 / a.scale_log2;
   a.prefix_len = prefix_len;
   a.group = group;
+  a.pos_dev = pos_dev;
 
   int ns = vec_attention_splits(B, H, Tq, Tk, D);
   const size_t need = vec_attention_workspace(B, H, Tq, Tk, D);

@@ -33,6 +33,14 @@ struct RopeArgs {
   int64_t rows;  // B*T*H
   int T, H, D;
   int qknorm;
+  // Decode-step form (graph-replayable): when pos_dev is set, the number of
+  // positions already cached is read on the device; destinations advance by
+  // pstep[w] and the table by fpos elements per position.  Positions outside
+  // [0, max_pos) write nothing.
+  const int* pos_dev;
+  int max_pos;
+  int64_t pstep[3];
+  int64_t fpos;
 };
 
 // One row (b,t,h) of D elements is owned by LPK = DPAD/EPL consecutive lanes,
@@ -49,6 +57,11 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
   const int sub = threadIdx.x % LPK;
   const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / LPK;
   if (row >= a.rows) return;  // a whole lane group leaves together; no barriers follow
+  int64_t pos = 0;
+  if (a.pos_dev != nullptr) {  // uniform over the grid
+    pos = *a.pos_dev;
+    if (pos < 0 || pos >= a.max_pos) return;
+  }
 
   const int h = (int)(row % a.H);
   const int64_t bt = row / a.H;
@@ -59,7 +72,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
 
   float cs[EPL];  // (cos, sin) of the EPL/2 pairs of this lane, interleaved
   if (active) {
-    const FT* f = static_cast<const FT*>(a.freqs) + b * a.fb + (int64_t)t * a.ft +
+    const FT* f = static_cast<const FT*>(a.freqs) + pos * a.fpos + b * a.fb + (int64_t)t * a.ft +
                   (int64_t)h * a.fh + d0;
     load_vec<FT, EPL>(f, cs);
   }
@@ -100,7 +113,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
       }
     }
     if (active) {
-      T* d = static_cast<T*>(a.dst[w]) + b * a.db[w] + (int64_t)t * a.dt[w] +
+      T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + b * a.db[w] + (int64_t)t * a.dt[w] +
              (int64_t)h * a.dh[w] + d0;
       store_vec<T, EPL>(d, x);
     }
@@ -262,14 +275,16 @@ int rms_pick(int npad, const RowNormArgs& a, hipStream_t s) {
 
 using namespace dg;
 
-extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, const void* q,
-                                     const dg_stride3* q_st, void* q_out, const dg_stride3* qo_st,
-                                     const void* k, const dg_stride3* k_st, void* k_out,
-                                     const dg_stride3* ko_st, const void* v,
-                                     const dg_stride3* v_st, void* v_out,
-                                     const dg_stride3* vo_st, const void* freqs,
-                                     const dg_stride3* f_st, int freqs_dtype, int flags,
-                                     void* stream) {
+namespace dg {
+namespace {
+
+// Shared body of the two RoPE entry points; pos_dev == nullptr is the plain form.
+int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_stride3* q_st,
+               void* q_out, const dg_stride3* qo_st, const void* k, const dg_stride3* k_st,
+               void* k_out, const dg_stride3* ko_st, const void* v, const dg_stride3* v_st,
+               void* v_out, const dg_stride3* vo_st, const void* freqs, const dg_stride3* f_st,
+               int freqs_dtype, int flags, const int32_t* pos_dev, int max_pos,
+               const int64_t (&pstep)[3], int64_t fpos, void* stream) {
   DG_REQUIRE(B >= 0 && T >= 0 && H >= 0, DG_EINVAL, "rope: negative size");
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "rope: head_dim must be even and >= 2 (got %d)", D);
   DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
@@ -311,9 +326,11 @@ extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, cons
       if (!src[w]) continue;
       if (!aligned(src[w], (int64_t)epl * es) || !aligned(dst[w], (int64_t)epl * es)) return false;
       if (!strides_multiple(sst[w], epl) || !strides_multiple(dst_st[w], epl)) return false;
+      if (pstep[w] % epl != 0) return false;
     }
     if (need_freqs) {
       if (!aligned(freqs, (int64_t)epl * fes) || !strides_multiple(f_st, epl)) return false;
+      if (fpos % epl != 0) return false;
     }
     return true;
   };
@@ -339,6 +356,10 @@ extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, cons
   a.H = H;
   a.D = D;
   a.qknorm = (flags & DG_QKNORM) ? 1 : 0;
+  a.pos_dev = pos_dev;
+  a.max_pos = max_pos;
+  for (int w = 0; w < 3; ++w) a.pstep[w] = pstep[w];
+  a.fpos = fpos;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
   if (dtype == DG_F32) return rope_pick_d<float, float>(dpad, epl, a, s);
@@ -348,6 +369,42 @@ extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, cons
   }
   if (freqs_dtype == DG_F32) return rope_pick_d<f16_t, float>(dpad, epl, a, s);
   return rope_pick_d<f16_t, f16_t>(dpad, epl, a, s);
+}
+
+}  // namespace
+}  // namespace dg
+
+extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, const void* q,
+                                     const dg_stride3* q_st, void* q_out, const dg_stride3* qo_st,
+                                     const void* k, const dg_stride3* k_st, void* k_out,
+                                     const dg_stride3* ko_st, const void* v,
+                                     const dg_stride3* v_st, void* v_out,
+                                     const dg_stride3* vo_st, const void* freqs,
+                                     const dg_stride3* f_st, int freqs_dtype, int flags,
+                                     void* stream) {
+  const int64_t none[3] = {0, 0, 0};
+  return rope_entry(B, T, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_out, ko_st, v, v_st, v_out,
+                    vo_st, freqs, f_st, freqs_dtype, flags, nullptr, 0, none, 0, stream);
+}
+
+extern "C" int dg_rope_qknorm_append_at(int B, int H, int D, int dtype, const void* q,
+                                        const dg_stride3* q_st, void* q_out,
+                                        const dg_stride3* qo_st, const void* k,
+                                        const dg_stride3* k_st, void* k_cache,
+                                        const dg_stride3* kc_st, const void* v,
+                                        const dg_stride3* v_st, void* v_cache,
+                                        const dg_stride3* vc_st, const void* freqs,
+                                        int64_t freqs_pos_stride, int freqs_dtype,
+                                        const int32_t* pos, int max_pos, int flags, void* stream) {
+  DG_REQUIRE(pos != nullptr, DG_EINVAL, "rope_at: NULL position pointer");
+  DG_REQUIRE(max_pos >= 1, DG_EINVAL, "rope_at: max_pos must be >= 1 (got %d)", max_pos);
+  DG_REQUIRE((k == nullptr || kc_st != nullptr) && (v == nullptr || vc_st != nullptr), DG_EINVAL,
+             "rope_at: missing cache strides");
+  const int64_t pstep[3] = {0, k ? kc_st->t : 0, v ? vc_st->t : 0};
+  const dg_stride3 fst = {0, 0, 0};  // one position per call, broadcast over rows and heads
+  return rope_entry(B, 1, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_cache, kc_st, v, v_st,
+                    v_cache, vc_st, freqs, &fst, freqs_dtype, flags, pos, max_pos, pstep,
+                    freqs_pos_stride, stream);
 }
 
 extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,

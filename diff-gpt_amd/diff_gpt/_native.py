@@ -62,6 +62,21 @@ _SIGNATURES = {
         + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
            ctypes.c_void_p],
     ),
+    "dg_rope_qknorm_append_at": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 6  # q, q_out, k, k_cache, v, v_cache
+        + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+           ctypes.c_int, ctypes.c_void_p],
+    ),
+    "dg_decode_attention_at_workspace_size": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "dg_decode_attention_at": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4  # q, k_cache, v_cache, y
+        + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+           ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+    ),
     "dg_rms_norm": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
@@ -242,6 +257,77 @@ def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tenso
         float(scale), int(prefix_len), int(group), _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "attention")
+
+
+def rope_qknorm_append_at_(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    freqs_table: torch.Tensor,
+    q_out: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    pos: torch.Tensor,
+    qknorm: bool,
+) -> None:
+    """dg_rope_qknorm_append_at: q, k, v, q_out (B,1,H,D); k_cache / v_cache the
+    (B,Tcap,H,D) cache views at position 0; freqs_table (Tmax, D/2, 2); pos a
+    one-element int32 device tensor (positions already cached)."""
+    B, T, H, D = q.shape
+    if T != 1 or k.shape != q.shape or v.shape != q.shape or q_out.shape != q.shape:
+        raise ValueError("rope_qknorm_append_at: q, k, v, q_out must be (B, 1, H, D)")
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2:] != (H, D):
+        raise ValueError("rope_qknorm_append_at: cache views must be (B, Tcap, H, D)")
+    if v_cache.shape != k_cache.shape:
+        raise ValueError("rope_qknorm_append_at: k and v caches differ in shape")
+    if freqs_table.dim() != 3 or freqs_table.shape[1:] != (D // 2, 2) or not freqs_table.is_contiguous():
+        raise ValueError("rope_qknorm_append_at: freqs_table must be a contiguous (Tmax, D/2, 2) table")
+    if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != q.device:
+        raise TypeError("rope_qknorm_append_at: pos must be a one-element int32 tensor on q's device")
+    max_pos = min(k_cache.size(1), freqs_table.size(0))
+    st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
+    rc = lib().dg_rope_qknorm_append_at(
+        B, H, D, _dtype_code(q),
+        _ptr(q), st(q), _ptr(q_out), st(q_out),
+        _ptr(k), st(k), _ptr(k_cache), st(k_cache),
+        _ptr(v), st(v), _ptr(v_cache), st(v_cache),
+        _ptr(freqs_table), freqs_table.stride(0), _dtype_code(freqs_table),
+        _ptr(pos), max_pos, DG_QKNORM if qknorm else 0, _stream(q),
+    )
+    _check(rc, "rope_qknorm_append_at")
+
+
+def decode_attention_at_(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    y: torch.Tensor,
+    scale: float,
+    pos: torch.Tensor,
+    prefix_len: int = 0,
+    group: int = 1,
+) -> None:
+    """dg_decode_attention_at: q, y (B,1,H,D); k_cache / v_cache (B,Tcap,H,D)
+    views; attends over positions 0 .. pos[0]."""
+    B, T, H, D = q.shape
+    if T != 1 or y.shape != q.shape:
+        raise ValueError("decode_attention_at: q and y must be (B, 1, H, D)")
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2:] != (H, D) or v_cache.shape != k_cache.shape:
+        raise ValueError("decode_attention_at: cache views must be (B, Tcap, H, D)")
+    if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != q.device:
+        raise TypeError("decode_attention_at: pos must be a one-element int32 tensor on q's device")
+    code = _dtype_code(q)
+    L = lib()
+    max_keys = k_cache.size(1)
+    ws_bytes = L.dg_decode_attention_at_workspace_size(B, H, max_keys, D, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
+    rc = L.dg_decode_attention_at(
+        B, H, D, code, _ptr(q), st(q), _ptr(k_cache), st(k_cache), _ptr(v_cache), st(v_cache),
+        _ptr(y), st(y), float(scale), int(prefix_len), int(group), _ptr(pos), max_keys,
+        _ptr(ws), ws_bytes, _stream(q),
+    )
+    _check(rc, "decode_attention_at")
 
 
 def rms_norm_(x: torch.Tensor, out: torch.Tensor) -> None:

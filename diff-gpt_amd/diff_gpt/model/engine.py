@@ -32,11 +32,65 @@ class RowState:
         self.forced_tokens = deque()
 
 
-class Engine:
-    __slots__ = "model"
+class _DecodeGraph:
+    """GPT.forward over one new token per row, captured once as a HIP graph and
+    replayed for every decode step.
 
-    def __init__(self, model: BaseGPT) -> None:
+    The cache carries a device copy of its position (KVCache.pos_dev); the
+    attention layers then launch the position-reading kernels
+    (dg_rope_qknorm_append_at, dg_decode_attention_at) and the model hands
+    them the whole RoPE table, so nothing in the captured launches depends on
+    the step.  The graph ends by advancing pos_dev; step() advances the host
+    copy.  Inputs go through a static id buffer, the logits come back in a
+    static buffer that the next replay overwrites."""
+
+    __slots__ = ("cache", "ids", "graph", "logits")
+
+    def __init__(self, model: BaseGPT, cache: KVCache, n_rows: int, device: torch.device) -> None:
+        self.cache = cache
+        self.ids = torch.zeros((n_rows, 1), dtype=torch.long, device=device)
+        pos0 = cache.pos
+        cache.pos_dev = torch.full((1,), pos0, dtype=torch.int32, device=device)
+        try:
+            # warm-up outside the capture (library handles, allocator); it
+            # appends the K/V of a zero token at pos0, which the first replay
+            # overwrites
+            side = torch.cuda.Stream(device=device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                model.forward(self.ids, kv_cache=cache)
+            torch.cuda.current_stream(device).wait_stream(side)
+            cache.pos = pos0
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                logits, _ = model.forward(self.ids, kv_cache=cache)
+                self.logits = logits[:, -1, :]
+                cache.pos_dev.add_(1)
+            cache.pos = pos0
+        except BaseException:
+            cache.pos = pos0
+            cache.pos_dev = None
+            raise
+
+    def step(self, ids: torch.Tensor) -> torch.Tensor:
+        self.ids.copy_(ids)
+        self.graph.replay()
+        self.cache.pos += 1
+        return self.logits
+
+    def close(self) -> None:
+        self.cache.pos_dev = None
+
+
+class Engine:
+    __slots__ = ("model", "use_graph")
+
+    def __init__(self, model: BaseGPT, use_graph: bool = True) -> None:
+        """use_graph: replay the decode step as a captured HIP graph (same
+        kernels and arithmetic as the eager forward, no per-step launch
+        overhead); False runs every step eagerly."""
         self.model = model
+        self.use_graph = use_graph
 
     def _budget(self, prompt_len: int, max_tokens: int | None) -> int:
         # RoPE table covers 2*block_size positions (engine.py:55-64)
@@ -61,6 +115,27 @@ class Engine:
         that token for every row.  Its length must be at least the number of
         generated steps.
         """
+        # The per-row forcing queues of RowState are never filled inside a
+        # generation call (engine.py:129-144 passes the sampled or scheduled
+        # column through), so a column is the sampled/forced tokens and its
+        # mask is 1 for a sampled step, 0 for a forced one.
+        for column, forced in self._device_steps(
+            tokens, num_samples, max_tokens, sampler, seed, force_schedule
+        ):
+            yield column.tolist(), [0 if forced else 1] * num_samples
+
+    def _device_steps(
+        self,
+        tokens: list[int],
+        num_samples: int,
+        max_tokens: int | None,
+        sampler: Sampler | None,
+        seed: int,
+        force_schedule: list[int | None] | None,
+    ) -> Generator[tuple[torch.Tensor, bool], None, None]:
+        """The generation loop with the token columns kept on the device:
+        yields ((num_samples,) int64 column, forced) per step, and feeds each
+        column to the next decode forward without a host round trip."""
         assert isinstance(tokens, list), "tokens must be a list of ints"
         assert len(tokens) > 0, "tokens must be non-empty"
         assert all(isinstance(t, int) for t in tokens), "tokens must be a list of ints"
@@ -90,41 +165,42 @@ class Engine:
         logits, _ = model.forward(ids, kv_cache=prompt_cache)
         logits = logits[:, -1, :].expand(num_samples, -1)
 
-        # 2) every row starts from the same prompt cache
+        # 2) every row starts from the same prompt cache (read once per
+        #    decode step thanks to the recorded shared prefix)
         cache = KVCache(batch_size=num_samples, seq_len=len(tokens) + steps, **geometry)
         cache.prefill(prompt_cache)
         del prompt_cache
 
-        rows = [RowState(list(tokens)) for _ in range(num_samples)]
-
-        for step in range(steps):
-            forced = None if force_schedule is None else force_schedule[step]
-            if forced is None:
-                if sampler is not None:
-                    picked = sampler(logits, rng=rng)
+        decode = None
+        if self.use_graph and steps > 1 and torch.device(device).type == "cuda":
+            decode = _DecodeGraph(model, cache, num_samples, torch.device(device))
+        try:
+            for step in range(steps):
+                forced = None if force_schedule is None else force_schedule[step]
+                if forced is None:
+                    if sampler is not None:
+                        picked = sampler(logits, rng=rng)
+                    else:
+                        picked = torch.multinomial(
+                            torch.softmax(logits, dim=-1), num_samples=1, generator=rng
+                        )
+                    column = picked[:, 0]
                 else:
-                    picked = torch.multinomial(
-                        torch.softmax(logits, dim=-1), num_samples=1, generator=rng
-                    )
-                proposals = picked[:, 0].tolist()
-            else:
-                proposals = [forced] * num_samples
+                    column = torch.full((num_samples,), forced, dtype=torch.long, device=logits.device)
+                yield column, forced is not None
 
-            column: list[int] = []
-            masks: list[int] = []
-            for row, proposal in zip(rows, proposals):
-                queued = len(row.forced_tokens) > 0
-                tok = row.forced_tokens.popleft() if queued else proposal
-                masks.append(0 if (queued or forced is not None) else 1)
-                column.append(tok)
-                row.current_tokens.append(tok)
-            yield column, masks
+                # 3) one decode forward for the column just emitted
+                ids = column.unsqueeze(1)
+                if decode is not None:
+                    logits = decode.step(ids)
+                else:
+                    logits, _ = model.forward(ids, kv_cache=cache)
+                    logits = logits[:, -1, :]
+        finally:
+            if decode is not None:
+                decode.close()
 
-            # 3) one decode forward for the column just emitted
-            ids = torch.tensor(column, dtype=torch.long, device=device).unsqueeze(1)
-            logits, _ = model.forward(ids, kv_cache=cache)
-            logits = logits[:, -1, :]
-
+    @torch.inference_mode()
     def generate_batch(
         self, tokens: list[int], num_samples: int = 1, **kwargs
     ) -> tuple[list[list[int]], list[list[int]]]:
@@ -132,10 +208,21 @@ class Engine:
         Non-streaming batch generation that just returns the final token sequences.
         Returns (results, masks): each a list of `num_samples` lists of ints.
         """
-        results = [list(tokens) for _ in range(num_samples)]
-        masks = [[0] * len(tokens) for _ in range(num_samples)]
-        for column, mask_column in self.generate(tokens, num_samples, **kwargs):
-            for res, m, tok, mk in zip(results, masks, column, mask_column):
-                res.append(tok)
-                m.append(mk)
+        unknown = set(kwargs) - {"max_tokens", "sampler", "seed", "force_schedule"}
+        if unknown:
+            raise TypeError(f"generate() got unexpected keyword arguments {sorted(unknown)}")
+        columns, mask_steps = [], []
+        for column, forced in self._device_steps(
+            tokens,
+            num_samples,
+            kwargs.get("max_tokens"),
+            kwargs.get("sampler"),
+            kwargs.get("seed", 42),
+            kwargs.get("force_schedule"),
+        ):
+            columns.append(column)
+            mask_steps.append(0 if forced else 1)
+        generated = torch.stack(columns, dim=1).tolist() if columns else [[] for _ in range(num_samples)]
+        results = [list(tokens) + row for row in generated]
+        masks = [[0] * len(tokens) + mask_steps for _ in range(num_samples)]
         return results, masks

@@ -149,7 +149,12 @@ class GPT(BaseGPT):
         start = 0 if kv_cache is None else kv_cache.get_pos()
         end = start + T
         assert end <= self.freqs_cis.shape[0]
-        freqs_cis = self.freqs_cis[start:end].view(1, T, 1, -1, 2)
+        if kv_cache is not None and kv_cache.pos_dev is not None:
+            # captured decode step: the kernels index the whole table with the
+            # position they read on the device
+            freqs_cis = self.freqs_cis
+        else:
+            freqs_cis = self.freqs_cis[start:end].view(1, T, 1, -1, 2)
 
         x = rms_norm(self.token_embedding_table(idx))
         # Block-AttnRes state: the normalised embedding is block 0 and also the

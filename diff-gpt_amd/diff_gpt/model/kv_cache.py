@@ -40,6 +40,7 @@ class KVCache:
         "kv_cache",
         "pos",
         "shared_prefix",
+        "pos_dev",
     )
 
     def __init__(
@@ -58,6 +59,10 @@ class KVCache:
         # prefill); decode attention then reads that prefix from the group's
         # first row only.  None otherwise.
         self.shared_prefix: tuple[int, int] | None = None
+        # Device mirror of `pos` (one int32) while a captured decode step is in
+        # use: the graph-replayable kernels read the position from it, and the
+        # step advances both copies.  None in ordinary (eager) use.
+        self.pos_dev: torch.Tensor | None = None
 
     def reset(self) -> None:
         self.pos = 0

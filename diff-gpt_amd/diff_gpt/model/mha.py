@@ -62,6 +62,8 @@ class MultiHeadAttention(nn.Module):
         g = self.c_g(x)
 
         q_rot = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
+        if kv_cache is not None and kv_cache.pos_dev is not None:
+            return self._decode_step_at(q, k, v, g, q_rot, freqs_cis, kv_cache)
         if kv_cache is None:
             # no cache: normalised keys go to a scratch tensor, values are read
             # in place from the projection output
@@ -90,4 +92,25 @@ class MultiHeadAttention(nn.Module):
         y = ops.attention(q_rot, keys, values, 1.0 / math.sqrt(D), prefix_len, group)
         y = y.view(B, T, H * D)
         y = y * torch.sigmoid(g)
+        return self.c_proj(y)
+
+    def _decode_step_at(self, q, k, v, g, q_rot, freqs_table, kv_cache: KVCache) -> torch.Tensor:
+        """One decode token per row with the position read on the device
+        (kv_cache.pos_dev): the same arithmetic as forward(), in the launch form
+        a HIP graph can replay at every position.  freqs_table is the model's
+        whole (Tmax, D/2, 2) table."""
+        B, T, H, D = q.shape
+        assert T == 1, "a captured decode step takes one token per row"
+        t0, t1 = kv_cache.ensure_window(1, k.dtype, k.device)
+        cache = kv_cache.kv_cache
+        assert cache.size(4) >= t1, "the cache must not grow inside a captured decode step"
+        k_cache = cache[self.layer_idx, 0].transpose(1, 2)  # (B, Tcap, H, D) at position 0
+        v_cache = cache[self.layer_idx, 1].transpose(1, 2)
+        _native.rope_qknorm_append_at_(q, k, v, freqs_table, q_rot, k_cache, v_cache, kv_cache.pos_dev, True)
+        kv_cache.advance(self.layer_idx, t1)
+        prefix_len, group = (0, 1) if kv_cache.shared_prefix is None else kv_cache.shared_prefix
+        y = torch.empty_like(q_rot)
+        _native.decode_attention_at_(q_rot, k_cache, v_cache, y, 1.0 / math.sqrt(D), kv_cache.pos_dev,
+                                     prefix_len, group)
+        y = y.view(B, T, H * D) * torch.sigmoid(g)
         return self.c_proj(y)

@@ -140,6 +140,44 @@ DG_API int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Decode-step forms for HIP graph capture.  The number of positions already in
+ * the cache is read on the device from *pos (int32), so a captured decode step
+ * (GPT.forward over one new token per row, gpt.py:140-200) replays unchanged
+ * at every position; the caller advances *pos after the step.
+ *
+ * dg_rope_qknorm_append_at: dg_rope_qknorm_append with T = 1 at position *pos
+ * (mha.py:44-56 with kv_cache.py:108-109): k_cache / v_cache are the cache
+ * pages at position 0 viewed as (B,Tcap,H,D) (strides b, t = D, h), the new
+ * key / value go to t = *pos; freqs is the (cos, sin) table at position 0
+ * with freqs_pos_stride elements per position (gpt.py:150-153 slicing done on
+ * the device).  Nothing is written when *pos is outside [0, max_pos).
+ *
+ * dg_decode_attention_at: dg_attention_grouped with Tq = 1 over the keys
+ * 0 .. *pos of the cache pages (mha.py:65-68), at most max_keys of them.  Key
+ * splits and the workspace (dg_decode_attention_at_workspace_size) are sized
+ * for max_keys.
+ */
+DG_API int dg_rope_qknorm_append_at(int B, int H, int D, int dtype,
+                                    const void* q, const dg_stride3* q_st,
+                                    void* q_out, const dg_stride3* qo_st,
+                                    const void* k, const dg_stride3* k_st,
+                                    void* k_cache, const dg_stride3* kc_st,
+                                    const void* v, const dg_stride3* v_st,
+                                    void* v_cache, const dg_stride3* vc_st,
+                                    const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
+                                    const int32_t* pos, int max_pos, int flags, void* stream);
+
+DG_API size_t dg_decode_attention_at_workspace_size(int B, int H, int max_keys, int D, int dtype);
+
+DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
+                                  const void* q, const dg_stride3* q_st,
+                                  const void* k_cache, const dg_stride3* kc_st,
+                                  const void* v_cache, const dg_stride3* vc_st,
+                                  void* y, const dg_stride3* y_st, float scale,
+                                  int prefix_len, int group, const int32_t* pos, int max_keys,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with
  * eps=None, i.e. FLT_EPSILON, computed in fp32 and rounded once to dtype).
  * x and out are M rows of N elements with row strides x_ld / out_ld.

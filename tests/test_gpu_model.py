@@ -445,3 +445,63 @@ def test_bf16_model_logits_close_to_oracle(dev):
     span = max(e.abs().max().item() for e in exact)
     assert worst_ours <= 1.5 * worst_ref + 1e-3, (worst_ours, worst_ref)
     assert worst_ours <= 2e-2 * 2 * span, (worst_ours, span)
+
+
+# ------------------------------------------------------------------ captured decode step
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_step_kernels_match_plain(dev, dtype):
+    """dg_rope_qknorm_append_at / dg_decode_attention_at (position read on the
+    device) write and compute exactly what the plain kernels do at that
+    position, and write nothing for a position past the cache."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, D, cap, pos = 6, 4, 16, 40, 23
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(B, 1, H, D, generator=g).to(dtype).to(dev) for _ in range(3))
+    table = precompute_freqs_cis(D, 2 * cap, 10000).to(dtype).to(dev)
+    base = torch.randn(2, B, H, cap, D, generator=g).to(dtype).to(dev)
+    c1, c2 = base.clone(), base.clone()
+    ops = _native.ops()
+    # plain: explicit window at pos
+    q1 = torch.empty_like(q)
+    ops.rope_qknorm_append(q, k, v, table[pos:pos + 1].view(1, 1, 1, D // 2, 2), q1,
+                           c1[0, :, :, pos:pos + 1].transpose(1, 2), c1[1, :, :, pos:pos + 1].transpose(1, 2), True)
+    y1 = ops.attention(q1, c1[0, :, :, :pos + 1].transpose(1, 2), c1[1, :, :, :pos + 1].transpose(1, 2), D ** -0.5)
+    # device position
+    p = torch.tensor([pos], dtype=torch.int32, device=dev)
+    q2, y2 = torch.empty_like(q), torch.empty_like(q)
+    _native.rope_qknorm_append_at_(q, k, v, table, q2, c2[0].transpose(1, 2), c2[1].transpose(1, 2), p, True)
+    _native.decode_attention_at_(q2, c2[0].transpose(1, 2), c2[1].transpose(1, 2), y2, D ** -0.5, p)
+    assert torch.equal(q1, q2) and torch.equal(c1, c2) and torch.equal(y1, y2)
+    # out-of-range position: nothing written
+    c3 = base.clone()
+    _native.rope_qknorm_append_at_(q, k, v, table, q2, c3[0].transpose(1, 2), c3[1].transpose(1, 2),
+                                   torch.tensor([cap], dtype=torch.int32, device=dev), True)
+    torch.cuda.synchronize()
+    assert torch.equal(c3, base)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_graph_replay_equals_eager(dev, dtype):
+    """The captured decode step replayed once per step (with the sampler, the
+    H2D token copy and host syncs between replays) reproduces the eager
+    engine token for token: greedy, forced steps, and temperature-1 sampling
+    with the same seed (identical logits -> identical draws)."""
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2,
+                use_checkpoint=False).eval().to(dev).to(dtype)
+    prompt = torch.randint(0, 256, (40,), generator=torch.Generator().manual_seed(3)).tolist()
+    schedule = [None, 5, None, None, 9, None, None, None]
+    for kw in (dict(sampler=TemperatureSampler(0.0)),
+               dict(sampler=TemperatureSampler(0.0), force_schedule=schedule),
+               dict(sampler=TemperatureSampler(1.0), seed=7)):
+        a = Engine(model).generate_batch(prompt, num_samples=12, max_tokens=8, **kw)
+        b = Engine(model, use_graph=False).generate_batch(prompt, num_samples=12, max_tokens=8, **kw)
+        assert a == b, kw
