@@ -72,6 +72,24 @@ __global__ __launch_bounds__(256) void copy4d_kernel(const CopyArgs a) {
   }
 }
 
+// Rows whose last dimension is contiguous on both sides and a whole number of
+// 16-byte chunks: one workgroup per (i0, i1, i2) row, 16-byte loads and
+// stores, the row index decomposed once per row.  Strides here are in bytes.
+__global__ __launch_bounds__(256) void copy4d_rows_kernel(const CopyArgs a) {
+  const int chunks = (int)a.n3;
+  for (int64_t row = blockIdx.x; row < a.total; row += gridDim.x) {
+    int64_t r = row;
+    const int64_t i2 = r % a.n2;
+    r /= a.n2;
+    const int64_t i1 = r % a.n1;
+    const int64_t i0 = r / a.n1;
+    const uint4* src = reinterpret_cast<const uint4*>(static_cast<const char*>(a.src) + i0 * a.s0 +
+                                                      i1 * a.s1 + i2 * a.s2);
+    uint4* dst = reinterpret_cast<uint4*>(static_cast<char*>(a.dst) + i0 * a.d0 + i1 * a.d1 + i2 * a.d2);
+    for (int c = threadIdx.x; c < chunks; c += blockDim.x) dst[c] = src[c];
+  }
+}
+
 }  // namespace dg
 
 using namespace dg;
@@ -165,9 +183,25 @@ extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const
   a.n0 = shape[0]; a.n1 = shape[1]; a.n2 = shape[2]; a.n3 = shape[3];
   a.s0 = src_st[0]; a.s1 = src_st[1]; a.s2 = src_st[2]; a.s3 = src_st[3];
   a.d0 = dst_st[0]; a.d1 = dst_st[1]; a.d2 = dst_st[2]; a.d3 = dst_st[3];
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  const int64_t row_bytes = shape[3] * es;
+  auto bytes16 = [&](int64_t stride) { return (stride * es) % 16 == 0; };
+  if (src_st[3] == 1 && dst_st[3] == 1 && row_bytes % 16 == 0 &&
+      (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0 &&
+      bytes16(src_st[0]) && bytes16(src_st[1]) && bytes16(src_st[2]) && bytes16(dst_st[0]) &&
+      bytes16(dst_st[1]) && bytes16(dst_st[2]) && row_bytes / 16 <= 0x7fffffffLL) {
+    CopyArgs r = a;
+    r.total = shape[0] * shape[1] * shape[2];  // rows
+    r.n3 = row_bytes / 16;                     // 16-byte chunks per row
+    r.s0 = src_st[0] * es; r.s1 = src_st[1] * es; r.s2 = src_st[2] * es;
+    r.d0 = dst_st[0] * es; r.d1 = dst_st[1] * es; r.d2 = dst_st[2] * es;
+    const int64_t grid = r.total < 262144 ? r.total : 262144;
+    hipLaunchKernelGGL(copy4d_rows_kernel, dim3((unsigned)grid), dim3(256), 0, s, r);
+    return check_launch("copy4d_rows_kernel");
+  }
   int64_t blocks = (a.total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == DG_F32)
     hipLaunchKernelGGL(copy4d_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
   else

@@ -237,3 +237,20 @@ def test_copy4d_exact_with_broadcast(dev, dtype):
     dst2 = torch.zeros((3, 4, 7, 5), dtype=TDT[dtype], device=dev)
     _native.ops().copy4d(src.expand(4, 3, 5, 7).transpose(0, 1).transpose(2, 3), dst2)
     assert torch.equal(dst2.cpu(), src.cpu().expand(4, 3, 5, 7).transpose(0, 1).transpose(2, 3))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_copy4d_row_vector_path(dev, dtype):
+    """Rows with a contiguous, 16-byte-multiple last dimension take the
+    row-vectorised kernel: batch broadcast of a cache prefix into strided
+    pages (KVCache.prefill), exact."""
+    from diff_gpt import _native
+
+    L2, B, H, T, D, cap = 4, 6, 3, 10, 16, 13
+    src = _randn((L2, 1, H, cap * D), 11, dtype).to(dev)
+    big = torch.full((L2, B, H, cap * D), -1.0, dtype=TDT[dtype], device=dev)
+    dst = big[..., : T * D]
+    _native.ops().copy4d(src[..., : T * D].expand(L2, B, H, T * D), dst)
+    ref = torch.full((L2, B, H, cap * D), -1.0, dtype=TDT[dtype])
+    ref[..., : T * D] = src[..., : T * D].cpu().expand(L2, B, H, T * D)
+    assert torch.equal(big.cpu(), ref)
