@@ -211,6 +211,98 @@ def prefill_leg(reps: int = 5):
     }
 
 
+def engine_leg(dtype_name: str):
+    """configs[1] end to end through the drop-in API: the README GPT (random
+    init, seed 0), 64 series of 96 uniform ids, each one
+    Engine.generate_batch(prompt, num_samples=100, max_tokens=48) with a
+    temperature-1 sampler -- the reference's call pattern (diff_gpt.py:229-235).
+    Includes the non-attention model work (projections, FFN, Block-AttnRes,
+    lm_head), sampling and the host-side result lists.  Also one batched call
+    with all 6400 rows on one prompt."""
+    import torch
+
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    dev = torch.device("cuda:0")
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=138, n_head=HEADS, n_layer=LAYERS,
+                use_checkpoint=False).eval().to(dev).to(dt)
+    g = torch.Generator().manual_seed(1)
+    prompts = [torch.randint(0, 256, (PREFIX,), generator=g).tolist() for _ in range(SERIES)]
+    engine = Engine(model)
+    sampler = TemperatureSampler(1.0)
+    engine.generate_batch(prompts[0], num_samples=TRAJ, max_tokens=NEW, sampler=sampler)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, prompt in enumerate(prompts):
+        engine.generate_batch(prompt, num_samples=TRAJ, max_tokens=NEW, sampler=sampler, seed=s)
+    torch.cuda.synchronize()
+    per_series = time.perf_counter() - t0
+    engine.generate_batch(prompts[0], num_samples=SERIES * TRAJ, max_tokens=NEW, sampler=sampler)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    engine.generate_batch(prompts[0], num_samples=SERIES * TRAJ, max_tokens=NEW, sampler=sampler)
+    torch.cuda.synchronize()
+    batched = time.perf_counter() - t0
+    tokens = SERIES * TRAJ * NEW
+    return {
+        "workload": "configs[1] through Engine.generate_batch: 64 calls x 100 trajectories, "
+                    "96-token prompt, 48 temperature-1 steps, README GPT (2 layers, d64, h4)",
+        "dtype": dtype_name,
+        "tokens_per_s": tokens / per_series,
+        "seconds": per_series,
+        "one_call_6400_rows_tokens_per_s": tokens / batched,
+    }
+
+
+def engine_cpu_baseline(dtype_name: str, budget_s: float = 10.0):
+    """The reference's engine pattern on the host cores (oracle.torch_ref): per
+    series a batch-1 prefill, the cache broadcast to 100 rows, 48 steps of
+    softmax + multinomial and a 100-row forward -- for as many series as fit
+    the budget."""
+    import torch
+
+    from diff_gpt.model.gpt import GPT
+    from oracle import torch_ref as tr
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    dt = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=138, n_head=HEADS, n_layer=LAYERS, use_checkpoint=False)
+    p = {k: v.detach().to(dt) for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=HEADS, n_layer=LAYERS)
+    table = tr.freqs_table(HEAD_DIM, 2 * 138, 10000)
+    g = torch.Generator().manual_seed(1)
+    done, t0 = 0, time.perf_counter()
+    with torch.no_grad():
+        while done < SERIES:
+            prompt = torch.randint(0, 256, (1, PREFIX), generator=g)
+            pc = tr.RefCache(1, HEADS, PREFIX, HEAD_DIM, LAYERS)
+            logits = tr.forward(p, cfg, prompt, pc, table)[:, -1].expand(TRAJ, -1)
+            cache = tr.RefCache(TRAJ, HEADS, PREFIX + NEW, HEAD_DIM, LAYERS)
+            cache.broadcast_from(pc)
+            rng = torch.Generator().manual_seed(done)
+            for _ in range(NEW):
+                nxt = torch.multinomial(torch.softmax(logits.float(), -1), 1, generator=rng)
+                logits = tr.forward(p, cfg, nxt, cache, table)[:, -1]
+            done += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+    el = time.perf_counter() - t0
+    return {
+        "value": done * TRAJ * NEW / el,
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} of 64 series (100 trajectories x 48 steps each), {dtype_name}, "
+                  "oracle.torch_ref model on the host cores",
+    }
+
+
 def cpu_baseline(dtype_name: str, budget_s: float = 12.0):
     """The oracle's torch-CPU restatement of the reference decode path
     (rope.py, rms_norm.py, kv_cache.py insert, mha.py:68 SDPA) on the same
@@ -272,6 +364,7 @@ def main():
     ap.add_argument("--dtype", default="fp32", choices=["fp32", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-engine", action="store_true", help="skip the end-to-end Engine leg")
     ap.add_argument("--traffic-json", default=str(REPO / "profiles" / "decode_attn_cfg1_traffic.json"))
     ap.add_argument("--single-dtype", action="store_true", help="skip the other-dtype decode leg")
     ap.add_argument("--decode-mode", default="shared", choices=["shared", "plain"],
@@ -319,6 +412,12 @@ def main():
     prefill = None if args.no_prefill else prefill_leg()
     if prefill:
         log(f"prefill: {prefill}")
+    engine = None if args.no_engine else engine_leg(args.dtype)
+    if engine:
+        log(f"engine: {engine}")
+        if not args.no_cpu_baseline:
+            engine["cpu_baseline"] = engine_cpu_baseline(args.dtype)
+            log(f"engine cpu: {engine['cpu_baseline']}")
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.dtype)
     out = {
         "metric": METRIC,
@@ -356,6 +455,7 @@ def main():
             "achieved_gbs": res_other["achieved_gbs"],
             "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill": prefill,
+        "engine": engine,
     }
     print(json.dumps(out), flush=True)
 
