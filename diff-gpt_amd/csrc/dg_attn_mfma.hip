@@ -47,6 +47,9 @@
 #ifndef DG_PREFILL_QW_D128
 #define DG_PREFILL_QW_D128 1
 #endif
+#ifndef DG_PREFILL_WAVES
+#define DG_PREFILL_WAVES 4
+#endif
 
 namespace dg {
 
@@ -134,7 +137,9 @@ __device__ __forceinline__ float half_pair_sum(float x) {
 
 template <typename T, int D, int QW>
 struct PrefillCfg {
-  static constexpr int BM = 128 * QW;       // queries per workgroup
+  static constexpr int WAVES = DG_PREFILL_WAVES;  // wavefronts per workgroup
+  static constexpr int NT = 64 * WAVES;           // threads per workgroup
+  static constexpr int BM = 32 * QW * WAVES;      // queries per workgroup
   static constexpr int KP = D + 8;          // padded K row (elements)
   static constexpr int VP = kBN + 4;        // padded V^T row (elements)
   static constexpr int K_ELEMS = kBN * KP;
@@ -144,10 +149,10 @@ struct PrefillCfg {
   static constexpr int NC = D / 16;         // 16-wide contraction chunks of QK^T
   static constexpr int NB = D / 32;         // 32-row blocks of O^T
   static constexpr int CPR = D / 8;         // 16-byte chunks per K row
-  static constexpr int KCPT = kBN * CPR / 256;      // K chunks per thread per tile
-  static constexpr int VBPT = kBN * D / 16 / 256;   // 4x4 V blocks per thread per tile
-  static_assert(KCPT >= 1 && (kBN * CPR) % 256 == 0, "K tile mapping");
-  static_assert(VBPT >= 1 && (kBN * D / 16) % 256 == 0, "V tile mapping");
+  static constexpr int KCHUNKS = kBN * CPR;       // 16-byte K chunks per tile
+  static constexpr int VBLOCKS = kBN * D / 16;    // 4x4 V blocks per tile
+  static constexpr int KCPT = (KCHUNKS + NT - 1) / NT;  // per thread (last round guarded)
+  static constexpr int VBPT = (VBLOCKS + NT - 1) / NT;
 };
 
 // Resident workgroups per CU the register allocation must allow: D = 64 fits
@@ -159,7 +164,8 @@ constexpr int prefill_wgs_per_cu() {
 }
 
 template <typename T, int D, int QW>
-__global__ __launch_bounds__(256, prefill_wgs_per_cu<D>()) void prefill_mfma_kernel(const PrefillArgs a) {
+__global__ __launch_bounds__(64 * DG_PREFILL_WAVES, prefill_wgs_per_cu<D>() * 4 / DG_PREFILL_WAVES)
+void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
   using C = PrefillCfg<T, D, QW>;
@@ -228,7 +234,7 @@ __global__ __launch_bounds__(256, prefill_wgs_per_cu<D>()) void prefill_mfma_ker
   int koff[KCPT], kkey[KCPT], kdst[KCPT];
 #pragma unroll
   for (int i = 0; i < KCPT; ++i) {
-    const int chunk = tid + 256 * i;
+    const int chunk = min(tid + C::NT * i, C::KCHUNKS - 1);  // guarded below
     kkey[i] = chunk / CPR;
     koff[i] = kkey[i] * (int)a.kt + 8 * (chunk % CPR);
     kdst[i] = kkey[i] * KP + 8 * (chunk % CPR);
@@ -236,7 +242,7 @@ __global__ __launch_bounds__(256, prefill_wgs_per_cu<D>()) void prefill_mfma_ker
   int vkey[VBPT], voff[VBPT], vdst[VBPT];
 #pragma unroll
   for (int i = 0; i < VBPT; ++i) {
-    const int blk = tid + 256 * i;
+    const int blk = min(tid + C::NT * i, C::VBLOCKS - 1);  // guarded below
     const int dg = blk % (D / 4), kg = blk / (D / 4);
     vkey[i] = 4 * kg;
     voff[i] = 4 * kg * (int)a.vt + 4 * dg;
@@ -279,8 +285,10 @@ __global__ __launch_bounds__(256, prefill_wgs_per_cu<D>()) void prefill_mfma_ker
     uint16_t* Ks_ = lds + (SLOT) * C::BUF;                                                 \
     uint16_t* Vt_ = Ks_ + C::K_ELEMS;                                                      \
     _Pragma("unroll") for (int i = 0; i < KCPT; ++i)                                       \
-        *reinterpret_cast<u32x4_t*>(&Ks_[kdst[i]]) = kreg[i];                                \
+        if (C::KCHUNKS % C::NT == 0 || tid + C::NT * i < C::KCHUNKS)                       \
+            *reinterpret_cast<u32x4_t*>(&Ks_[kdst[i]]) = kreg[i];                            \
     _Pragma("unroll") for (int i = 0; i < VBPT; ++i) {                                     \
+      if (C::VBLOCKS % C::NT != 0 && tid + C::NT * i >= C::VBLOCKS) continue;               \
       const uint2* e = vreg[i];                                                            \
       const uint2 d0 = make_uint2((e[0].x & 0xffffu) | (e[1].x << 16),                     \
                                   (e[2].x & 0xffffu) | (e[3].x << 16));                    \
@@ -456,7 +464,8 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
   const int64_t nwg = (int64_t)(a.nwg) * a.nqb;  // a.nwg holds B*H on entry
   DG_REQUIRE(nwg <= 0x7fffffffLL, DG_EINVAL, "prefill: too many workgroups");
   a.nwg = (int)nwg;
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW>), dim3((unsigned)a.nwg), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW>), dim3((unsigned)a.nwg),
+                     dim3(PrefillCfg<T, D, QW>::NT), 0, s, a);
   return check_launch("prefill_mfma_kernel");
 }
 
