@@ -11,10 +11,15 @@ synthetic q/k/v resident in HBM.
     python bench.py [--steps K] [--warmup W] [--dtype fp32|bf16] [--no-prefill]
                     [--no-cpu-baseline] [--traffic-json FILE]
 
-Prints ONE JSON line.  value = sequences*48*K / timed seconds (tokens/s).
-roofline = decode-attention kernel: algorithmic bytes per launch
-B*H*es*(2*L_kv*D + 2*D) over its mean launch time, timed with HIP events on
-the launch stream inside the timed region.  The prefill leg (configs[2]:
+Prints ONE JSON line.  value = sequences*48*K / timed seconds (tokens/s); the
+job's 192 launches are captured once in a HIP graph (as Engine captures its
+decode step) and the K timed steps are K graph replays.  roofline =
+decode-attention kernel: algorithmic bytes per launch over its mean launch
+time, timed with HIP events on the launch stream around K replays of a graph
+holding only the job's 96 decode-attention launches (so the graph's short
+gaps between kernels count as kernel time).  Bytes per launch:
+B*H*es*(2*L_kv*D + 2*D) in plain mode; in shared mode the prefix rows count
+once per series.  The prefill leg (configs[2]:
 B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s with
 FLOP = 2*B*H*D*T*(T+1).  cpu_baseline = the oracle's torch-CPU restatement of
 the reference decode path on a bounded sample, on this host's cores.
@@ -74,11 +79,13 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
     y = torch.empty((B, 1, H, D), dtype=dt, device=dev)
     torch.cuda.synchronize()
 
-    # The job calls the C-ABI directly with argument packs prepared once, as a
-    # native engine would: the host then stays far ahead of the GPU, kernels
-    # run back to back, and the events below time the kernels themselves.
+    # The job calls the C-ABI directly with argument packs prepared once, on a
+    # stream of its own, and is captured in a HIP graph, as the Engine's decode
+    # step is: the 192 launches of a job then run back to back with no host
+    # in between.
     lib = _native.lib()
-    stream = _native._stream(q_rot)
+    side = torch.cuda.Stream()
+    stream = ctypes.c_void_p(side.cuda_stream)
     code = _native._DTYPE_CODE[dt]
     P = ctypes.pointer
     S3 = _native._bthd_strides
@@ -109,39 +116,44 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
             packs.append((rope_args, attn_args))
     rope_fn, attn_fn = lib.dg_rope_qknorm_append, lib.dg_attention_grouped
 
-    ev = []  # (start, end) events around each decode-attention launch
-
-    def run_job(record: bool):
+    def run(with_rope: bool):
         for rope_args, attn_args in packs:
-            if rope_fn(*rope_args) != 0:
+            if with_rope and rope_fn(*rope_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
-            if record:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
-                rc = attn_fn(*attn_args)
-                b.record()
-                ev.append((a, b))
-            else:
-                rc = attn_fn(*attn_args)
-            if rc != 0:
+            if attn_fn(*attn_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
 
-    for _ in range(warmup):
-        run_job(False)
+    with torch.cuda.stream(side):
+        for _ in range(max(1, warmup)):  # eager: loads the code objects before capture
+            run(True)
+    torch.cuda.synchronize()
+    job, attn_only = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(job, stream=side):
+        run(True)
+    with torch.cuda.graph(attn_only, stream=side):
+        run(False)
     torch.cuda.synchronize()
     log(f"decode {dtype_name}: warmup done, timing {steps} jobs")
-    t_start = time.perf_counter()
-    for _ in range(steps):
-        run_job(True)
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t_start
-
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    launches = len(kern_ms)
-    mean_kernel_s = sum(kern_ms) / launches / 1e3
-    # algorithmic bytes per launch, averaged over the job's L_kv = 97..144
-    # algorithmic bytes per launch: K+V rows of every visible position, q, y;
-    # with a shared prefix the prefix rows count once per series (unique bytes)
+    with torch.cuda.stream(side):
+        t_start = time.perf_counter()
+        for _ in range(steps):
+            job.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t_start
+        # decode-attention launches alone (the same 96 per job), bracketed by
+        # events on their stream: mean launch duration including the graph's
+        # small gaps between kernels
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(side)
+        for _ in range(steps):
+            attn_only.replay()
+        b.record(side)
+        torch.cuda.synchronize()
+    launches = steps * len(packs)
+    attn_s = a.elapsed_time(b) / 1e3
+    mean_kernel_s = attn_s / launches
+    # algorithmic bytes per launch, averaged over the job's L_kv = 97..144:
+    # K+V rows of every visible position, q, y; with a shared prefix the prefix rows count once per series (unique bytes)
     if shared:
         bytes_job = sum(H * es * (2 * D * (PREFIX * SERIES + (s + 1) * B) + 2 * D * B)
                         for s in range(NEW)) * L
@@ -157,7 +169,7 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
         "bytes_per_launch": bytes_per_launch,
         "achieved_gbs": achieved,
         "launches": launches,
-        "attn_only_tokens_per_s": B * NEW / (sum(kern_ms) / steps / 1e3),
+        "attn_only_tokens_per_s": B * NEW * steps / attn_s,
     }
 
 

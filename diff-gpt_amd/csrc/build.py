@@ -20,7 +20,7 @@ PKG = HERE.parent
 REPO = PKG.parent
 BUILD = HERE / "_build"
 LIB = PKG / "lib" / "libdgattn.so"
-SOURCES = ["dg_abi.hip", "dg_rope.hip", "dg_attn_vec.hip", "dg_attn_mfma.hip"]
+SOURCES = ["dg_abi.hip", "dg_rope.hip", "dg_attn_vec.hip", "dg_attn_mfma.hip", "dg_attn_shared.hip"]
 HEADERS = ["dg_common.h", str(REPO / "include" / "dgattn.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -62,7 +62,7 @@ def _compile(src: str, force: bool) -> Path:
 def build(force: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(4, len(SOURCES))) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(5, len(SOURCES))) as ex:
         objs = list(ex.map(lambda s: _compile(s, force), SOURCES))
     if force or not LIB.exists() or LIB.stat().st_mtime < _newest(objs):
         tmp = LIB.with_suffix(".so.tmp")

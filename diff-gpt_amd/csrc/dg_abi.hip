@@ -33,6 +33,15 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                   int prefix_len, int group, const int* pos_dev, void* workspace,
                   size_t workspace_bytes, hipStream_t s);
+// dg_attn_shared.hip
+bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, int prefix_len,
+                                 int group, const void* q, const dg_stride3* q_st, const void* k,
+                                 const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
+                                 const void* y, const dg_stride3* y_st);
+int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
+                     const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
+                     void* y, const dg_stride3* y_st, float scale, int prefix_len, int group,
+                     const int* pos_dev, hipStream_t s);
 // dg_attn_mfma.hip
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
@@ -125,6 +134,13 @@ extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dty
   if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
     return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
   if (group == 1) prefix_len = 0;
+  // Groups of at least 16 rows: the shared prefix as a matrix product (when the
+  // vector kernel would not split the keys, so no workspace is involved).
+  if (vec_attention_splits(B, H, Tq, Tk, D) == 1 &&
+      shared_attention_applicable(B, H, Tq, Tk, D, dtype, prefix_len, group, q, q_st, k, k_st, v, v_st,
+                                  y, y_st))
+    return shared_attention(B, H, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
+                            group, nullptr, s);
   return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
                        group, nullptr, workspace, workspace_bytes, s);
 }
@@ -152,8 +168,13 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
   DG_REQUIRE(pos && q && k_cache && v_cache && y && q_st && kc_st && vc_st && y_st, DG_EINVAL,
              "attention_at: NULL argument");
   if (group == 1) prefix_len = 0;
-  // The kernel reads at most max_keys keys (Tk = min(*pos + 1, max_keys)); key
+  // The kernels read at most max_keys keys (Tk = min(*pos + 1, max_keys)); key
   // splits and the workspace are sized for max_keys.
+  if (vec_attention_splits(B, H, 1, max_keys, D) == 1 &&
+      shared_attention_applicable(B, H, 1, max_keys, D, dtype, prefix_len, group, q, q_st, k_cache, kc_st,
+                                  v_cache, vc_st, y, y_st))
+    return shared_attention(B, H, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
+                            scale, prefix_len, group, pos, static_cast<hipStream_t>(stream));
   return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
                        scale, prefix_len, group, pos, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));

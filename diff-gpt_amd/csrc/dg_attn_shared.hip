@@ -1,0 +1,389 @@
+// Decode attention (Tq = 1, mha.py:65-68) over a batch whose rows come in
+// groups sharing a cache prefix, with the prefix on the matrix cores.
+//
+// After KVCache.prefill from a batch-1 cache (kv_cache.py:77-79) the `group`
+// consecutive rows of each group hold identical keys and values at positions
+// 0 .. prefix_len-1.  For one decode step the scores of a group's rows against
+// that prefix form a real matrix product, S = Q_rows K_prefix^T, and so does
+// P V_prefix: this kernel runs both on MFMA, reading the prefix (L2-resident,
+// shared by the tiles of a group) once per 16-row tile.  The rows' own keys,
+// positions prefix_len .. Tk-1, differ from row to row and go through the
+// vector ALUs.  Both parts share one softmax offset per row and merge in
+// registers.
+//
+// Work unit = one wavefront = (group, tile of 16 rows of the group, head).
+// Lane l: c = l & 15 is the tile row, g = l >> 4 one of four lanes per row.
+//
+// Prefix (MFMA, v_mfma_f32_16x16x4_f32 or v_mfma_f32_16x16x16_{bf16,f16}):
+//   S^T (16 keys x 16 rows) = K_tile Q^T: lane (c, g) feeds key row c and
+//   query row c of the tile, each with the D/4 contiguous elements
+//   g*D/4 .. g*D/4 + D/4 - 1 (a fixed permutation of the contraction index,
+//   the same for both operands, so the dot products are unchanged); it gets
+//   back the scores of row c against keys 4g .. 4g+3 of the tile.  The
+//   online softmax runs over chunks of 64 keys (max over the chunk, lazy
+//   rescale as in the vector kernel), then
+//   O^T (D x 16 rows) += V^T P^T in steps of 4 keys: lane (c, g) feeds
+//   V[4g+s][16t+c] and its own probability of key 4g+s, and holds O^T for
+//   row c, columns 16t + 4g .. 16t + 4g + 3.
+// Own keys (VALU): lane (c, g) takes keys prefix_len + g + 4u of row c with
+//   the whole q, k and v rows in registers (D FMAs for q.k, D for p.v, no
+//   cross-lane traffic), starting from the prefix's softmax offset; the four
+//   lanes of a row merge at the end (max, rescale, then a two-step
+//   reduce-scatter with v_permlane32_swap / v_permlane16_swap that leaves each
+//   lane the columns its O^T registers hold).
+#include "dg_common.h"
+
+namespace dg {
+
+struct SharedArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* y;
+  int64_t qb, qh;
+  int64_t kb, kt, kh;
+  int64_t vb, vt, vh;
+  int64_t yb, yh;
+  int64_t units;  // ceil(B / group) * tiles * H
+  int B, H, Tk, prefix_len, group, tiles;
+  float scale_log2;  // scale * log2(e)
+  float lazy_raw;    // kSharedLazyLog2 / scale_log2
+  // graph-replayable form: keys are positions 0 .. *pos_dev, at most Tk
+  const int* pos_dev;
+};
+
+constexpr float kSharedLazyLog2 = 8.0f;
+constexpr int kSharedMinGroup = 16;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+// S^T += A B over one contraction step of 4 (fp32) or 16 (16-bit) elements.
+template <typename T, int DQ>
+__device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowRegs<T, DQ>& qop, f32x4_t acc) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int s = 0; s < DQ; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kop.w[s]), __uint_as_float(qop.w[s]), acc,
+                                                 0, 0, 0);
+  } else {
+    static_assert(DQ % 4 == 0, "16-bit operands come in runs of 4");
+#pragma unroll
+    for (int s = 0; s < DQ / 4; ++s) {
+      const uint32_t ka[2] = {kop.w[2 * s], kop.w[2 * s + 1]};
+      const uint32_t qa[2] = {qop.w[2 * s], qop.w[2 * s + 1]};
+      if constexpr (__is_same(T, bf16_t))
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, ka),
+                                                        __builtin_bit_cast(i16x4_t, qa), acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, ka),
+                                                    __builtin_bit_cast(f16x4_t, qa), acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
+// Max / sum over the four lanes c, c+16, c+32, c+48 of a tile row (identical
+// bits in all four).
+__device__ __forceinline__ float row_max4(float x) {
+  float a, b;
+  pair16(x, a, b);
+  x = fmaxf(a, b);
+  pair32(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float row_sum4(float x) {
+  float a, b;
+  pair16(x, a, b);
+  x = a + b;
+  pair32(x, a, b);
+  return a + b;
+}
+
+// Own-key lane layout: a quad of lanes holds one tile row, LPK lanes per key
+// row with EPL contiguous elements each (16 bytes, 32 for fp32 at D = 32), so
+// every quad reads whole cache rows and one load instruction covers 16 rows x
+// KPQ keys: few L1 accesses per byte, like the vector kernel's layout.
+template <typename T, int D>
+struct OwnCfg {
+  static constexpr int ROWB = D * (int)sizeof(T);
+  static constexpr int LPK = ROWB >= 64 ? 4 : 2;  // lanes per key row
+  static constexpr int KPQ = 4 / LPK;             // keys per quad and instruction
+  static constexpr int EPL = D / LPK;             // elements per lane
+  static constexpr int WORDS = EPL * (int)sizeof(T) / 4;
+  static constexpr int UO = 32 / WORDS;           // key instructions per register set (K+V: 64 VGPRs)
+  static constexpr int STEP = UO * KPQ;           // keys per row and register set
+};
+
+// Lane `src` of the wave's value x (ds_bpermute: a gather over the wave).
+__device__ __forceinline__ float lane_get(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
+  constexpr int DQ = D / 4;   // contraction elements per lane and key tile
+  constexpr int DT = D / 16;  // 16-column tiles of the output
+  constexpr int NT = 4;       // prefix key tiles (16 keys) per softmax chunk
+  using O = OwnCfg<T, D>;
+  constexpr int LPK = O::LPK, KPQ = O::KPQ, EPL = O::EPL, UO = O::UO, STEP = O::STEP;
+  using Op = RowRegs<T, DQ>;
+  using Slice = RowRegs<T, EPL>;
+
+  const int lane = threadIdx.x & 63;
+  // the tiles and heads of one group run on one XCD, whose L2 keeps the prefix
+  int blk = blockIdx.x;
+  if ((gridDim.x & 7) == 0) blk = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  const int unit = blk * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (unit >= a.units) return;  // whole wave exits; no barriers below
+  const int h = unit % a.H;
+  const int rest = unit / a.H;
+  const int tile = rest % a.tiles;
+  const int grp = rest / a.tiles;
+
+  const int64_t b0 = (int64_t)grp * a.group;  // the group's first row holds the prefix
+  // tile row r of the wave -> batch row (rows past the group compute on b0
+  // and store nothing)
+  auto row_of = [&](int r, bool& ok) __attribute__((always_inline)) {
+    const int rin = tile * 16 + r;
+    ok = rin < a.group && b0 + rin < a.B;
+    return ok ? b0 + rin : b0;
+  };
+
+  int Tk = a.Tk;
+  if (a.pos_dev != nullptr) Tk = min(*a.pos_dev + 1, a.Tk);
+  const int P = min(a.prefix_len, Tk);
+  const float cl = a.scale_log2;
+  const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
+  const T* kbase = static_cast<const T*>(a.k) + (int64_t)h * a.kh;
+  const T* vbase = static_cast<const T*>(a.v) + (int64_t)h * a.vh;
+  const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * a.qh;
+
+  // --- own keys: quad layout, first two register sets loaded up front --------
+  const int orow = lane >> 2, kk = (lane & 3) / LPK, piece = (lane & 3) % LPK;
+  bool ovalid;
+  const int64_t bo = row_of(orow, ovalid);
+  const T* kown = kbase + bo * a.kb + piece * EPL;
+  const T* vown = vbase + bo * a.vb + piece * EPL;
+  Slice qs;
+  load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
+  Slice kA[UO], vA[UO], kB[UO], vB[UO];
+  auto load_set = [&](Slice (&kr)[UO], Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < UO; ++u) {
+      if (j0 + KPQ * u >= Tk) break;  // wave-uniform
+      const int j = min(j0 + KPQ * u + kk, Tk - 1);  // past Tk: a valid row, masked below
+      load_row<T, EPL>(kr[u], kown + j * kt);
+      load_row<T, EPL>(vr[u], vown + j * vt);
+    }
+  };
+  if (P < Tk) load_set(kA, vA, P);
+  if (P + STEP < Tk) load_set(kB, vB, P + STEP);
+
+  // --- prefix on MFMA: lane (c, g) ---------------------------------------------
+  const int c = lane & 15, g = lane >> 4;
+  bool cvalid;
+  const int64_t bc = row_of(c, cvalid);
+  const T* kpre = kbase + b0 * a.kb;
+  const T* vpre = vbase + b0 * a.vb;
+  Op qop;
+  load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
+  float m = kNegInf, lp = 0.f;
+  f32x4_t oacc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < P; c0 += 16 * NT) {
+    f32x4_t sc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      sc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const int base = c0 + 16 * j;
+      if (base >= P) continue;  // wave-uniform
+      Op kop;
+      load_row<T, DQ>(kop, kpre + min(base + c, P - 1) * kt + g * DQ);
+      sc[j] = qk_mfma<T, DQ>(kop, qop, sc[j]);
+    }
+    float mx = kNegInf;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool in = c0 + 16 * j + 4 * g + r < P;
+        sc[j][r] = in ? sc[j][r] : kNegInf;
+        mx = fmaxf(mx, sc[j][r]);
+      }
+    }
+    mx = row_max4(mx);  // every chunk holds a prefix key: finite
+    if (mx > m + a.lazy_raw) {
+      const float alpha = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - mx) * cl);
+      m = mx;
+      lp *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+    }
+    const float moff = m * cl;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], cl, -moff));
+        sc[j][r] = p;
+        lp += p;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int base = c0 + 16 * j;
+      if (base >= P) continue;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const T* vp = vpre + min(base + 4 * g + s, P - 1) * vt + c;
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vp[16 * t]), sc[j][s], oacc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // --- own keys on the vector ALUs, from the prefix's offset (rescales stay rare)
+  float mo = lane_get(m, orow), lo = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
+    float sv[UO];
+    float mt = kNegInf;
+#pragma unroll
+    for (int u = 0; u < UO; ++u) {
+      sv[u] = kNegInf;
+      if (j0 + KPQ * u >= Tk) continue;  // slot not loaded (wave-uniform)
+      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
+      sv[u] = (j0 + KPQ * u + kk < Tk) ? dot : kNegInf;
+      mt = fmaxf(mt, sv[u]);
+    }
+    if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));  // one offset per quad
+    if (mt > mo + a.lazy_raw) {
+      const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
+      mo = mt;
+      lo *= alpha;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+    }
+    const float moff = mo * cl;
+#pragma unroll
+    for (int u = 0; u < UO; ++u) {
+      if (j0 + KPQ * u >= Tk) continue;
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[u], cl, -moff));
+      lo += p;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr[u], e), acc[e]);
+    }
+  };
+  for (int j0 = P; j0 < Tk;) {
+    process(kA, vA, j0);
+    j0 += STEP;
+    if (j0 + STEP < Tk) load_set(kA, vA, j0 + STEP);
+    if (j0 >= Tk) break;
+    process(kB, vB, j0);
+    j0 += STEP;
+    if (j0 + STEP < Tk) load_set(kB, vB, j0 + STEP);
+  }
+  if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
+    lo += dpp<kDppQuadXor2>(lo);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += dpp<kDppQuadXor2>(acc[e]);
+  }
+
+  // --- merge in the MFMA layout: lane (c, g) holds columns 16t + 4g + r -------
+  const float m_own = lane_get(mo, 4 * c), l_own = lane_get(lo, 4 * c);
+  const float M = fmaxf(m, m_own);
+  const float ao = (m_own == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m_own - M) * cl);
+  const float ap = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - M) * cl);
+  const float inv = 1.0f / (row_sum4(lp) * ap + l_own * ao);
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    // column 16t + 4g + r sits in own lane 4c + (16t + 4g) / EPL, element
+    // (16t + 4g) % EPL + r
+    const int src = 4 * c + (16 * t + 4 * g) / EPL;
+    const int sel = (4 * g % EPL) / 4;
+    float out[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float own = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < EPL / 4; ++s4) {
+        const float x = lane_get(acc[4 * s4 + r], src);
+        own = (s4 == sel) ? x : own;
+      }
+      out[r] = __builtin_fmaf(oacc[t][r], ap, own * ao) * inv;
+    }
+    if (cvalid)
+      store_vec<T, 4>(static_cast<T*>(a.y) + bc * a.yb + (int64_t)h * a.yh + 16 * t + 4 * g, out);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+namespace {
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <typename T, int D>
+int launch_shared(const SharedArgs& a, hipStream_t s) {
+  const int64_t blocks = (a.units + 3) / 4;
+  hipLaunchKernelGGL((attn_shared_kernel<T, D>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  return check_launch("attn_shared_kernel");
+}
+
+}  // namespace
+
+// The matrix-core path takes single-token decode over groups of at least 16
+// rows, head_dim 16 or 32, 16-byte aligned rows; everything else stays on the
+// vector kernel.
+bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, int prefix_len,
+                                 int group, const void* q, const dg_stride3* q_st, const void* k,
+                                 const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
+                                 const void* y, const dg_stride3* y_st) {
+  if (Tq != 1 || group < kSharedMinGroup || prefix_len < 1 || prefix_len > Tk) return false;
+  if (D != 16 && D != 32) return false;
+  if (dtype != DG_F32 && dtype != DG_BF16 && dtype != DG_F16) return false;
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  if (!al16(q) || !al16(k) || !al16(v) || !al16(y)) return false;
+  auto st16 = [&](int64_t st) { return (st * es) % 16 == 0; };
+  if (!st16(q_st->b) || !st16(q_st->h) || !st16(y_st->b) || !st16(y_st->h)) return false;
+  if (!st16(k_st->b) || !st16(k_st->t) || !st16(k_st->h)) return false;
+  if (!st16(v_st->b) || !st16(v_st->t) || !st16(v_st->h)) return false;
+  if (k_st->t < 0 || v_st->t < 0) return false;
+  if ((int64_t)Tk * k_st->t >= ((int64_t)1 << 31) || (int64_t)Tk * v_st->t >= ((int64_t)1 << 31)) return false;
+  const int64_t groups = ((int64_t)B + group - 1) / group;
+  const int64_t tiles = (group + 15) / 16;
+  const int64_t units = groups * tiles * H;
+  return units < ((int64_t)1 << 31) - 4;
+}
+
+int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
+                     const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
+                     void* y, const dg_stride3* y_st, float scale, int prefix_len, int group,
+                     const int* pos_dev, hipStream_t s) {
+  DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
+  SharedArgs a{};
+  a.q = q; a.k = k; a.v = v; a.y = y;
+  a.qb = q_st->b; a.qh = q_st->h;
+  a.kb = k_st->b; a.kt = k_st->t; a.kh = k_st->h;
+  a.vb = v_st->b; a.vt = v_st->t; a.vh = v_st->h;
+  a.yb = y_st->b; a.yh = y_st->h;
+  a.B = B; a.H = H; a.Tk = Tk; a.prefix_len = prefix_len; a.group = group;
+  a.tiles = (group + 15) / 16;
+  a.units = (((int64_t)B + group - 1) / group) * a.tiles * H;
+  a.scale_log2 = scale * 1.44269504088896340736f;
+  a.lazy_raw = kSharedLazyLog2 / a.scale_log2;
+  a.pos_dev = pos_dev;
+  if (dtype == DG_F32) return D == 16 ? launch_shared<float, 16>(a, s) : launch_shared<float, 32>(a, s);
+  if (dtype == DG_BF16) return D == 16 ? launch_shared<bf16_t, 16>(a, s) : launch_shared<bf16_t, 32>(a, s);
+  return D == 16 ? launch_shared<f16_t, 16>(a, s) : launch_shared<f16_t, 32>(a, s);
+}
+
+}  // namespace dg

@@ -54,78 +54,6 @@ struct AttnArgs {
 
 constexpr float kVecLazyLog2 = 8.0f;
 
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
-typedef _Float16 __attribute__((ext_vector_type(2))) f16x2v_t;
-
-// EPL elements of one row as raw 32-bit words (EPL*sizeof(T) bytes).
-template <typename T, int EPL>
-struct RowRegs {
-  static constexpr int BYTES = EPL * (int)sizeof(T);
-  static constexpr int WORDS = BYTES / 4;
-  static_assert(BYTES % 4 == 0, "row slice must be whole 32-bit words");
-  uint32_t w[WORDS];
-};
-
-template <typename T, int EPL>
-__device__ __forceinline__ void load_row(RowRegs<T, EPL>& r, const T* p) {
-  constexpr int W = RowRegs<T, EPL>::WORDS;
-  if constexpr (W % 4 == 0) {
-#pragma unroll
-    for (int c = 0; c < W / 4; ++c) {
-      const u32x4_t x = reinterpret_cast<const u32x4_t*>(p)[c];
-      r.w[4 * c] = x[0];
-      r.w[4 * c + 1] = x[1];
-      r.w[4 * c + 2] = x[2];
-      r.w[4 * c + 3] = x[3];
-    }
-  } else if constexpr (W == 2) {
-    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
-    r.w[0] = x[0];
-    r.w[1] = x[1];
-  } else {
-    static_assert(W == 1, "row slice width");
-    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
-  }
-}
-
-// Element e of the slice as fp32.
-template <typename T, int EPL>
-__device__ __forceinline__ float elem(const RowRegs<T, EPL>& r, int e) {
-  if constexpr (sizeof(T) == 4) {
-    return __uint_as_float(r.w[e]);
-  } else if constexpr (__is_same(T, bf16_t)) {
-    const uint32_t w = r.w[e >> 1];
-    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
-  } else {
-    const uint32_t w = r.w[e >> 1];
-    const uint16_t hbits = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
-    return (float)__builtin_bit_cast(_Float16, hbits);
-  }
-}
-
-// Partial dot product of the lane's slices of q and k.
-template <typename T, int EPL>
-__device__ __forceinline__ float slice_dot(const RowRegs<T, EPL>& q, const RowRegs<T, EPL>& k) {
-  float d = 0.f;
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(__uint_as_float(q.w[e]), __uint_as_float(k.w[e]), d);
-  } else if constexpr (__is_same(T, bf16_t)) {
-#pragma unroll
-    for (int w = 0; w < EPL / 2; ++w)
-      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, q.w[w]),
-                                          __builtin_bit_cast(bf16x2v_t, k.w[w]), d, false);
-  } else {
-#pragma unroll
-    for (int w = 0; w < EPL / 2; ++w)
-      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v_t, q.w[w]),
-                                 __builtin_bit_cast(f16x2v_t, k.w[w]), d, false);
-  }
-  return d;
-}
-
 template <typename T, int DPAD, int EPL, int U>
 __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   constexpr int LPK = DPAD / EPL;

@@ -53,6 +53,10 @@ __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
 }
 template <>
 __device__ __forceinline__ f16_t from_f32<f16_t>(float x) {
+  // x is materialised as an fp32 register first: otherwise the backend may fold
+  // the product that made x into the conversion (v_fma_mix*_f16), rounding
+  // once where fp32 arithmetic followed by .to(float16) rounds twice
+  asm("" : "+v"(x));
   _Float16 h = static_cast<_Float16>(x);  // v_cvt_f16_f32: round to nearest even
   f16_t r;
   r.bits = __builtin_bit_cast(uint16_t, h);
@@ -243,6 +247,84 @@ __device__ __forceinline__ float group_sum_dpp(float v) {
     v = a + b;
   }
   return v;
+}
+
+// ---------------------------------------------------------------------------
+// A lane's slice of one cache row: EPL consecutive elements held as raw
+// 32-bit words, loaded with 16/8/4-byte vector loads, and the partial dot
+// product of two such slices (fp32 FMAs, or v_dot2_f32_{bf16,f16} on the
+// packed 16-bit data: products of two 16-bit floats are exact in fp32).
+// ---------------------------------------------------------------------------
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
+typedef _Float16 __attribute__((ext_vector_type(2))) f16x2v_t;
+
+// EPL elements of one row as raw 32-bit words (EPL*sizeof(T) bytes).
+template <typename T, int EPL>
+struct RowRegs {
+  static constexpr int BYTES = EPL * (int)sizeof(T);
+  static constexpr int WORDS = BYTES / 4;
+  static_assert(BYTES % 4 == 0, "row slice must be whole 32-bit words");
+  uint32_t w[WORDS];
+};
+
+template <typename T, int EPL>
+__device__ __forceinline__ void load_row(RowRegs<T, EPL>& r, const T* p) {
+  constexpr int W = RowRegs<T, EPL>::WORDS;
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int c = 0; c < W / 4; ++c) {
+      const u32x4_t x = reinterpret_cast<const u32x4_t*>(p)[c];
+      r.w[4 * c] = x[0];
+      r.w[4 * c + 1] = x[1];
+      r.w[4 * c + 2] = x[2];
+      r.w[4 * c + 3] = x[3];
+    }
+  } else if constexpr (W == 2) {
+    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
+    r.w[0] = x[0];
+    r.w[1] = x[1];
+  } else {
+    static_assert(W == 1, "row slice width");
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+}
+
+// Element e of the slice as fp32.
+template <typename T, int EPL>
+__device__ __forceinline__ float elem(const RowRegs<T, EPL>& r, int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(r.w[e]);
+  } else if constexpr (__is_same(T, bf16_t)) {
+    const uint32_t w = r.w[e >> 1];
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    const uint32_t w = r.w[e >> 1];
+    const uint16_t hbits = (e & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+    return (float)__builtin_bit_cast(_Float16, hbits);
+  }
+}
+
+// Partial dot product of the lane's slices of q and k.
+template <typename T, int EPL>
+__device__ __forceinline__ float slice_dot(const RowRegs<T, EPL>& q, const RowRegs<T, EPL>& k) {
+  float d = 0.f;
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(__uint_as_float(q.w[e]), __uint_as_float(k.w[e]), d);
+  } else if constexpr (__is_same(T, bf16_t)) {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w)
+      d = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, q.w[w]),
+                                          __builtin_bit_cast(bf16x2v_t, k.w[w]), d, false);
+  } else {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w)
+      d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2v_t, q.w[w]),
+                                 __builtin_bit_cast(f16x2v_t, k.w[w]), d, false);
+  }
+  return d;
 }
 
 }  // namespace dg

@@ -77,18 +77,24 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
     load_vec<FT, EPL>(f, cs);
   }
 
+  // all three sources are read before anything is stored: the destinations
+  // may alias them as far as the compiler knows, so this order keeps the
+  // loads of q, k and v in flight together
+  float xs[3][EPL];
+#pragma unroll
+  for (int w = 0; w < 3; ++w) {
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) xs[w][i] = 0.f;
+    if (a.src[w] == nullptr || !active) continue;  // src: uniform over the grid
+    const T* s = static_cast<const T*>(a.src[w]) + b * a.sb[w] + (int64_t)t * a.st[w] +
+                 (int64_t)h * a.sh[w] + d0;
+    load_vec<T, EPL>(s, xs[w]);
+  }
+
 #pragma unroll
   for (int w = 0; w < 3; ++w) {
     if (a.src[w] == nullptr) continue;  // uniform over the grid
-    float x[EPL];
-    if (active) {
-      const T* s = static_cast<const T*>(a.src[w]) + b * a.sb[w] + (int64_t)t * a.st[w] +
-                   (int64_t)h * a.sh[w] + d0;
-      load_vec<T, EPL>(s, x);
-    } else {
-#pragma unroll
-      for (int i = 0; i < EPL; ++i) x[i] = 0.f;
-    }
+    float (&x)[EPL] = xs[w];
     if (w < 2) {
 #pragma unroll
       for (int p = 0; p < EPL / 2; ++p) {

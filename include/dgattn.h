@@ -125,11 +125,15 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * instead of row b; keys j >= prefix_len from row b itself.  This is the
  * decode attention of mha.py:65-68 over the cache that KVCache.prefill's
  * batch broadcast (kv_cache.py:77-79) leaves behind: every row of a group
- * holds the same first prefix_len positions, so the result is exactly
+ * holds the same first prefix_len positions, so the result is
  * dg_attention's, while the prefix is fetched from HBM about once per group
  * (rows of one group run on one XCD and hit its L2).  The caller guarantees
  * the identical prefixes.  group = 1 (or prefix_len = 0) is dg_attention.
- * Prefill launches that take the MFMA kernel read every row's own keys.
+ * Single-token decode with group >= 16, head_dim 16 or 32 and no key splits
+ * runs the prefix part as a matrix product on MFMA (fp32 products for fp32
+ * inputs): equal to dg_attention within the fp32 rounding of a different
+ * summation order.  Other shapes give dg_attention's bits exactly.  Prefill
+ * launches that take the MFMA kernel read every row's own keys.
  */
 DG_API int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype,
                                 const void* q, const dg_stride3* q_st,

@@ -185,12 +185,39 @@ def test_decode_without_workspace_matches_split(dev):
         assert err <= 2e-2
 
 
-GROUPED = [  # (B, group, H, prefix, Tk, D): cfg1 series of 100 rows, ragged last group
-    (300, 100, 4, 96, 144, 16),
+GROUPED = [  # (B, group, H, prefix, Tk, D)
     (10, 4, 2, 33, 70, 16),
     (12, 6, 8, 600, 1100, 64),
     (4, 2, 8, 1500, 2600, 128),
 ]
+# Groups of >= 16 rows with head_dim 16 / 32 take the matrix-core kernel
+# (dg_attn_shared.hip) whenever the vector kernel would not split the keys
+# (Tk < 256, or B*H >= 8192): cfg1 (series of 100 rows), a ragged last group,
+# a prefix not a multiple of 16 or spanning several 64-key chunks, one own
+# key, many own keys, no own key at all.
+GROUPED_MFMA = [
+    (300, 100, 4, 96, 144, 16),
+    (250, 100, 4, 96, 97, 16),
+    (70, 16, 2, 33, 70, 32),
+    (45, 20, 3, 150, 151, 16),
+    (40, 40, 2, 5, 250, 16),
+    (32, 16, 2, 50, 50, 32),
+    (17, 17, 1, 200, 250, 32),
+    (1100, 100, 8, 64, 260, 16),  # B*H >= 8192: no key splits at Tk >= 256 either
+]
+
+
+def _grouped_case(dtype, shape):
+    B, G, H, P, Tk, D = shape
+    cap = Tk + 3
+    groups = (B + G - 1) // G
+    pre = _randn((groups, 2, H, P, D), 70 + D, dtype)
+    own = _randn((B, 2, H, Tk - P, D), 71 + D, dtype)
+    cache = torch.empty((2, B, H, cap, D), dtype=TDT[dtype])
+    cache[:, :, :, :P] = pre.repeat_interleave(G, dim=0)[:B].transpose(0, 1)
+    cache[:, :, :, P:Tk] = own.transpose(0, 1)
+    q = _randn((B, 1, H, D), 72 + D, dtype)
+    return q, cache
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
@@ -202,14 +229,7 @@ def test_grouped_prefix_attention_equals_plain(dev, dtype, shape):
     from diff_gpt import _native
 
     B, G, H, P, Tk, D = shape
-    cap = Tk + 3
-    groups = (B + G - 1) // G
-    pre = _randn((groups, 2, H, P, D), 70 + D, dtype)
-    own = _randn((B, 2, H, Tk - P, D), 71 + D, dtype)
-    cache = torch.empty((2, B, H, cap, D), dtype=TDT[dtype])
-    cache[:, :, :, :P] = pre.repeat_interleave(G, dim=0)[:B].transpose(0, 1)
-    cache[:, :, :, P:Tk] = own.transpose(0, 1)
-    q = _randn((B, 1, H, D), 72 + D, dtype)
+    q, cache = _grouped_case(dtype, shape)
     cd, qd = cache.to(dev), q.to(dev)
     keys = cd[0, :, :, :Tk].transpose(1, 2)
     vals = cd[1, :, :, :Tk].transpose(1, 2)
@@ -220,6 +240,37 @@ def test_grouped_prefix_attention_equals_plain(dev, dtype, shape):
     ref = on.attention_f64(q.float().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy())
     err = np.abs(y_grp.float().cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", GROUPED_MFMA, ids=lambda s: "x".join(map(str, s)))
+def test_grouped_prefix_attention_mfma(dev, dtype, shape):
+    """The shared prefix on MFMA, own keys on the VALU: against fp64 at the
+    north-star bars, against the plain decode kernel within them, and the
+    device-position entry point (graph form) bit-identical to the eager call
+    at the same position."""
+    from diff_gpt import _native
+
+    B, G, H, P, Tk, D = shape
+    q, cache = _grouped_case(dtype, shape)
+    cd, qd = cache.to(dev), q.to(dev)
+    keys = cd[0, :, :, :Tk].transpose(1, 2)
+    vals = cd[1, :, :, :Tk].transpose(1, 2)
+    ops = _native.ops()
+    y_plain = ops.attention(qd, keys, vals, 1.0 / np.sqrt(D))
+    y_grp = ops.attention(qd, keys, vals, 1.0 / np.sqrt(D), P, G)
+    ref = on.attention_f64(q.float().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy())
+    scale = np.abs(ref).max()
+    err = np.abs(y_grp.float().cpu().numpy() - ref).max() / scale
+    assert err <= TOL[dtype], err
+    gap = (y_grp.float() - y_plain.float()).abs().max().item() / scale
+    assert gap <= TOL[dtype], gap
+    # graph form: positions 0 .. pos of the full-capacity cache views
+    y_at = torch.empty_like(qd)
+    pos = torch.tensor([Tk - 1], dtype=torch.int32, device=dev)
+    _native.decode_attention_at_(qd, cd[0].transpose(1, 2), cd[1].transpose(1, 2), y_at, 1.0 / np.sqrt(D),
+                                 pos, P, G)
+    assert torch.equal(y_at, y_grp)
 
 
 # ------------------------------------------------------------------ strided copy
