@@ -4,22 +4,24 @@ Default workload: 64 series x 100 trajectories =
 6400 concurrent sequences of the README GPT geometry (2 layers, 4 heads,
 head_dim 16), a shared 96-token prefix per series already broadcast into the
 KV cache, then 48 decode steps (L_kv 97..144).  One bench step = that whole
-decode job through the hot path: per decode step and layer, one fused
-RoPE + QK-norm + KV-append launch and one decode-attention launch, on
-synthetic q/k/v resident in HBM.
+decode job through the hot path: per decode step and layer, one
+dg_decode_step launch (RoPE + QK-norm + KV append + decode attention) on
+synthetic q/k/v projections resident in HBM.
 
     python bench.py [--steps K] [--warmup W] [--dtype fp32|bf16] [--no-prefill]
                     [--no-cpu-baseline] [--traffic-json FILE]
 
 Prints ONE JSON line.  value = sequences*48*K / timed seconds (tokens/s); the
-job's 192 launches are captured once in a HIP graph (as Engine captures its
-decode step) and the K timed steps are K graph replays.  roofline =
-decode-attention kernel: algorithmic bytes per launch over its mean launch
-time, timed with HIP events on the launch stream around K replays of a graph
-holding only the job's 96 decode-attention launches (so the graph's short
-gaps between kernels count as kernel time).  Bytes per launch:
-B*H*es*(2*L_kv*D + 2*D) in plain mode; in shared mode the prefix rows count
-once per series.  The prefill leg (configs[2]:
+job's 96 launches are captured once in a HIP graph (as Engine captures its
+decode step) and the K timed steps are K graph replays.  roofline = the
+decode-step kernel: algorithmic bytes per launch over its mean launch time,
+timed with HIP events on the launch stream around K replays of the graph (so
+the graph's short gaps between kernels count as kernel time).  Bytes per
+(row, head): es*(2*L_kv*D + 4*D) -- K+V of every visible position, q, y, the
+k/v projections read and appended; in shared mode the prefix rows count once
+per series.  The decode_unfused leg runs the same job as two launches per
+layer-step (RoPE/append, then attention) and reports the attention kernel
+alone (es*(2*L_kv*D + 2*D) per (row, head)).  The prefill leg (configs[2]:
 B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s with
 FLOP = 2*B*H*D*T*(T+1).  cpu_baseline = the oracle's torch-CPU restatement of
 the reference decode path on a bounded sample, on this host's cores.
@@ -53,7 +55,7 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
+def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, fused: bool = True):
     import torch
 
     from diff_gpt import _native
@@ -90,11 +92,25 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
     P = ctypes.pointer
     S3 = _native._bthd_strides
     packs = []
+    # shared: the 96-token prefix of each series is read from the series'
+    # first row (all 100 rows hold it, KVCache.prefill)
+    prefix_len, group = (PREFIX, TRAJ) if shared else (0, 1)
     for s in range(NEW):
         t0 = PREFIX + s
         fc = table[t0:t0 + 1].view(1, 1, 1, D // 2, 2)
         for layer in range(L):
             q, k, v = qkv[s, layer]
+            if fused:
+                # one launch: RoPE + QK-norm + append at t0 + attention over 0..t0
+                kc = cache[layer, 0].transpose(1, 2)
+                vc = cache[layer, 1].transpose(1, 2)
+                assert lib.dg_decode_step_workspace_size(B, H, cap, D, code) == 0
+                args = (B, H, D, code, _native._ptr(q), P(S3(q)), _native._ptr(k), P(S3(k)),
+                        _native._ptr(v), P(S3(v)), _native._ptr(kc), P(S3(kc)), _native._ptr(vc), P(S3(vc)),
+                        _native._ptr(table[t0]), 0, code, t0, None, cap, _native._ptr(y), P(S3(y)),
+                        0.25, prefix_len, group, _native.DG_QKNORM, None, 0, stream)
+                packs.append((None, args))
+                continue
             kd = cache[layer, 0, :, :, t0:t0 + 1].transpose(1, 2)
             vd = cache[layer, 1, :, :, t0:t0 + 1].transpose(1, 2)
             keys = cache[layer, 0, :, :, :t0 + 1].transpose(1, 2)
@@ -106,19 +122,17 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
                          _native._ptr(fc), P(_native.Stride3(0, 0, 0)), code, _native.DG_QKNORM, stream)
             ws = lib.dg_attention_workspace_size(B, H, 1, t0 + 1, D, code)
             assert ws == 0, "configs[1] decode runs without key splits"
-            # shared: the 96-token prefix of each series is read from the
-            # series' first row (all 100 rows hold it, KVCache.prefill)
-            prefix, group = (PREFIX, TRAJ) if shared else (0, 1)
             attn_args = (B, H, 1, t0 + 1, D, code,
                          _native._ptr(q_rot), P(S3(q_rot)), _native._ptr(keys), P(S3(keys)),
                          _native._ptr(vals), P(S3(vals)), _native._ptr(y), P(S3(y)),
-                         0.25, prefix, group, None, 0, stream)
+                         0.25, prefix_len, group, None, 0, stream)
             packs.append((rope_args, attn_args))
-    rope_fn, attn_fn = lib.dg_rope_qknorm_append, lib.dg_attention_grouped
+    rope_fn = lib.dg_rope_qknorm_append
+    attn_fn = lib.dg_decode_step if fused else lib.dg_attention_grouped
 
     def run(with_rope: bool):
         for rope_args, attn_args in packs:
-            if with_rope and rope_fn(*rope_args) != 0:
+            if with_rope and rope_args is not None and rope_fn(*rope_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
             if attn_fn(*attn_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
@@ -153,12 +167,17 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False):
     attn_s = a.elapsed_time(b) / 1e3
     mean_kernel_s = attn_s / launches
     # algorithmic bytes per launch, averaged over the job's L_kv = 97..144:
-    # K+V rows of every visible position, q, y; with a shared prefix the prefix rows count once per series (unique bytes)
+    # K+V rows of every visible position, q, y; the fused step also reads the
+    # k, v projections and writes them to the cache (and takes the new
+    # position's K+V from registers instead of the cache), + 2*D per (row,
+    # head) in all; with a shared prefix the prefix rows count once per series
+    # (unique bytes)
+    extra = 2 * D if fused else 0
     if shared:
-        bytes_job = sum(H * es * (2 * D * (PREFIX * SERIES + (s + 1) * B) + 2 * D * B)
+        bytes_job = sum(H * es * (2 * D * (PREFIX * SERIES + (s + 1) * B) + (2 * D + extra) * B)
                         for s in range(NEW)) * L
     else:
-        bytes_job = sum(B * H * es * (2 * (PREFIX + s + 1) * D + 2 * D) for s in range(NEW)) * L
+        bytes_job = sum(B * H * es * (2 * (PREFIX + s + 1) * D + 2 * D + extra) for s in range(NEW)) * L
     bytes_per_launch = bytes_job / (NEW * L)
     achieved = bytes_per_launch / mean_kernel_s / 1e9
     tokens = B * NEW * steps
@@ -408,6 +427,11 @@ def main():
     if not args.single_dtype:
         res_other = decode_job(other, max(1, args.steps // 2), 1, shared)
         log(f"decode {other} {args.decode_mode}: {res_other}")
+    res_unfused = None
+    if not args.single_mode:
+        # the same job as two launches per layer-step (RoPE/append, then attention)
+        res_unfused = decode_job(args.dtype, max(1, args.steps // 2), 1, shared, fused=False)
+        log(f"decode {args.dtype} {args.decode_mode} unfused: {res_unfused}")
     traffic = None
     tp = Path(args.traffic_json)
     if tp.exists():
@@ -461,6 +485,11 @@ def main():
             "mode": "plain" if shared else "shared", "tokens_per_s": res_mode["tokens_per_s"],
             "kernel_mean_us": res_mode["kernel_mean_us"],
             "achieved_gbs": res_mode["achieved_gbs"], "frac": res_mode["achieved_gbs"] / HBM_PEAK_GBS},
+        "decode_unfused": None if res_unfused is None else {
+            "tokens_per_s": res_unfused["tokens_per_s"], "ms_per_step": res_unfused["ms_per_step"],
+            "attention_kernel_mean_us": res_unfused["kernel_mean_us"],
+            "attention_achieved_gbs": res_unfused["achieved_gbs"],
+            "attention_frac": res_unfused["achieved_gbs"] / HBM_PEAK_GBS},
         "decode_other_dtype": None if res_other is None else {
             "dtype": other, "tokens_per_s": res_other["tokens_per_s"],
             "kernel_mean_us": res_other["kernel_mean_us"],

@@ -42,6 +42,17 @@ int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, cons
                      const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
                      void* y, const dg_stride3* y_st, float scale, int prefix_len, int group,
                      const int* pos_dev, hipStream_t s);
+bool shared_step_applicable(int B, int H, int D, int dtype, int prefix_len, int group, int max_pos,
+                            const void* q, const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
+                            const void* v, const dg_stride3* v_st, const void* kc, const dg_stride3* kc_st,
+                            const void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
+                            int fdtype, const void* y, const dg_stride3* y_st);
+int shared_decode_step(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, const void* k,
+                       const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
+                       const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs,
+                       int64_t fpos, int fdtype, int pos, const int* pos_dev, int max_pos, void* y,
+                       const dg_stride3* y_st, float scale, int prefix_len, int group, int qknorm,
+                       hipStream_t s);
 // dg_attn_mfma.hip
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
@@ -178,6 +189,69 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
   return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
                        scale, prefix_len, group, pos, workspace, workspace_bytes,
                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype) {
+  return dg_attention_workspace_size(B, H, 1, max_pos, D, dtype);
+}
+
+extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st,
+                              const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
+                              void* k_cache, const dg_stride3* kc_st, void* v_cache, const dg_stride3* vc_st,
+                              const void* freqs, int64_t freqs_pos_stride, int freqs_dtype, int pos,
+                              const int32_t* pos_dev, int max_pos, void* y, const dg_stride3* y_st,
+                              float scale, int prefix_len, int group, int flags, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "decode_step: negative size");
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "decode_step: dtype %d unsupported", dtype);
+  DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == DG_BF16 || freqs_dtype == DG_F16, DG_EUNSUPPORTED,
+             "decode_step: freqs dtype %d unsupported", freqs_dtype);
+  DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "decode_step: head_dim must be even (got %d)", D);
+  DG_REQUIRE(max_pos >= 1, DG_EINVAL, "decode_step: max_pos must be >= 1 (got %d)", max_pos);
+  DG_REQUIRE(group >= 1, DG_EINVAL, "decode_step: group must be >= 1 (got %d)", group);
+  DG_REQUIRE(prefix_len >= 0 && prefix_len <= max_pos, DG_EINVAL,
+             "decode_step: prefix_len %d outside [0, max_pos=%d]", prefix_len, max_pos);
+  DG_REQUIRE(freqs_pos_stride >= 0, DG_EINVAL, "decode_step: negative freqs_pos_stride");
+  if (pos_dev == nullptr) {
+    DG_REQUIRE(pos >= 0 && pos < max_pos, DG_EINVAL, "decode_step: position %d outside [0, max_pos=%d)", pos,
+               max_pos);
+    DG_REQUIRE(group == 1 || prefix_len <= pos, DG_EINVAL,
+               "decode_step: position %d inside the shared prefix (prefix_len %d)", pos, prefix_len);
+  }
+  if ((int64_t)B * H == 0) return DG_OK;
+  DG_REQUIRE(q && k && v && k_cache && v_cache && freqs && y && q_st && k_st && v_st && kc_st && vc_st && y_st,
+             DG_EINVAL, "decode_step: NULL argument");
+  if (group == 1) prefix_len = 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int qknorm = (flags & DG_QKNORM) ? 1 : 0;
+  if (vec_attention_splits(B, H, 1, max_pos, D) == 1 &&
+      shared_step_applicable(B, H, D, dtype, prefix_len, group, max_pos, q, q_st, k, k_st, v, v_st, k_cache,
+                             kc_st, v_cache, vc_st, freqs, freqs_pos_stride, freqs_dtype, y, y_st))
+    return shared_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, k_cache, kc_st, v_cache, vc_st, freqs,
+                              freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, prefix_len,
+                              group, qknorm, s);
+  // Two launches: RoPE/QK-norm/append with the rotated q staged in y, then the
+  // attention reading q from y (every attention kernel reads a query row
+  // before it writes the output row at the same place).
+  int rc;
+  if (pos_dev != nullptr) {
+    rc = dg_rope_qknorm_append_at(B, H, D, dtype, q, q_st, y, y_st, k, k_st, k_cache, kc_st, v, v_st, v_cache,
+                                  vc_st, freqs, freqs_pos_stride, freqs_dtype, pos_dev, max_pos, flags, stream);
+    if (rc != DG_OK) return rc;
+    return dg_decode_attention_at(B, H, D, dtype, y, y_st, k_cache, kc_st, v_cache, vc_st, y, y_st, scale,
+                                  prefix_len, group, pos_dev, max_pos, workspace, workspace_bytes, stream);
+  }
+  const int64_t es = dtype == DG_F32 ? 4 : 2, fes = freqs_dtype == DG_F32 ? 4 : 2;
+  const dg_stride3 f_st = {0, 0, 0};
+  rc = dg_rope_qknorm_append(B, 1, H, D, dtype, q, q_st, y, y_st, k, k_st,
+                             static_cast<char*>(k_cache) + (int64_t)pos * kc_st->t * es, kc_st, v, v_st,
+                             static_cast<char*>(v_cache) + (int64_t)pos * vc_st->t * es, vc_st,
+                             static_cast<const char*>(freqs) + (int64_t)pos * freqs_pos_stride * fes, &f_st,
+                             freqs_dtype, flags, stream);
+  if (rc != DG_OK) return rc;
+  return dg_attention_grouped(B, H, 1, pos + 1, D, dtype, y, y_st, k_cache, kc_st, v_cache, vc_st, y, y_st, scale,
+                              prefix_len, group, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,

@@ -31,13 +31,20 @@
 //   lanes of a row merge at the end (max, rescale, then a two-step
 //   reduce-scatter with v_permlane32_swap / v_permlane16_swap that leaves each
 //   lane the columns its O^T registers hold).
-#include "dg_common.h"
+//
+// Fused decode step (FUSED = true; mha.py:44-68 for one new token): the same
+// kernel first applies RoPE and QK-norm to the step's q and k projections
+// (the arithmetic of rope_qknorm_kernel, shared through dg_rope_math.h),
+// appends k and v to the cache at position pos (kv_cache.py:108-109), and
+// attends over positions 0 .. pos, taking the new key and value from
+// registers: one launch per layer-step instead of two.
+#include "dg_rope_math.h"
 
 namespace dg {
 
 struct SharedArgs {
-  const void* q;
-  const void* k;
+  const void* q;  // attention q (unfused), or the step's q projection (fused)
+  const void* k;  // cache pages (keys at position t: k + b*kb + t*kt + h*kh)
   const void* v;
   void* y;
   int64_t qb, qh;
@@ -45,11 +52,21 @@ struct SharedArgs {
   int64_t vb, vt, vh;
   int64_t yb, yh;
   int64_t units;  // ceil(B / group) * tiles * H
-  int B, H, Tk, prefix_len, group, tiles;
+  int B, H, D, Tk, prefix_len, group, tiles;
   float scale_log2;  // scale * log2(e)
   float lazy_raw;    // kSharedLazyLog2 / scale_log2
   // graph-replayable form: keys are positions 0 .. *pos_dev, at most Tk
   const int* pos_dev;
+  // fused step: projections of the new token (B,1,H,D) and the RoPE table at
+  // position 0 with fpos elements per position; the new token goes to
+  // position pos (Tk = pos + 1), or *pos_dev when set; nothing is computed or
+  // written when that position is outside [0, max_pos)
+  const void* kp;
+  const void* vp;
+  int64_t kpb, kph, vpb, vph;
+  const void* freqs;
+  int64_t fpos;
+  int pos, max_pos, qknorm;
 };
 
 constexpr float kSharedLazyLog2 = 8.0f;
@@ -120,8 +137,37 @@ struct OwnCfg {
 __device__ __forceinline__ float lane_get(float x, int src) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
 }
+__device__ __forceinline__ uint32_t lane_get_u(uint32_t x, int src) {
+  return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)x);
+}
 
-template <typename T, int D>
+// EPL fp32 values rounded to T and packed as the raw words of a row slice.
+template <typename T, int EPL>
+__device__ __forceinline__ void pack_row(RowRegs<T, EPL>& r, const float (&x)[EPL]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) r.w[e] = __float_as_uint(x[e]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w)
+      r.w[w] = (uint32_t)from_f32<T>(x[2 * w]).bits | ((uint32_t)from_f32<T>(x[2 * w + 1]).bits << 16);
+  }
+}
+
+template <typename T, int EPL>
+__device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
+  constexpr int W = RowRegs<T, EPL>::WORDS;
+  static_assert(W % 4 == 0 || W == 2, "row slice width");
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int c4 = 0; c4 < W / 4; ++c4)
+      reinterpret_cast<u32x4_t*>(p)[c4] = u32x4_t{r.w[4 * c4], r.w[4 * c4 + 1], r.w[4 * c4 + 2], r.w[4 * c4 + 3]};
+  } else {
+    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{r.w[0], r.w[1]};
+  }
+}
+
+template <typename T, int D, bool FUSED, typename FT>
 __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
   constexpr int DQ = D / 4;   // contraction elements per lane and key tile
   constexpr int DT = D / 16;  // 16-column tiles of the output
@@ -151,35 +197,69 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
     return ok ? b0 + rin : b0;
   };
 
-  int Tk = a.Tk;
-  if (a.pos_dev != nullptr) Tk = min(*a.pos_dev + 1, a.Tk);
-  const int P = min(a.prefix_len, Tk);
+  // keys 0 .. Tk-1; the fused step appends key Tk-1 = pos and takes it from
+  // registers, so the cache is read for keys below Tc only
+  int Tk, Tc;
+  if constexpr (FUSED) {
+    const int pos = a.pos_dev != nullptr ? *a.pos_dev : a.pos;
+    if (pos < 0 || pos >= a.max_pos) return;  // uniform over the grid
+    Tk = pos + 1;
+    Tc = pos;
+  } else {
+    Tk = a.Tk;
+    if (a.pos_dev != nullptr) Tk = min(*a.pos_dev + 1, a.Tk);
+    Tc = Tk;
+  }
+  const int P = min(a.prefix_len, Tc);
   const float cl = a.scale_log2;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
   const T* kbase = static_cast<const T*>(a.k) + (int64_t)h * a.kh;
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)h * a.vh;
   const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * a.qh;
 
-  // --- own keys: quad layout, first two register sets loaded up front --------
+  // --- own keys: quad layout -------------------------------------------------
   const int orow = lane >> 2, kk = (lane & 3) / LPK, piece = (lane & 3) % LPK;
   bool ovalid;
   const int64_t bo = row_of(orow, ovalid);
+  Slice qs;  // the attention query of row orow (this lane's EPL elements)
+  Slice knew, vnew;  // fused: the appended key and value
+  if constexpr (FUSED) {
+    // RoPE + QK-norm of the new token (mha.py:44-48), rounded to T as the
+    // standalone kernel stores it, then the append (kv_cache.py:108-109)
+    float xq[EPL], xk[EPL], cs[EPL];
+    load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
+    load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
+    load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
+    load_vec<FT, EPL>(static_cast<const FT*>(a.freqs) + (int64_t)Tc * a.fpos + piece * EPL, cs);
+    rope_rotate<T, EPL>(xq, cs);
+    rope_rotate<T, EPL>(xk, cs);
+    if (a.qknorm) {
+      qk_rms_norm<EPL, LPK>(xq, D);
+      qk_rms_norm<EPL, LPK>(xk, D);
+    }
+    pack_row<T, EPL>(qs, xq);
+    pack_row<T, EPL>(knew, xk);
+    if (ovalid && kk == 0) {
+      store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
+      store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
+    }
+  } else {
+    load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
+  }
   const T* kown = kbase + bo * a.kb + piece * EPL;
   const T* vown = vbase + bo * a.vb + piece * EPL;
-  Slice qs;
-  load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
   Slice kA[UO], vA[UO], kB[UO], vB[UO];
   auto load_set = [&](Slice (&kr)[UO], Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < UO; ++u) {
-      if (j0 + KPQ * u >= Tk) break;  // wave-uniform
-      const int j = min(j0 + KPQ * u + kk, Tk - 1);  // past Tk: a valid row, masked below
+      if (j0 + KPQ * u >= Tc) break;  // wave-uniform
+      const int j = min(j0 + KPQ * u + kk, Tc - 1);  // past Tc: a valid row, masked below
       load_row<T, EPL>(kr[u], kown + j * kt);
       load_row<T, EPL>(vr[u], vown + j * vt);
     }
   };
-  if (P < Tk) load_set(kA, vA, P);
-  if (P + STEP < Tk) load_set(kB, vB, P + STEP);
+  if (P < Tc) load_set(kA, vA, P);
+  if (P + STEP < Tc) load_set(kB, vB, P + STEP);
 
   // --- prefix on MFMA: lane (c, g) ---------------------------------------------
   const int c = lane & 15, g = lane >> 4;
@@ -187,8 +267,26 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
   const int64_t bc = row_of(c, cvalid);
   const T* kpre = kbase + b0 * a.kb;
   const T* vpre = vbase + b0 * a.vb;
-  Op qop;
-  load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
+  Op qop;  // q row c, elements g*DQ .. g*DQ + DQ - 1
+  if constexpr (FUSED) {
+    // gathered from the quad layout: own lane 4c + (g*DQ)/EPL (key lane 0)
+    // holds them at word (g*DQ % EPL) * sizeof(T) / 4 of its slice
+    constexpr int OPW = Op::WORDS, SW = Slice::WORDS;
+    const int src = 4 * c + (g * DQ) / EPL;
+    const int wo = ((g * DQ) % EPL) * (int)sizeof(T) / 4;
+#pragma unroll
+    for (int w = 0; w < OPW; ++w) {
+      uint32_t x = 0;
+#pragma unroll
+      for (int cand = 0; cand + OPW <= SW; cand += OPW) {
+        const uint32_t y = lane_get_u(qs.w[cand + w], src);
+        x = (wo == cand) ? y : x;
+      }
+      qop.w[w] = x;
+    }
+  } else {
+    load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
+  }
   float m = kNegInf, lp = 0.f;
   f32x4_t oacc[DT];
 #pragma unroll
@@ -252,18 +350,10 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
   float acc[EPL];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
-    float sv[UO];
-    float mt = kNegInf;
-#pragma unroll
-    for (int u = 0; u < UO; ++u) {
-      sv[u] = kNegInf;
-      if (j0 + KPQ * u >= Tk) continue;  // slot not loaded (wave-uniform)
-      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
-      sv[u] = (j0 + KPQ * u + kk < Tk) ? dot : kNegInf;
-      mt = fmaxf(mt, sv[u]);
-    }
-    if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));  // one offset per quad
+  // raise the quad's offset to mt when a score exceeds it by more than the
+  // lazy margin (one offset per quad row)
+  auto raise_offset = [&](float mt) __attribute__((always_inline)) {
+    if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
     if (mt > mo + a.lazy_raw) {
       const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
       mo = mt;
@@ -271,24 +361,46 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
     }
+  };
+  auto add_key = [&](float score, const Slice& vr, float moff) __attribute__((always_inline)) {
+    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(score, cl, -moff));
+    lo += p;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr, e), acc[e]);
+  };
+  auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
+    float sv[UO];
+    float mt = kNegInf;
+#pragma unroll
+    for (int u = 0; u < UO; ++u) {
+      sv[u] = kNegInf;
+      if (j0 + KPQ * u >= Tc) continue;  // slot not loaded (wave-uniform)
+      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
+      sv[u] = (j0 + KPQ * u + kk < Tc) ? dot : kNegInf;
+      mt = fmaxf(mt, sv[u]);
+    }
+    raise_offset(mt);
     const float moff = mo * cl;
 #pragma unroll
     for (int u = 0; u < UO; ++u) {
-      if (j0 + KPQ * u >= Tk) continue;
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[u], cl, -moff));
-      lo += p;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr[u], e), acc[e]);
+      if (j0 + KPQ * u >= Tc) continue;
+      add_key(sv[u], vr[u], moff);
     }
   };
-  for (int j0 = P; j0 < Tk;) {
+  for (int j0 = P; j0 < Tc;) {
     process(kA, vA, j0);
     j0 += STEP;
-    if (j0 + STEP < Tk) load_set(kA, vA, j0 + STEP);
-    if (j0 >= Tk) break;
+    if (j0 + STEP < Tc) load_set(kA, vA, j0 + STEP);
+    if (j0 >= Tc) break;
     process(kB, vB, j0);
     j0 += STEP;
-    if (j0 + STEP < Tk) load_set(kB, vB, j0 + STEP);
+    if (j0 + STEP < Tc) load_set(kB, vB, j0 + STEP);
+  }
+  if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
+    const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
+    const float sn = kk == 0 ? dot : kNegInf;
+    raise_offset(sn);
+    add_key(sn, vnew, mo * cl);
   }
   if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
     lo += dpp<kDppQuadXor2>(lo);
@@ -331,11 +443,32 @@ namespace {
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-template <typename T, int D>
+template <typename T, int D, bool FUSED, typename FT>
 int launch_shared(const SharedArgs& a, hipStream_t s) {
   const int64_t blocks = (a.units + 3) / 4;
-  hipLaunchKernelGGL((attn_shared_kernel<T, D>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_shared_kernel<T, D, FUSED, FT>), dim3((unsigned)blocks), dim3(256), 0, s, a);
   return check_launch("attn_shared_kernel");
+}
+
+template <typename T, bool FUSED, typename FT>
+int launch_shared_d(const SharedArgs& a, hipStream_t s) {
+  return a.D == 16 ? launch_shared<T, 16, FUSED, FT>(a, s) : launch_shared<T, 32, FUSED, FT>(a, s);
+}
+
+void fill_common(SharedArgs& a, int B, int H, int D, int Tk, const void* q, const dg_stride3* q_st,
+                 const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+                 const dg_stride3* y_st, float scale, int prefix_len, int group, const int* pos_dev) {
+  a.q = q; a.k = k; a.v = v; a.y = y;
+  a.qb = q_st->b; a.qh = q_st->h;
+  a.kb = k_st->b; a.kt = k_st->t; a.kh = k_st->h;
+  a.vb = v_st->b; a.vt = v_st->t; a.vh = v_st->h;
+  a.yb = y_st->b; a.yh = y_st->h;
+  a.B = B; a.H = H; a.D = D; a.Tk = Tk; a.prefix_len = prefix_len; a.group = group;
+  a.tiles = (group + 15) / 16;
+  a.units = (((int64_t)B + group - 1) / group) * a.tiles * H;
+  a.scale_log2 = scale * 1.44269504088896340736f;
+  a.lazy_raw = kSharedLazyLog2 / a.scale_log2;
+  a.pos_dev = pos_dev;
 }
 
 }  // namespace
@@ -370,20 +503,49 @@ int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, cons
                      const int* pos_dev, hipStream_t s) {
   DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
   SharedArgs a{};
-  a.q = q; a.k = k; a.v = v; a.y = y;
-  a.qb = q_st->b; a.qh = q_st->h;
-  a.kb = k_st->b; a.kt = k_st->t; a.kh = k_st->h;
-  a.vb = v_st->b; a.vt = v_st->t; a.vh = v_st->h;
-  a.yb = y_st->b; a.yh = y_st->h;
-  a.B = B; a.H = H; a.Tk = Tk; a.prefix_len = prefix_len; a.group = group;
-  a.tiles = (group + 15) / 16;
-  a.units = (((int64_t)B + group - 1) / group) * a.tiles * H;
-  a.scale_log2 = scale * 1.44269504088896340736f;
-  a.lazy_raw = kSharedLazyLog2 / a.scale_log2;
-  a.pos_dev = pos_dev;
-  if (dtype == DG_F32) return D == 16 ? launch_shared<float, 16>(a, s) : launch_shared<float, 32>(a, s);
-  if (dtype == DG_BF16) return D == 16 ? launch_shared<bf16_t, 16>(a, s) : launch_shared<bf16_t, 32>(a, s);
-  return D == 16 ? launch_shared<f16_t, 16>(a, s) : launch_shared<f16_t, 32>(a, s);
+  fill_common(a, B, H, D, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len, group, pos_dev);
+  if (dtype == DG_F32) return launch_shared_d<float, false, float>(a, s);
+  if (dtype == DG_BF16) return launch_shared_d<bf16_t, false, bf16_t>(a, s);
+  return launch_shared_d<f16_t, false, f16_t>(a, s);
+}
+
+// The fused decode step takes what shared_attention takes, with the cache as
+// (B, max_pos, H, D) pages, plus 16-byte aligned projection rows and RoPE
+// table rows (table dtype: the data's or fp32).
+bool shared_step_applicable(int B, int H, int D, int dtype, int prefix_len, int group, int max_pos,
+                            const void* q, const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
+                            const void* v, const dg_stride3* v_st, const void* kc, const dg_stride3* kc_st,
+                            const void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
+                            int fdtype, const void* y, const dg_stride3* y_st) {
+  if (!shared_attention_applicable(B, H, 1, max_pos, D, dtype, prefix_len, group, q, q_st, kc, kc_st, vc,
+                                   vc_st, y, y_st))
+    return false;
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  const int64_t fes = fdtype == DG_F32 ? 4 : 2;
+  if (fdtype != dtype && fdtype != DG_F32) return false;
+  auto st16 = [&](int64_t st, int64_t e) { return (st * e) % 16 == 0; };
+  if (!al16(k) || !al16(v) || !al16(freqs)) return false;
+  if (!st16(k_st->b, es) || !st16(k_st->h, es) || !st16(v_st->b, es) || !st16(v_st->h, es)) return false;
+  return fpos >= 0 && st16(fpos, fes);
+}
+
+int shared_decode_step(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, const void* k,
+                       const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
+                       const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs,
+                       int64_t fpos, int fdtype, int pos, const int* pos_dev, int max_pos, void* y,
+                       const dg_stride3* y_st, float scale, int prefix_len, int group, int qknorm,
+                       hipStream_t s) {
+  DG_REQUIRE(scale > 0.f, DG_EINVAL, "decode_step: scale must be positive (got %g)", (double)scale);
+  SharedArgs a{};
+  fill_common(a, B, H, D, max_pos, q, q_st, kc, kc_st, vc, vc_st, y, y_st, scale, prefix_len, group, pos_dev);
+  a.kp = k; a.vp = v;
+  a.kpb = k_st->b; a.kph = k_st->h; a.vpb = v_st->b; a.vph = v_st->h;
+  a.freqs = freqs; a.fpos = fpos;
+  a.pos = pos; a.max_pos = max_pos; a.qknorm = qknorm;
+  if (dtype == DG_F32) return launch_shared_d<float, true, float>(a, s);
+  if (dtype == DG_BF16)
+    return fdtype == DG_F32 ? launch_shared_d<bf16_t, true, float>(a, s) : launch_shared_d<bf16_t, true, bf16_t>(a, s);
+  return fdtype == DG_F32 ? launch_shared_d<f16_t, true, float>(a, s) : launch_shared_d<f16_t, true, f16_t>(a, s);
 }
 
 }  // namespace dg

@@ -17,9 +17,7 @@
 //     mean = sum / D, r = 1 / sqrt(mean + FLT_EPSILON) with correctly rounded
 //     sqrt and divide, y = x * r.
 //   * The V half of the append is an exact copy.
-#include "dg_common.h"
-
-#include <float.h>
+#include "dg_rope_math.h"
 
 namespace dg {
 
@@ -96,27 +94,8 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
     if (a.src[w] == nullptr) continue;  // uniform over the grid
     float (&x)[EPL] = xs[w];
     if (w < 2) {
-#pragma unroll
-      for (int p = 0; p < EPL / 2; ++p) {
-        const float re = x[2 * p], im = x[2 * p + 1];
-        const float c = cs[2 * p], sn = cs[2 * p + 1];
-        const float a0 = re * c, a1 = im * sn;
-        const float b0 = re * sn, b1 = im * c;
-        // rounding to the storage dtype happens here (type_as), before the norm
-        x[2 * p] = to_f32(from_f32<T>(a0 - a1));
-        x[2 * p + 1] = to_f32(from_f32<T>(b0 + b1));
-      }
-      if (a.qknorm) {
-        float sq[EPL];
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) sq[i] = x[i] * x[i];
-        float ss = tree_sum<EPL>(sq);
-        ss = group_sum<LPK>(ss);
-        const float mean = ss / (float)a.D;
-        const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
-#pragma unroll
-        for (int i = 0; i < EPL; ++i) x[i] = x[i] * r;
-      }
+      rope_rotate<T, EPL>(x, cs);
+      if (a.qknorm) qk_rms_norm<EPL, LPK>(x, a.D);
     }
     if (active) {
       T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + b * a.db[w] + (int64_t)t * a.dt[w] +

@@ -77,6 +77,15 @@ _SIGNATURES = {
         + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
+    "dg_decode_step_workspace_size": (ctypes.c_size_t, [ctypes.c_int] * 5),
+    "dg_decode_step": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 5  # q, k, v, k_cache, v_cache
+        + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.c_int, ctypes.c_int,
+           ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
+    ),
     "dg_rms_norm": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
@@ -328,6 +337,58 @@ def decode_attention_at_(
         _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "decode_attention_at")
+
+
+def decode_step_(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    freqs: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    y: torch.Tensor,
+    scale: float,
+    pos: int | torch.Tensor,
+    prefix_len: int = 0,
+    group: int = 1,
+    qknorm: bool = True,
+) -> None:
+    """dg_decode_step: RoPE + QK-norm of the step's q, k (B,1,H,D), the K/V
+    append at position p of the (B,Tcap,H,D) cache views (at position 0), and
+    the decode attention over positions 0 .. p into y (B,1,H,D).  pos is p as a
+    Python int, with freqs the (D/2, 2) (cos, sin) row of position p; or a
+    one-element int32 device tensor holding p, with freqs the whole contiguous
+    (Tmax, D/2, 2) table."""
+    B, T, H, D = q.shape
+    if T != 1 or k.shape != q.shape or v.shape != q.shape or y.shape != q.shape:
+        raise ValueError("decode_step: q, k, v, y must be (B, 1, H, D)")
+    if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2:] != (H, D) or v_cache.shape != k_cache.shape:
+        raise ValueError("decode_step: cache views must be (B, Tcap, H, D)")
+    max_pos = k_cache.size(1)
+    if isinstance(pos, torch.Tensor):
+        if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != q.device:
+            raise TypeError("decode_step: a device position must be a one-element int32 tensor on q's device")
+        if freqs.dim() != 3 or freqs.shape[1:] != (D // 2, 2) or not freqs.is_contiguous():
+            raise ValueError("decode_step: with a device position freqs must be the contiguous (Tmax, D/2, 2) table")
+        fstride, pos_host, pos_ptr = freqs.stride(0), 0, _ptr(pos)
+        max_pos = min(max_pos, freqs.size(0))
+    else:
+        if freqs.numel() != D or not freqs.is_contiguous():
+            raise ValueError("decode_step: with a host position freqs must be the contiguous (cos, sin) row of it")
+        fstride, pos_host, pos_ptr = 0, int(pos), None
+    code = _dtype_code(q)
+    L = lib()
+    ws_bytes = L.dg_decode_step_workspace_size(B, H, max_pos, D, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
+    rc = L.dg_decode_step(
+        B, H, D, code, _ptr(q), st(q), _ptr(k), st(k), _ptr(v), st(v),
+        _ptr(k_cache), st(k_cache), _ptr(v_cache), st(v_cache),
+        _ptr(freqs), fstride, _dtype_code(freqs), pos_host, pos_ptr, max_pos,
+        _ptr(y), st(y), float(scale), int(prefix_len), int(group), DG_QKNORM if qknorm else 0,
+        _ptr(ws), ws_bytes, _stream(q),
+    )
+    _check(rc, "decode_step")
 
 
 def rms_norm_(x: torch.Tensor, out: torch.Tensor) -> None:

@@ -10,6 +10,11 @@ nn.Linear.  Everything between the projections and the gate runs in libdgattn:
                                        chunked prefill (mha.py:61-81), written
                                        straight into the (B,T,H*D) layout that
                                        mha.py:83 re-assembles.
+
+A decode step over a KV cache (one new token per row) makes one
+dg_decode_step call instead: the same RoPE, QK-norm and append, and the
+attention over the cache including the new token, in one launch where the
+rows share a broadcast prefix (two launches otherwise).
 """
 
 import math
@@ -61,9 +66,10 @@ class MultiHeadAttention(nn.Module):
         v = self.c_v(x).view(B, T, H, D)
         g = self.c_g(x)
 
+        if kv_cache is not None and T == 1:
+            return self._decode_step(q, k, v, g, freqs_cis, kv_cache)
+        assert kv_cache is None or kv_cache.pos_dev is None, "a captured decode step takes one token per row"
         q_rot = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
-        if kv_cache is not None and kv_cache.pos_dev is not None:
-            return self._decode_step_at(q, k, v, g, q_rot, freqs_cis, kv_cache)
         if kv_cache is None:
             # no cache: normalised keys go to a scratch tensor, values are read
             # in place from the projection output
@@ -94,23 +100,29 @@ class MultiHeadAttention(nn.Module):
         y = y * torch.sigmoid(g)
         return self.c_proj(y)
 
-    def _decode_step_at(self, q, k, v, g, q_rot, freqs_table, kv_cache: KVCache) -> torch.Tensor:
-        """One decode token per row with the position read on the device
-        (kv_cache.pos_dev): the same arithmetic as forward(), in the launch form
-        a HIP graph can replay at every position.  freqs_table is the model's
-        whole (Tmax, D/2, 2) table."""
+    def _decode_step(self, q, k, v, g, freqs, kv_cache: KVCache) -> torch.Tensor:
+        """One new token per row over the KV cache (mha.py:44-68 with T = 1):
+        dg_decode_step appends k, v at the cache position and attends over it.
+        With kv_cache.pos_dev set the position is read on the device (the
+        launch form a HIP graph replays at every position) and freqs is the
+        model's whole (Tmax, D/2, 2) table; otherwise freqs is the row of the
+        current position."""
         B, T, H, D = q.shape
-        assert T == 1, "a captured decode step takes one token per row"
         t0, t1 = kv_cache.ensure_window(1, k.dtype, k.device)
         cache = kv_cache.kv_cache
-        assert cache.size(4) >= t1, "the cache must not grow inside a captured decode step"
+        if cache.dtype != k.dtype:
+            raise TypeError(f"KV cache holds {cache.dtype} but the layer computes in {k.dtype}")
+        if kv_cache.pos_dev is not None:
+            assert cache.size(4) >= t1, "the cache must not grow inside a captured decode step"
+            pos = kv_cache.pos_dev
+        else:
+            pos = t0
         k_cache = cache[self.layer_idx, 0].transpose(1, 2)  # (B, Tcap, H, D) at position 0
         v_cache = cache[self.layer_idx, 1].transpose(1, 2)
-        _native.rope_qknorm_append_at_(q, k, v, freqs_table, q_rot, k_cache, v_cache, kv_cache.pos_dev, True)
-        kv_cache.advance(self.layer_idx, t1)
+        # a broadcast prefix (KVCache.prefill) is read once per row group
         prefix_len, group = (0, 1) if kv_cache.shared_prefix is None else kv_cache.shared_prefix
-        y = torch.empty_like(q_rot)
-        _native.decode_attention_at_(q_rot, k_cache, v_cache, y, 1.0 / math.sqrt(D), kv_cache.pos_dev,
-                                     prefix_len, group)
+        y = torch.empty_like(q)
+        _native.decode_step_(q, k, v, freqs, k_cache, v_cache, y, 1.0 / math.sqrt(D), pos, prefix_len, group)
+        kv_cache.advance(self.layer_idx, t1)
         y = y.view(B, T, H * D) * torch.sigmoid(g)
         return self.c_proj(y)

@@ -182,6 +182,40 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step of a layer, fused: dg_rope_qknorm_append with T = 1 at
+ * position p (mha.py:44-56, kv_cache.py:108-109) followed by
+ * dg_attention_grouped with Tq = 1 over positions 0 .. p (mha.py:65-68).
+ * q, k, v are the step's projections (B,1,H,D); k_cache / v_cache the cache
+ * pages at position 0 viewed as (B,max_pos,H,D); freqs the (cos, sin) row of
+ * position 0 with freqs_pos_stride elements per position (0: freqs already
+ * points at position p's row); y (B,1,H,D) receives the attention output.
+ * p = *pos_dev when pos_dev != NULL (graph-replayable: nothing is written when
+ * *pos_dev is outside [0, max_pos)), else p = pos, which must lie in
+ * [0, max_pos) and at or past prefix_len when group > 1.
+ *
+ * With a shared prefix (group >= 16, D 16 or 32) this is one launch: the new
+ * key and value are appended and also used from registers.  The cache
+ * contents are those of dg_rope_qknorm_append bit for bit; y equals the
+ * two-call result within fp32 rounding (the new key is accumulated last).
+ * Other shapes run the two calls, with the rotated q staged in y.  The
+ * workspace (dg_decode_step_workspace_size) serves the second call's key
+ * splits; NULL runs it without splits.
+ */
+DG_API size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype);
+
+DG_API int dg_decode_step(int B, int H, int D, int dtype,
+                          const void* q, const dg_stride3* q_st,
+                          const void* k, const dg_stride3* k_st,
+                          const void* v, const dg_stride3* v_st,
+                          void* k_cache, const dg_stride3* kc_st,
+                          void* v_cache, const dg_stride3* vc_st,
+                          const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
+                          int pos, const int32_t* pos_dev, int max_pos,
+                          void* y, const dg_stride3* y_st, float scale,
+                          int prefix_len, int group, int flags,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with
  * eps=None, i.e. FLT_EPSILON, computed in fp32 and rounded once to dtype).
  * x and out are M rows of N elements with row strides x_ld / out_ld.

@@ -19,7 +19,7 @@ def test_header_declares_the_entry_points():
     syms = _declared_symbols()
     assert {"dg_abi_version", "dg_last_error", "dg_rope_qknorm_append", "dg_attention",
             "dg_attention_grouped", "dg_attention_workspace_size", "dg_rms_norm",
-            "dg_copy4d"} <= set(syms)
+            "dg_copy4d", "dg_decode_step", "dg_decode_step_workspace_size"} <= set(syms)
 
 
 def test_library_exports_every_declared_symbol():
@@ -68,6 +68,29 @@ def test_argument_errors_return_status_and_message():
     # empty work is a no-op success
     assert lib.dg_attention(0, 1, 1, 1, 16, 0, nul, _s3(), nul, _s3(), nul, _s3(), nul, _s3(),
                             1.0, nul, 0, nul) == 0
+
+
+def _decode_step(lib, pos, max_pos=8, prefix_len=0, group=1, dtype=0, D=16, B=1):
+    fake = ctypes.c_void_p(0x1000)
+    nul = ctypes.c_void_p(0)
+    return lib.dg_decode_step(B, 1, D, dtype, fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(),
+                              fake, 0, 0, pos, nul, max_pos, fake, _s3(), 0.25, prefix_len, group, 1, nul, 0, nul)
+
+
+def test_decode_step_argument_errors():
+    """dg_decode_step rejects a host position outside the cache or inside the
+    shared prefix, bad dtypes and odd head dims before any launch."""
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    assert _decode_step(lib, pos=8) == -1 and b"position" in lib.dg_last_error()
+    assert _decode_step(lib, pos=-1) == -1 and b"position" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, prefix_len=5, group=4) == -1 and b"prefix" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, prefix_len=9, group=4) == -1 and b"prefix_len" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, dtype=7) == -2 and b"dtype" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, D=15) == -1 and b"even" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, max_pos=0) == -1 and b"max_pos" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, B=0) == 0  # empty work
 
 
 def test_workspace_sizes():

@@ -273,6 +273,71 @@ def test_grouped_prefix_attention_mfma(dev, dtype, shape):
     assert torch.equal(y_at, y_grp)
 
 
+DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
+    (300, 100, 4, 96, 120, 16, 144),  # cfg1 series: one launch
+    (70, 16, 2, 33, 69, 32, 80),      # D = 32, prefix not a multiple of 16
+    (45, 20, 3, 150, 150, 16, 160),   # no cached own key: the new one only
+    (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: two launches
+    (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): two launches
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", DECODE_STEP, ids=lambda s: "x".join(map(str, s)))
+def test_decode_step_matches_two_calls(dev, dtype, shape):
+    """dg_decode_step == dg_rope_qknorm_append at pos + dg_attention_grouped over
+    0 .. pos: the cache bit for bit; y bit for bit where it runs the two calls,
+    within the north-star bars (and against fp64) where it fuses them; the
+    device-position form equal to the host-position form; an out-of-range
+    device position leaves the cache untouched."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, G, H, P, pos, D, cap = shape
+    groups = (B + G - 1) // G
+    cache = torch.zeros((2, B, H, cap, D), dtype=TDT[dtype])
+    if P:
+        pre = _randn((groups, 2, H, P, D), 80 + D, dtype)
+        cache[:, :, :, :P] = pre.repeat_interleave(G, dim=0)[:B].transpose(0, 1)
+    cache[:, :, :, P:pos] = _randn((B, 2, H, pos - P, D), 81 + D, dtype).transpose(0, 1)
+    q, k, v = (_randn((B, 1, H, D), 82 + D + i, dtype, 2.0).to(dev) for i in range(3))
+    table = precompute_freqs_cis(D, 2 * cap, 10000).to(TDT[dtype]).to(dev)
+    scale = 1.0 / np.sqrt(D)
+    prefix, group = (P, G) if G > 1 else (0, 1)
+    ops = _native.ops()
+
+    c1 = cache.to(dev)
+    q_rot = torch.empty_like(q)
+    ops.rope_qknorm_append(q, k, v, table[pos:pos + 1].view(1, 1, 1, D // 2, 2), q_rot,
+                           c1[0, :, :, pos:pos + 1].transpose(1, 2), c1[1, :, :, pos:pos + 1].transpose(1, 2), True)
+    keys, vals = c1[0, :, :, :pos + 1].transpose(1, 2), c1[1, :, :, :pos + 1].transpose(1, 2)
+    y1 = ops.attention(q_rot, keys, vals, scale, prefix, group)
+
+    c2, y2 = cache.to(dev), torch.empty_like(q)
+    _native.decode_step_(q, k, v, table[pos], c2[0].transpose(1, 2), c2[1].transpose(1, 2), y2, scale, pos,
+                         prefix, group)
+    assert torch.equal(c2, c1)
+    if G >= 16 and D in (16, 32):
+        ref = on.attention_f64(q_rot.float().cpu().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy(),
+                               scale)
+        mag = np.abs(ref).max()
+        assert np.abs(y2.float().cpu().numpy() - ref).max() <= TOL[dtype] * mag
+        assert (y2.float() - y1.float()).abs().max().item() <= TOL[dtype] * mag
+    else:
+        assert torch.equal(y2, y1)
+
+    c3, y3 = cache.to(dev), torch.empty_like(q)
+    p = torch.tensor([pos], dtype=torch.int32, device=dev)
+    _native.decode_step_(q, k, v, table, c3[0].transpose(1, 2), c3[1].transpose(1, 2), y3, scale, p, prefix, group)
+    assert torch.equal(c3, c2) and torch.equal(y3, y2)
+
+    c4 = cache.to(dev)
+    _native.decode_step_(q, k, v, table, c4[0].transpose(1, 2), c4[1].transpose(1, 2), torch.empty_like(q), scale,
+                         torch.tensor([cap], dtype=torch.int32, device=dev), prefix, group)
+    torch.cuda.synchronize()
+    assert torch.equal(c4.cpu(), cache)
+
+
 # ------------------------------------------------------------------ strided copy
 
 
