@@ -192,10 +192,12 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
     }
 
 
-def prefill_leg(reps: int = 5):
+def prefill_leg(reps: int = 10):
     """B=256, T=1024, H=8, D=64 bf16, q/k/v in (B,T,H,D) projection
     layout, RoPE base 1e4 + QK-norm fused in the first launch, causal attention
-    in the second."""
+    in the second.  attn_ms: mean over `reps` back-to-back attention launches
+    (one graph replay, HIP events on its stream); with_rope_ms: the same for
+    the two-launch step."""
     import torch
 
     from diff_gpt import _native
@@ -210,24 +212,35 @@ def prefill_leg(reps: int = 5):
     ops = _native.ops()
     flop = 2.0 * B * H * D * T * (T + 1)
 
-    def once(evs=None):
-        ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
-        if evs is not None:
-            evs[0].record()
+    def step(with_rope: bool):
+        if with_rope:
+            ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
         _native.attention_(q_rot, k_rot, v, y, 1.0 / D**0.5)
-        if evs is not None:
-            evs[1].record()
 
-    once()
+    # reps back-to-back steps captured in a graph (as the decode job), and the
+    # attention launches alone; each timed over 3 replays with events
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(True)
     torch.cuda.synchronize()
+    full, attn_only = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(full, stream=side):
+        for _ in range(reps):
+            step(True)
+    with torch.cuda.graph(attn_only, stream=side):
+        for _ in range(reps):
+            step(False)
     times, attn = [], []
-    for _ in range(reps):
-        evs = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-        t0 = time.perf_counter()
-        once(evs)
-        torch.cuda.synchronize()
-        times.append(time.perf_counter() - t0)
-        attn.append(evs[0].elapsed_time(evs[1]) / 1e3)
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            for graph, out in ((full, times), (attn_only, attn)):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(side)
+                graph.replay()
+                b.record(side)
+                torch.cuda.synchronize()
+                out.append(a.elapsed_time(b) / 1e3 / reps)
     t_attn = sorted(attn)[len(attn) // 2]
     t_all = sorted(times)[len(times) // 2]
     tf = flop / t_attn / 1e12

@@ -2,18 +2,23 @@
 // branches of mha.py:61-81 when Tq is large and head_dim is 64 or 128).
 //
 // Workgroup = 4 wavefronts; each wavefront owns QW blocks of 32 queries of one
-// (b, h), so a workgroup covers BM = 128*QW queries.  Keys stream through a
-// double-buffered LDS ring in tiles of BN = 64 (one barrier per tile; the
-// global loads of tile t+2 are in flight while tile t is computed and tile t+1
-// is being written to the other buffer).  Both products are issued
-// transposed so that a lane's statistics all belong to ONE query:
+// (b, h), so a workgroup covers BM = 128*QW queries.  Keys stream through two
+// LDS stages in tiles of BN = 64: every wave copies its share of the next tile
+// straight from global memory into LDS (global_load_lds_dwordx4: no registers,
+// no shuffles) while the current tile is computed, then waits for its own
+// copies and meets the others at one barrier per tile.  K and V tiles are kept
+// row-major with the 16-byte pieces of row r XOR-swizzled (piece_swz), which
+// makes both operand reads below free of bank conflicts.  Both products are
+// issued transposed so that a lane's statistics all belong to ONE query:
 //
 //   S^T (64 keys x 32 queries) = K (64 x D) . Q^T (D x 32)
-//        A = K rows from LDS (shared by the QW query blocks of the wave),
-//        B = Q^T held in registers for the whole loop
+//        A = K rows from LDS (ds_read_b128), B = Q^T held in registers for the
+//        whole loop
 //   O^T (D x 32 queries)      = V^T (D x 64) . P^T (64 x 32)
-//        A = V^T from the transposed LDS copy of V, B = P^T straight from
-//        the S^T accumulators (packed to bf16/fp16, no lane exchange)
+//        A = V^T read from the row-major V tile with ds_read_b64_tr_b16 (the
+//        transposing LDS read: 4 keys x 16 dims per 16 lanes), B = P^T
+//        straight from the S^T accumulators (packed to bf16/fp16, no lane
+//        exchange)
 //
 // with v_mfma_f32_32x32x16_{bf16,f16}.  Lane l (half hh = l/32) holds, in a
 // 32x32 accumulator block, row 8*(r/4) + 4*hh + r%4 of column l%32 for
@@ -21,7 +26,7 @@
 // online-softmax statistics of a query live in lanes l and l^32 and meet
 // through one v_permlane32_swap.  The contraction order of P^T.V^T follows
 // that register order (keys 16c + 4hh + {0..3} and 16c + 8 + 4hh + {0..3} for
-// chunk c); V^T is read from LDS in exactly that permuted order.
+// chunk c); the two transposing reads fetch V^T in exactly that order.
 //
 // Softmax arithmetic per score: one max (v_max3), one FMA (scale and max
 // subtraction in log2 units), one exp2, half a bf16 pack and half a dot2 (the
@@ -46,9 +51,6 @@
 #endif
 #ifndef DG_PREFILL_QW_D128
 #define DG_PREFILL_QW_D128 1
-#endif
-#ifndef DG_PREFILL_WAVES
-#define DG_PREFILL_WAVES 4
 #endif
 
 namespace dg {
@@ -137,46 +139,68 @@ __device__ __forceinline__ float half_pair_sum(float x) {
 
 template <typename T, int D, int QW>
 struct PrefillCfg {
-  static constexpr int WAVES = DG_PREFILL_WAVES;  // wavefronts per workgroup
+  static constexpr int WAVES = 4;                 // wavefronts per workgroup
   static constexpr int NT = 64 * WAVES;           // threads per workgroup
   static constexpr int BM = 32 * QW * WAVES;      // queries per workgroup
-  static constexpr int KP = D + 8;          // padded K row (elements)
-  static constexpr int VP = kBN + 4;        // padded V^T row (elements)
-  static constexpr int K_ELEMS = kBN * KP;
-  static constexpr int V_ELEMS = D * VP;
-  static constexpr int BUF = K_ELEMS + V_ELEMS;  // one ring slot
-  static constexpr int LDS_BYTES = 2 * BUF * 2;
-  static constexpr int NC = D / 16;         // 16-wide contraction chunks of QK^T
-  static constexpr int NB = D / 32;         // 32-row blocks of O^T
-  static constexpr int CPR = D / 8;         // 16-byte chunks per K row
-  static constexpr int KCHUNKS = kBN * CPR;       // 16-byte K chunks per tile
-  static constexpr int VBLOCKS = kBN * D / 16;    // 4x4 V blocks per tile
-  static constexpr int KCPT = (KCHUNKS + NT - 1) / NT;  // per thread (last round guarded)
-  static constexpr int VBPT = (VBLOCKS + NT - 1) / NT;
+  static constexpr int NC = D / 16;               // 16-wide contraction chunks of QK^T
+  static constexpr int NB = D / 32;               // 32-row blocks of O^T
+  static constexpr int PPR = D / 8;               // 16-byte pieces per K/V row
+  static constexpr int TILE = kBN * D;            // elements of one K or V tile
+  static constexpr int ROWS_PER_DMA = 64 / PPR;   // rows one wave-wide 1 KB copy covers
+  static constexpr int DMA_PER_WAVE = kBN / ROWS_PER_DMA / WAVES;
+  static constexpr int LDS_BYTES = 4 * TILE * 2;  // K and V, two stages
 };
 
+// XOR swizzle of the 16-byte pieces of K/V row r in LDS (slot = piece ^ f(r)):
+// conflict-free both for the K operand reads (16 consecutive rows, one piece
+// each) and for the transposed V reads (4 consecutive rows, 4 adjacent pieces,
+// per 16 lanes).
+template <int D>
+__device__ __forceinline__ int piece_swz(int r) {
+  if constexpr (D == 64) return ((r & 2) << 1) | ((r >> 2) & 3);
+  else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the wave
+// writes lds + 16*l (lds wave-uniform), no registers involved
+__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// ds_read_b64_tr_b16: within each 16 lanes, lane t receives element t & 3 of
+// the 8-byte chunks addressed by lanes t/4, 4 + t/4, 8 + t/4, 12 + t/4
+__device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
+  const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)lds);
+  return __builtin_bit_cast(uint2, r);
+}
+
 // Resident workgroups per CU the register allocation must allow: D = 64 fits
-// 4 (LDS 35 KB each, <= 128 VGPRs -> 4 waves per SIMD to overlap one wave's
-// MFMAs with another's softmax); D = 128 is LDS-limited to 2.
+// 4 (<= 128 VGPRs -> 4 waves per SIMD to overlap one wave's MFMAs with
+// another's softmax); D = 128 is LDS-limited to 2.
 template <int D>
 constexpr int prefill_wgs_per_cu() {
   return D == 64 ? 4 : 2;
 }
 
 template <typename T, int D, int QW>
-__global__ __launch_bounds__(64 * DG_PREFILL_WAVES, prefill_wgs_per_cu<D>() * 4 / DG_PREFILL_WAVES)
+__global__ __launch_bounds__(256, prefill_wgs_per_cu<D>())
 void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
   using C = PrefillCfg<T, D, QW>;
-  constexpr int KP = C::KP, VP = C::VP, NC = C::NC, NB = C::NB, CPR = C::CPR;
-  constexpr int KCPT = C::KCPT, VBPT = C::VBPT;
+  constexpr int NC = C::NC, NB = C::NB, PPR = C::PPR;
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * C::BUF];
+  // two ring stages, K and V each in an array of its own: the compiler can
+  // then tell the stage being copied into from the one being read
+  __shared__ __attribute__((aligned(16))) uint16_t ks0[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t vs0[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t ks1[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t vs1[C::TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wv = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hh = lane >> 5;
   const int r32 = lane & 31;
 
@@ -228,196 +252,151 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     l[qb] = 0.f;
   }
 
-  // ---- global -> registers -> LDS staging of one key tile ------------------
-  // Per-thread element offsets inside a tile (32-bit: the host guarantees
-  // Tk * stride < 2^31); the tile base kt0 * stride is wave-uniform.
-  int koff[KCPT], kkey[KCPT], kdst[KCPT];
+  // ---- global -> LDS copy of one key tile (no registers involved) -----------
+  // Wave wv copies DMA_PER_WAVE blocks of 1 KB of K and of V; lane l of a block
+  // fills slot l % PPR of row l / PPR with the piece that the swizzle puts
+  // there.  Rows past Tk re-read the last key (masked, probability 0).
+  const int dma_row = lane / PPR, dma_slot = lane % PPR;
+  auto dma_tile = [&](uint16_t* ks, uint16_t* vs, int kt0) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < KCPT; ++i) {
-    const int chunk = min(tid + C::NT * i, C::KCHUNKS - 1);  // guarded below
-    kkey[i] = chunk / CPR;
-    koff[i] = kkey[i] * (int)a.kt + 8 * (chunk % CPR);
-    kdst[i] = kkey[i] * KP + 8 * (chunk % CPR);
-  }
-  int vkey[VBPT], voff[VBPT], vdst[VBPT];
+    for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
+      const int blk = wv * C::DMA_PER_WAVE + i;
+      const int row = blk * C::ROWS_PER_DMA + dma_row;
+      const int piece = dma_slot ^ piece_swz<D>(row);
+      const int key = min(kt0 + row, a.Tk - 1);
+      lds_copy16(kp + key * (int)a.kt + 8 * piece, ks + blk * 512);
+      lds_copy16(vp + key * (int)a.vt + 8 * piece, vs + blk * 512);
+    }
+  };
+  // this wave's copies are in LDS (each wave waits for its own before the
+  // barrier that hands the stage to all waves)
+  auto stage_ready = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_s_barrier();
+  };
+
+  // per-lane parts of the LDS operand addresses
+  const int kswz = piece_swz<D>(r32);  // rows 32mb + r32 share it
+  const int g16 = lane >> 4, t16 = lane & 15;
+  const int vhh = g16 >> 1, vhalf = g16 & 1;
+  int voff[2][NB];
 #pragma unroll
-  for (int i = 0; i < VBPT; ++i) {
-    const int blk = min(tid + C::NT * i, C::VBLOCKS - 1);  // guarded below
-    const int dg = blk % (D / 4), kg = blk / (D / 4);
-    vkey[i] = 4 * kg;
-    voff[i] = 4 * kg * (int)a.vt + 4 * dg;
-    vdst[i] = (4 * dg) * VP + 4 * kg;
-  }
-  u32x4_t kreg[KCPT];
-  uint2 vreg[VBPT][4];
-
-#define DG_PREFILL_GLOAD(KT0)                                                              \
-  do {                                                                                     \
-    const int kt0_ = (KT0);                                                                \
-    const T* kbase = kp + (int64_t)kt0_ * a.kt;                                            \
-    const T* vbase = vp + (int64_t)kt0_ * a.vt;                                            \
-    if (kt0_ + kBN <= a.Tk) {                                                              \
-      _Pragma("unroll") for (int i = 0; i < KCPT; ++i)                                     \
-          kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + koff[i]);                      \
-      _Pragma("unroll") for (int i = 0; i < VBPT; ++i)                                     \
-          _Pragma("unroll") for (int j = 0; j < 4; ++j)                                    \
-              vreg[i][j] = *reinterpret_cast<const uint2*>(vbase + voff[i] + j * (int)a.vt); \
-    } else {                                                                               \
-      /* last, partial tile: rows past Tk re-read the last key; their scores are masked */ \
-      /* and their probabilities are 0, so only finiteness matters */                      \
-      const int last = a.Tk - 1 - kt0_;                                                    \
-      _Pragma("unroll") for (int i = 0; i < KCPT; ++i) {                                   \
-        const int shift = (min(kkey[i], last) - kkey[i]) * (int)a.kt;                      \
-        kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + koff[i] + shift);                \
-      }                                                                                    \
-      _Pragma("unroll") for (int i = 0; i < VBPT; ++i)                                     \
-          _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                  \
-        const int shift = (min(vkey[i] + j, last) - vkey[i]) * (int)a.vt;                  \
-        vreg[i][j] = *reinterpret_cast<const uint2*>(vbase + voff[i] + shift);             \
-      }                                                                                    \
-    }                                                                                      \
-  } while (0)
-
-  // 4 keys x 4 dims in registers -> 4 rows of V^T with 4 consecutive keys each
-  // (vreg[i][j].x = dims (0, 1) of key j, .y = dims (2, 3))
-#define DG_PREFILL_SSTORE(SLOT)                                                            \
-  do {                                                                                     \
-    uint16_t* Ks_ = lds + (SLOT) * C::BUF;                                                 \
-    uint16_t* Vt_ = Ks_ + C::K_ELEMS;                                                      \
-    _Pragma("unroll") for (int i = 0; i < KCPT; ++i)                                       \
-        if (C::KCHUNKS % C::NT == 0 || tid + C::NT * i < C::KCHUNKS)                       \
-            *reinterpret_cast<u32x4_t*>(&Ks_[kdst[i]]) = kreg[i];                            \
-    _Pragma("unroll") for (int i = 0; i < VBPT; ++i) {                                     \
-      if (C::VBLOCKS % C::NT != 0 && tid + C::NT * i >= C::VBLOCKS) continue;               \
-      const uint2* e = vreg[i];                                                            \
-      const uint2 d0 = make_uint2((e[0].x & 0xffffu) | (e[1].x << 16),                     \
-                                  (e[2].x & 0xffffu) | (e[3].x << 16));                    \
-      const uint2 d1 = make_uint2((e[0].x >> 16) | (e[1].x & 0xffff0000u),                 \
-                                  (e[2].x >> 16) | (e[3].x & 0xffff0000u));                \
-      const uint2 d2 = make_uint2((e[0].y & 0xffffu) | (e[1].y << 16),                     \
-                                  (e[2].y & 0xffffu) | (e[3].y << 16));                    \
-      const uint2 d3 = make_uint2((e[0].y >> 16) | (e[1].y & 0xffff0000u),                 \
-                                  (e[2].y >> 16) | (e[3].y & 0xffff0000u));                \
-      uint16_t* vb_ = &Vt_[vdst[i]];                                                       \
-      *reinterpret_cast<uint2*>(vb_) = d0;                                                 \
-      *reinterpret_cast<uint2*>(vb_ + VP) = d1;                                            \
-      *reinterpret_cast<uint2*>(vb_ + 2 * VP) = d2;                                        \
-      *reinterpret_cast<uint2*>(vb_ + 3 * VP) = d3;                                        \
-    }                                                                                      \
-  } while (0)
-
-  if (ntiles > 0) {
-    DG_PREFILL_GLOAD(0);
-    DG_PREFILL_SSTORE(0);
-    if (ntiles > 1) DG_PREFILL_GLOAD(kBN);
-  }
-  __syncthreads();
-
-  for (int tile = 0; tile < ntiles; ++tile) {
-    const int kt0 = tile * kBN;
-    const int buf = tile & 1;
-    if (wave_live && kt0 <= wave_last_key) {
-      const uint16_t* Ks = lds + buf * C::BUF;
-      const uint16_t* Vt = Ks + C::K_ELEMS;
-
-      // S^T = K . Q^T for the two 32-key halves of the tile
-      floatx16_t s[QW][2];
+  for (int u = 0; u < 2; ++u) {
+    const int row = 8 * u + 4 * vhh + (t16 >> 2);
 #pragma unroll
-      for (int qb = 0; qb < QW; ++qb)
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = 32 * nb + 16 * vhalf + 4 * (t16 & 3);
+      voff[u][nb] = row * D + 8 * ((col >> 3) ^ piece_swz<D>(row)) + (col & 7);
+    }
+  }
+
+  auto compute_tile = [&](const uint16_t* Ks, const uint16_t* Vs, int kt0) __attribute__((always_inline)) {
+    // S^T = K . Q^T for the two 32-key halves of the tile
+    floatx16_t s[QW][2];
+#pragma unroll
+    for (int qb = 0; qb < QW; ++qb)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 raw =
+            *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * D + 8 * ((2 * c + hh) ^ kswz)]);
+        const vec8 kf = __builtin_bit_cast(vec8, raw);
+#pragma unroll
+        for (int qb = 0; qb < QW; ++qb) s[qb][mb] = Ops::mma(kf, qf[qb][c], s[qb][mb]);
+      }
+    }
+
+    // mask (only on tiles that cross the diagonal or the end of the keys)
+    const bool needs_mask = (kt0 + kBN - 1 > qw + qoff) || (kt0 + kBN > a.Tk);
+    if (needs_mask) {
+#pragma unroll
+      for (int qb = 0; qb < QW; ++qb) {
+        const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
+          for (int r = 0; r < 16; ++r) {
+            const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
+            if (rel > lim) s[qb][mb][r] = kNegInf;
+          }
+      }
+    }
+
+    vec8 pf[QW][4];
+#pragma unroll
+    for (int qb = 0; qb < QW; ++qb) {
+      // tile max of the raw scores (scale > 0, so it commutes with the max)
+      float mt = s[qb][0][0];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
+      mt = half_pair_max(mt);
+      // raise the exponent offset only when some row of the wave would
+      // otherwise produce probabilities above 2^kLazyLog2
+      const float mnew = fmaxf(m[qb], mt);
+      if (__builtin_amdgcn_ballot_w64(mnew > m[qb] + a.lazy_raw) != 0) {
+        // m == -inf only before the first tile; key 0 is visible to every
+        // query, so mnew is finite from then on
+        const float alpha = (m[qb] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m[qb] - mnew) * a.scale_log2);
+        m[qb] = mnew;
+        l[qb] *= alpha;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[qb][nb][r] *= alpha;
+      }
+      const float moff = m[qb] * a.scale_log2;
+      float ls = l[qb];
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const uint4 raw = *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * KP + 16 * c + 8 * hh]);
-          const vec8 kf = __builtin_bit_cast(vec8, raw);
+        for (int c2 = 0; c2 < 2; ++c2) {
+          uint32_t w[4];
 #pragma unroll
-          for (int qb = 0; qb < QW; ++qb) s[qb][mb] = Ops::mma(kf, qf[qb][c], s[qb][mb]);
-        }
-      }
-
-      // mask (only on tiles that cross the diagonal or the end of the keys)
-      const bool needs_mask = (kt0 + kBN - 1 > qw + qoff) || (kt0 + kBN > a.Tk);
-      if (needs_mask) {
-#pragma unroll
-        for (int qb = 0; qb < QW; ++qb) {
-          const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
-#pragma unroll
-          for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
-              if (rel > lim) s[qb][mb][r] = kNegInf;
-            }
-        }
-      }
-
-      vec8 pf[QW][4];
-#pragma unroll
-      for (int qb = 0; qb < QW; ++qb) {
-        // tile max of the raw scores (scale > 0, so it commutes with the max)
-        float mt = s[qb][0][0];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
-        mt = half_pair_max(mt);
-        // raise the exponent offset only when some row of the wave would
-        // otherwise produce probabilities above 2^kLazyLog2
-        const float mnew = fmaxf(m[qb], mt);
-        if (__builtin_amdgcn_ballot_w64(mnew > m[qb] + a.lazy_raw) != 0) {
-          // m == -inf only before the first tile; key 0 is visible to every
-          // query, so mnew is finite from then on
-          const float alpha = (m[qb] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m[qb] - mnew) * a.scale_log2);
-          m[qb] = mnew;
-          l[qb] *= alpha;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[qb][nb][r] *= alpha;
-        }
-        const float moff = m[qb] * a.scale_log2;
-        float ls = l[qb];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) {
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            uint32_t w[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i], a.scale_log2, -moff));
-              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i + 1], a.scale_log2, -moff));
-              w[i] = Ops::pack2(p0, p1);
-              ls = Ops::add_pair(w[i], ls);
-            }
-            pf[qb][2 * mb + c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+          for (int i = 0; i < 4; ++i) {
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i], a.scale_log2, -moff));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i + 1], a.scale_log2, -moff));
+            w[i] = Ops::pack2(p0, p1);
+            ls = Ops::add_pair(w[i], ls);
           }
+          pf[qb][2 * mb + c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
         }
-        l[qb] = ls;
       }
+      l[qb] = ls;
+    }
 
-      // O^T += V^T . P^T
+    // O^T += V^T . P^T; the V^T operand comes straight from the row-major V
+    // tile through the transposing LDS read (4 keys x 16 dims per 16 lanes)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint16_t* vrow = &Vt[(32 * nb + r32) * VP + 4 * hh];
+    for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * c);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * c + 8);
-          const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      for (int c = 0; c < 4; ++c) {
+        const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
+        const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
+        const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-          for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c], o[qb][nb]);
-        }
+        for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c], o[qb][nb]);
       }
     }
-    if (tile + 1 < ntiles) {
-      DG_PREFILL_SSTORE(buf ^ 1);  // tile + 1, loaded one iteration ago
-      if (tile + 2 < ntiles) DG_PREFILL_GLOAD(kt0 + 2 * kBN);
-    }
-    __syncthreads();
+  };
+
+  if (ntiles > 0) dma_tile(ks0, vs0, 0);
+  stage_ready();
+  for (int tile = 0; tile < ntiles; tile += 2) {
+    const int kt0 = tile * kBN;
+    if (tile + 1 < ntiles) dma_tile(ks1, vs1, kt0 + kBN);
+    if (wave_live && kt0 <= wave_last_key) compute_tile(ks0, vs0, kt0);
+    stage_ready();  // stage 1 filled; every wave is done with stage 0
+    if (tile + 1 >= ntiles) break;
+    if (tile + 2 < ntiles) dma_tile(ks0, vs0, kt0 + 2 * kBN);
+    if (wave_live && kt0 + kBN <= wave_last_key) compute_tile(ks1, vs1, kt0 + kBN);
+    stage_ready();
   }
 
   if (!wave_live) return;
@@ -443,8 +422,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   }
 }
 
-#undef DG_PREFILL_GLOAD
-#undef DG_PREFILL_SSTORE
 
 namespace {
 
