@@ -75,6 +75,7 @@ struct PrefillArgs {
   int H, Tq, Tk, q_offset;
   int nqb;     // query blocks per (b, h)
   int nwg;     // total workgroups
+  int win;     // (b, h) pairs per scheduling window
   float scale_log2;  // SDPA scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2: allowed growth of a row max in raw score units
 };
@@ -120,6 +121,7 @@ struct MfmaOps<f16_t> {
 };
 
 constexpr int kBN = 64;             // keys per tile
+constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
 // max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
@@ -204,11 +206,20 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   const int hh = lane >> 5;
   const int r32 = lane & 31;
 
-  // XCD-aware placement: consecutive logical blocks land on one XCD.
-  int logical = blockIdx.x;
-  if ((a.nwg & 7) == 0) logical = (blockIdx.x & 7) * (a.nwg >> 3) + (blockIdx.x >> 3);
-  const int bh = logical / a.nqb;
-  const int qblk = a.nqb - 1 - (logical % a.nqb);  // longest query blocks first
+  // Schedule: the (b, h) pairs go in windows of a.win; inside a window the
+  // blocks run longest query block first (blocks are dispatched in index
+  // order, so long ones start early and short ones fill in at the end), and
+  // the window's K/V stays cache-resident while its query blocks run.  Block
+  // i runs on XCD i % 8: with a.win and B*H multiples of 8 all query blocks of
+  // a (b, h) share one XCD and its L2.
+  const int nbh = a.nwg / a.nqb;
+  const int per_win = a.win * a.nqb;
+  const int win_id = blockIdx.x / per_win;
+  const int wbh0 = win_id * a.win;
+  const int wsize = min(a.win, nbh - wbh0);
+  const int wj = blockIdx.x - win_id * per_win;
+  const int bh = wbh0 + wj % wsize;
+  const int qblk = a.nqb - 1 - wj / wsize;
   const int head = bh % a.H;
   const int64_t b = bh / a.H;
 
@@ -479,6 +490,9 @@ int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.H = H; a.Tq = Tq; a.Tk = Tk;
   a.q_offset = Tk - Tq;
   a.nwg = B * H;
+  // 64 (b, h) pairs per window: measured best or within 1 % of it from
+  // B*H = 64 to 2048 at T = 1024 and 3584, D = 64 and 128
+  a.win = B * H < kPrefillWindow ? B * H : kPrefillWindow;
   a.scale_log2 = scale * 1.44269504088896340736f;
   a.lazy_raw = kLazyLog2 / a.scale_log2;
   if (dtype == DG_BF16) return D == 64 ? launch_prefill<bf16_t, 64>(a, s) : launch_prefill<bf16_t, 128>(a, s);
