@@ -40,15 +40,12 @@ __device__ __forceinline__ float from_f32<float>(float x) {
 }
 template <>
 __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
-  uint32_t u = __float_as_uint(x);
+  // v_cvt_pk_bf16_f32: round to nearest, ties to even (NaN stays a quiet
+  // NaN), no data-dependent branch; x is materialised as an fp32 register
+  // first so that no producer is folded into the conversion
+  asm("" : "+v"(x));
   bf16_t r;
-  if ((u & 0x7fffffffu) > 0x7f800000u) {  // NaN: keep sign, force a quiet NaN
-    r.bits = static_cast<uint16_t>((u >> 16) | 0x0040u);
-    return r;
-  }
-  // round to nearest, ties to even, on the 16 discarded bits
-  u += 0x7fffu + ((u >> 16) & 1u);
-  r.bits = static_cast<uint16_t>(u >> 16);
+  r.bits = __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
   return r;
 }
 template <>

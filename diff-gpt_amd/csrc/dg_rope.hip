@@ -61,10 +61,12 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
     if (pos < 0 || pos >= a.max_pos) return;
   }
 
-  const int h = (int)(row % a.H);
-  const int64_t bt = row / a.H;
-  const int t = (int)(bt % a.T);
-  const int64_t b = bt / a.T;
+  // the host keeps B*T*H below 2^31: 32-bit division
+  const uint32_t row32 = (uint32_t)row;
+  const int h = (int)(row32 % (uint32_t)a.H);
+  const uint32_t bt = row32 / (uint32_t)a.H;
+  const int t = (int)(bt % (uint32_t)a.T);
+  const int64_t b = (int64_t)(bt / (uint32_t)a.T);
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
 
@@ -179,7 +181,7 @@ int launch_rope(const RopeArgs& a, hipStream_t s) {
   constexpr int LPK = DPAD / EPL;
   constexpr int RPB = 256 / LPK;
   const int64_t blocks = (a.rows + RPB - 1) / RPB;
-  DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "rope: too many rows (%lld)", (long long)a.rows);
+  DG_REQUIRE(a.rows < 0x7fffffffLL, DG_EINVAL, "rope: B*T*H = %lld rows, at most 2^31 - 1", (long long)a.rows);
   hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL>), dim3((unsigned)blocks), dim3(256), 0,
                      s, a);
   return check_launch("rope_qknorm_kernel");
