@@ -292,13 +292,12 @@ int pick_splits(int64_t base_units, int Tk) {
   return (int)n;
 }
 
-// Key slots per trip: 16-byte lane slices keep 4 slots (8 loads of K and V in
-// flight per register set); narrower slices take more slots per trip.
-// Key slots per trip.  16-byte lane slices: 2 slots for short rows (fewer
-// registers, more resident waves; the rows end within one or two trips) and
-// 4 for long ones (more loads in flight per wave).  Narrower slices double
-// both.
-constexpr int kShortRowKeys = 512;
+// Key slots per trip.  16-byte lane slices: 2 slots when a unit's keys end
+// within one or two trips (fewer registers, more resident waves) and 4 above
+// 128 keys (more loads in flight per wave: cfg4's 230-key splits run at 61 %
+// of HBM peak instead of 58 %, cfg1 and cfg3 unchanged).  Narrower slices
+// double both.
+constexpr int kShortRowKeys = 128;
 template <typename T, int EPL>
 constexpr int slots_for(bool long_rows) {
   const int wide = EPL * (int)sizeof(T) >= 16 ? 1 : 2;
