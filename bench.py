@@ -9,7 +9,7 @@ dg_decode_step launch (RoPE + QK-norm + KV append + decode attention) on
 synthetic q/k/v projections resident in HBM.
 
     python bench.py [--steps K] [--warmup W] [--dtype fp32|bf16] [--no-prefill]
-                    [--no-cpu-baseline] [--traffic-json FILE]
+                    [--no-shapes | --shapes-only] [--no-cpu-baseline] [--traffic-json FILE]
 
 Prints ONE JSON line.  value = sequences*48*K / timed seconds (tokens/s); the
 job's 96 launches are captured once in a HIP graph (as Engine captures its
@@ -23,8 +23,10 @@ per series.  The decode_unfused leg runs the same job as two launches per
 layer-step (RoPE/append, then attention) and reports the attention kernel
 alone (es*(2*L_kv*D + 2*D) per (row, head)).  The prefill leg (configs[2]:
 B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s with
-FLOP = 2*B*H*D*T*(T+1).  cpu_baseline = the oracle's torch-CPU restatement of
-the reference decode path on a bounded sample, on this host's cores.
+FLOP = 2*B*H*D*T*(T+1).  The shapes leg times decode and prefill attention
+alone at configs[3] / configs[4] shapes.  cpu_baseline = the oracle's
+torch-CPU restatement of the reference decode path on a bounded sample, on
+this host's cores.
 """
 
 from __future__ import annotations
@@ -255,6 +257,72 @@ def prefill_leg(reps: int = 10):
     }
 
 
+def shapes_leg(reps: int = 20):
+    """Decode and prefill attention alone at the larger configs' shapes, bf16,
+    plain per-row caches: configs[3] (B=512, H=8, D=64; decode at L_kv = 1025,
+    the first step after the 1024-token prefill, and 1536, the last; prefill
+    T=1024) and configs[4] (B=64, H=8, D=128; decode at L_kv = 3585 and 3680;
+    prefill T=3584).  The cache is (2, B, H, capacity, D), the layout the
+    model's KV cache uses.  Each case is `reps` launches captured in one graph,
+    timed with events over 5 replays (median); decode bytes per launch =
+    B*H*es*(2*L_kv*D + 2*D), prefill FLOP = 2*B*H*D*T*(T+1)."""
+    import torch
+
+    from diff_gpt import _native
+
+    dev = torch.device("cuda:0")
+    dt, es = torch.bfloat16, 2
+
+    def timed(fn):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for _ in range(reps):
+                fn()
+        ts = []
+        with torch.cuda.stream(side):
+            for _ in range(5):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(side)
+                graph.replay()
+                b.record(side)
+                torch.cuda.synchronize()
+                ts.append(a.elapsed_time(b) / 1e3 / reps)
+        return sorted(ts)[2]
+
+    out = []
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, B, H, D, cap, lens in (("configs[3]", 512, 8, 64, 1536, (1025, 1536)),
+                                     ("configs[4]", 64, 8, 128, 3680, (3585, 3680))):
+        cache = torch.randn((2, B, H, cap, D), generator=g, device=dev).to(dt)
+        q = torch.randn((B, 1, H, D), generator=g, device=dev).to(dt)
+        y = torch.empty_like(q)
+        for L in lens:
+            keys = cache[0, :, :, :L].transpose(1, 2)
+            vals = cache[1, :, :, :L].transpose(1, 2)
+            t = timed(lambda: _native.attention_(q, keys, vals, y, D ** -0.5))
+            nbytes = B * H * es * (2 * L * D + 2 * D)
+            out.append({"workload": f"{name} decode attention B={B} H={H} D={D} L_kv={L} bf16",
+                        "us": t * 1e6, "achieved_gbs": nbytes / t / 1e9,
+                        "frac": nbytes / t / 1e9 / HBM_PEAK_GBS})
+            log(f"shapes: {out[-1]}")
+        del cache, q, y
+    for name, B, H, D, T in (("configs[3]", 512, 8, 64, 1024), ("configs[4]", 64, 8, 128, 3584)):
+        q, k, v = (torch.randn((B, T, H, D), generator=g, device=dev).to(dt) for _ in range(3))
+        y = torch.empty_like(q)
+        t = timed(lambda: _native.attention_(q, k, v, y, D ** -0.5))
+        tf = 2.0 * B * H * D * T * (T + 1) / t / 1e12
+        out.append({"workload": f"{name} causal prefill attention B={B} H={H} T={T} D={D} bf16",
+                    "ms": t * 1e3, "tflops": tf, "frac": tf / BF16_PEAK_TFLOPS})
+        log(f"shapes: {out[-1]}")
+        del q, k, v, y
+    return out
+
+
 def engine_leg(dtype_name: str):
     """configs[1] end to end through the drop-in API: the README GPT (random
     init, seed 0), 64 series of 96 uniform ids, each one
@@ -409,6 +477,10 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-engine", action="store_true", help="skip the end-to-end Engine leg")
+    ap.add_argument("--no-shapes", action="store_true",
+                    help="skip the attention-alone leg at configs[3] / configs[4] shapes")
+    ap.add_argument("--shapes-only", action="store_true",
+                    help="run only that leg and print its JSON list")
     ap.add_argument("--traffic-json", default=str(REPO / "profiles" / "decode_attn_cfg1_traffic.json"))
     ap.add_argument("--single-dtype", action="store_true", help="skip the other-dtype decode leg")
     ap.add_argument("--decode-mode", default="shared", choices=["shared", "plain"],
@@ -428,6 +500,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a ROCm device"
     if args.calib_copy:
         calib_copy()
+    if args.shapes_only:
+        print(json.dumps(shapes_leg()), flush=True)
+        return
     shared = args.decode_mode == "shared"
     res = decode_job(args.dtype, args.steps, args.warmup, shared)
     log(f"decode {args.dtype} {args.decode_mode}: {res}")
@@ -461,6 +536,7 @@ def main():
     prefill = None if args.no_prefill else prefill_leg()
     if prefill:
         log(f"prefill: {prefill}")
+    shapes = None if args.no_shapes else shapes_leg()
     engine = None if args.no_engine else engine_leg(args.dtype)
     if engine:
         log(f"engine: {engine}")
@@ -509,6 +585,7 @@ def main():
             "achieved_gbs": res_other["achieved_gbs"],
             "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill": prefill,
+        "shapes": shapes,
         "engine": engine,
     }
     print(json.dumps(out), flush=True)

@@ -210,53 +210,102 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
     store_vec<T, EPL>(static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh + d0,
                       acc);
   } else {
-    float* pp = a.part + unit * (int64_t)(DPAD + 2);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) pp[d0 + e] = acc[e];
+    // workspace: acc of every unit ([units][DPAD] fp32), then its (m, l)
+    store_vec<float, EPL>(a.part + (int64_t)unit * DPAD + d0, acc);
     if (sub == 0) {
-      pp[DPAD] = m;
-      pp[DPAD + 1] = l;
+      float* ml = a.part + a.units * DPAD + 2 * (int64_t)unit;
+      ml[0] = m;
+      ml[1] = l;
     }
   }
 }
 
-// Merge the nsplit partials of each (b, h, i): one lane group per query row.
+// Merge the nsplit partials of each (b, h, i).  A row's threads are C chunks
+// of CW floats times SP split slots (SP a power of two, C * SP <= 256): slot j
+// folds splits j, j + SP, ... into a running (m, l, acc) -- all its loads are
+// independent of one another, so a row's partials arrive in about one memory
+// latency -- and the SP slot states meet in LDS, where slot 0 merges them.
 template <typename T, int DPAD, int EPL>
-__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a) {
-  constexpr int LPK = DPAD / EPL;
-  constexpr int RPB = 256 / LPK;
+__global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, const int sp_shift) {
+  constexpr int CW = DPAD < 4 ? DPAD : 4;
+  constexpr int C = DPAD / CW;
+  constexpr int LOG2C = __builtin_ctz(C);
+  __shared__ float red_acc[256 * CW];
+  __shared__ float red_m[256], red_l[256];
+
+  const int t = threadIdx.x;
+  const int tpr_shift = sp_shift + LOG2C;  // threads per row = 2^tpr_shift <= 256
+  const int SP = 1 << sp_shift;
+  const int j = (t >> LOG2C) & (SP - 1);
+  const int cidx = t & (C - 1);
   const int64_t rows = a.units / a.nsplit;
-  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPK;
-  if (row >= rows) return;
-  const int sub = threadIdx.x % LPK;
-  const int d0 = sub * EPL;
-  if (d0 >= a.D) return;
+  const int64_t row = ((int64_t)blockIdx.x << (8 - tpr_shift)) + (t >> tpr_shift);
+  const bool live = row < rows;
+  const int64_t r0 = live ? row : 0;  // threads past the last row read row 0 and store nothing
+  const int ns = a.nsplit;
+  const float* ml = a.part + a.units * DPAD + r0 * ns * 2;
+  const float* pacc = a.part + r0 * ns * (int64_t)DPAD + cidx * CW;
+  const float c = a.scale_log2;
+
+  float m = kNegInf, l = 0.f;
+  float acc[CW];
+#pragma unroll
+  for (int e = 0; e < CW; ++e) acc[e] = 0.f;
+  for (int s = j; s < ns; s += SP) {
+    const float2 mls = *reinterpret_cast<const float2*>(ml + 2 * s);
+    float v[CW];
+    load_vec<float, CW>(pacc + (int64_t)s * DPAD, v);
+    if (mls.x == kNegInf) continue;  // a split with no visible key
+    const float mn = fmaxf(m, mls.x);
+    const float w_old = m == kNegInf ? 0.f : __builtin_amdgcn_exp2f((m - mn) * c);
+    const float w_new = __builtin_amdgcn_exp2f((mls.x - mn) * c);
+    l = w_old * l + w_new * mls.y;
+#pragma unroll
+    for (int e = 0; e < CW; ++e) acc[e] = w_old * acc[e] + w_new * v[e];
+    m = mn;
+  }
+#pragma unroll
+  for (int e = 0; e < CW; ++e) red_acc[t * CW + e] = acc[e];
+  red_m[t] = m;
+  red_l[t] = l;
+  __syncthreads();
+  if (!live || j != 0) return;
+
+  float M = m;
+  for (int jj = 1; jj < SP; ++jj) M = fmaxf(M, red_m[t + (jj << LOG2C)]);
+  const float w0 = m == kNegInf ? 0.f : __builtin_amdgcn_exp2f((m - M) * c);
+  float L = w0 * l;
+#pragma unroll
+  for (int e = 0; e < CW; ++e) acc[e] *= w0;
+  for (int jj = 1; jj < SP; ++jj) {
+    const int o = t + (jj << LOG2C);
+    const float mj = red_m[o];
+    const float w = mj == kNegInf ? 0.f : __builtin_amdgcn_exp2f((mj - M) * c);
+    L += w * red_l[o];
+#pragma unroll
+    for (int e = 0; e < CW; ++e) acc[e] += w * red_acc[o * CW + e];
+  }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int e = 0; e < CW; ++e) acc[e] *= inv;
+
   int64_t r = row;
   const int i = (int)(r % a.Tq);
   r /= a.Tq;
   const int h = (int)(r % a.H);
   const int64_t b = r / a.H;
-
-  const float* base = a.part + row * a.nsplit * (int64_t)(DPAD + 2);
-  float M = kNegInf;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, base[s * (DPAD + 2) + DPAD]);
-  float L = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
-    const float* pp = base + s * (DPAD + 2);
-    const float ms = pp[DPAD];
-    if (ms == kNegInf) continue;
-    const float w = __builtin_amdgcn_exp2f((ms - M) * a.scale_log2);
-    L += w * pp[DPAD + 1];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += w * pp[d0 + e];
+  T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh;
+  const int d0 = cidx * CW;
+  if constexpr (EPL >= CW) {
+    // EPL-element alignment of y (host check) covers a CW-element store
+    if (d0 < a.D) store_vec<T, CW>(yp + d0, acc);
+  } else {
+    static_assert(EPL == 2 && CW == 4, "combine store width");
+    // D is even here (2-element alignment); store the pairs inside D
+    const float lo[2] = {acc[0], acc[1]}, hi[2] = {acc[2], acc[3]};
+    if (d0 < a.D) store_vec<T, 2>(yp + d0, lo);
+    if (d0 + 2 < a.D) store_vec<T, 2>(yp + d0 + 2, hi);
   }
-  const float inv = 1.0f / L;
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] *= inv;
-  store_vec<T, EPL>(static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh + d0, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -316,11 +365,14 @@ int launch_attn(AttnArgs a, hipStream_t s) {
                        dim3(256), 0, s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
-  constexpr int LPK = DPAD / EPL;
-  constexpr int RPB = 256 / LPK;
+  // combine: C chunks of 4 floats per row times SP split slots, SP <= nsplit
+  constexpr int C = DPAD < 4 ? 1 : DPAD / 4;
+  int sp_shift = 0;
+  while ((1 << sp_shift) < a.nsplit && (C << (sp_shift + 1)) <= 256) ++sp_shift;
   const int64_t rows = a.units / a.nsplit;
-  hipLaunchKernelGGL((attn_combine_kernel<T, DPAD, EPL>), dim3((unsigned)((rows + RPB - 1) / RPB)),
-                     dim3(256), 0, s, a);
+  const int64_t rpb = 256 / (C << sp_shift);
+  hipLaunchKernelGGL((attn_combine_kernel<T, DPAD, EPL>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+                     dim3(256), 0, s, a, sp_shift);
   return check_launch("attn_combine_kernel");
 }
 

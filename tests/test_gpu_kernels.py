@@ -130,6 +130,8 @@ DECODE = [  # (B, H, Tk, D): cfg1 rows, cfg3 / cfg4 rows (few, long: key splits)
     (4, 8, 3680, 128),
     (3, 2, 97, 32),
     (2, 3, 33, 10),
+    (2, 3, 600, 10),   # key splits with D below its power of two: 2-element slices
+    (3, 2, 700, 48),
 ]
 
 
