@@ -167,8 +167,10 @@ __device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
   }
 }
 
+// At most 256 VGPRs (two workgroups per CU): decode grids here have few waves,
+// and one wave per SIMD would leave some of them for a second round.
 template <typename T, int D, bool FUSED, typename FT>
-__global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_shared_kernel(const SharedArgs a) {
   constexpr int DQ = D / 4;   // contraction elements per lane and key tile
   constexpr int DT = D / 16;  // 16-column tiles of the output
   constexpr int NT = 4;       // prefix key tiles (16 keys) per softmax chunk
@@ -258,8 +260,9 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
       load_row<T, EPL>(vr[u], vown + j * vt);
     }
   };
+  // the first own-key set streams in under the prefix phase; the second is
+  // issued after it (both at once would exceed the register budget)
   if (P < Tc) load_set(kA, vA, P);
-  if (P + STEP < Tc) load_set(kB, vB, P + STEP);
 
   // --- prefix on MFMA: lane (c, g) ---------------------------------------------
   const int c = lane & 15, g = lane >> 4;
@@ -292,16 +295,33 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int c0 = 0; c0 < P; c0 += 16 * NT) {
+  // The K operand and the V values of a 64-key chunk are loaded together (V
+  // does not depend on the softmax), and the next chunk's while the current
+  // one computes: the prefix costs about one cache round trip, not two per
+  // chunk.
+  Op kopA[NT], kopB[D == 16 ? NT : 1];
+  T vvA[NT][4][DT], vvB[D == 16 ? NT : 1][4][DT];
+  auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int base = c0 + 16 * j;
+      if (base >= P) break;  // wave-uniform
+      load_row<T, DQ>(kop[j], kpre + min(base + c, P - 1) * kt + g * DQ);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const T* vq = vpre + min(base + 4 * g + s4, P - 1) * vt + c;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
+      }
+    }
+  };
+  auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
     f32x4_t sc[NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       sc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const int base = c0 + 16 * j;
-      if (base >= P) continue;  // wave-uniform
-      Op kop;
-      load_row<T, DQ>(kop, kpre + min(base + c, P - 1) * kt + g * DQ);
-      sc[j] = qk_mfma<T, DQ>(kop, qop, sc[j]);
+      if (c0 + 16 * j >= P) continue;  // wave-uniform
+      sc[j] = qk_mfma<T, DQ>(kop[j], qop, sc[j]);
     }
     float mx = kNegInf;
 #pragma unroll
@@ -333,17 +353,32 @@ __global__ __launch_bounds__(256) void attn_shared_kernel(const SharedArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const int base = c0 + 16 * j;
-      if (base >= P) continue;
+      if (c0 + 16 * j >= P) continue;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const T* vp = vpre + min(base + 4 * g + s, P - 1) * vt + c;
+      for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
         for (int t = 0; t < DT; ++t)
-          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vp[16 * t]), sc[j][s], oacc[t], 0, 0, 0);
+          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
       }
     }
+  };
+  if constexpr (D == 16) {  // two chunk buffers fit the register budget at D = 16
+    if (P > 0) load_chunk(0, kopA, vvA);
+    for (int c0 = 0; c0 < P; c0 += 32 * NT) {
+      if (c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB);
+      prefix_chunk(c0, kopA, vvA);
+      if (c0 + 16 * NT >= P) break;
+      if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA);
+      prefix_chunk(c0 + 16 * NT, kopB, vvB);
+    }
+  } else {
+    for (int c0 = 0; c0 < P; c0 += 16 * NT) {
+      load_chunk(c0, kopA, vvA);
+      prefix_chunk(c0, kopA, vvA);
+    }
   }
+
+  if (P + STEP < Tc) load_set(kB, vB, P + STEP);
 
   // --- own keys on the vector ALUs, from the prefix's offset (rescales stay rare)
   float mo = lane_get(m, orow), lo = 0.f;
