@@ -97,6 +97,27 @@ _SIGNATURES = {
          ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64),
          ctypes.c_void_p],
     ),
+    "dg_attn_res_norm": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+         ctypes.c_void_p],
+    ),
+    "dg_gate": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
+    "dg_swiglu": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p],
+    ),
+    "dg_softcap": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
+    ),
 }
 
 ABI_VERSION = 1
@@ -420,6 +441,59 @@ def copy4d_(src: torch.Tensor, dst: torch.Tensor) -> None:
     _check(rc, "copy4d")
 
 
+def _rows(x: torch.Tensor, what: str) -> torch.Tensor:
+    """(..., N) as a 2-D (M, N) view with unit column stride (a copy only when
+    the leading dims cannot be merged)."""
+    x2 = x.reshape(-1, x.size(-1))
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def attn_res_norm_(sources: list[torch.Tensor], w: torch.Tensor, out: torch.Tensor) -> None:
+    """out = rms_norm(block_attn_res(sources[:-1], sources[-1], w)) row by row."""
+    C = out.size(-1)
+    n = len(sources)
+    srcs = [_rows(t, "attn_res_norm") for t in sources]
+    for t in srcs:
+        if t.shape != srcs[0].shape or t.dtype != out.dtype:
+            raise ValueError("attn_res_norm: sources must share shape and dtype with the output")
+    o2 = out.view(-1, C)
+    w1 = w.reshape(-1).contiguous()
+    ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() for t in srcs])
+    lds = (ctypes.c_int64 * n)(*[t.stride(0) for t in srcs])
+    rc = lib().dg_attn_res_norm(
+        o2.size(0), C, _dtype_code(o2), n, ptrs, lds, _ptr(w1), _ptr(o2), o2.stride(0), _stream(o2)
+    )
+    _check(rc, "attn_res_norm")
+
+
+def gate_(y: torch.Tensor, g: torch.Tensor) -> None:
+    """y <- y * sigmoid(g), in place."""
+    C = y.size(-1)
+    y2, g2 = y.view(-1, C), _rows(g, "gate")
+    rc = lib().dg_gate(y2.size(0), C, _dtype_code(y2), _ptr(y2), y2.stride(0), _ptr(g2), g2.stride(0),
+                       _ptr(y2), y2.stride(0), _stream(y2))
+    _check(rc, "gate")
+
+
+def swiglu_(x: torch.Tensor, out: torch.Tensor, alpha: float, limit: float) -> None:
+    N = out.size(-1)
+    x2, o2 = _rows(x, "swiglu"), out.view(-1, N)
+    rc = lib().dg_swiglu(x2.size(0), N, _dtype_code(x2), _ptr(x2), x2.stride(0), _ptr(o2), o2.stride(0),
+                         float(alpha), float(limit), _stream(x2))
+    _check(rc, "swiglu")
+
+
+def softcap_(x: torch.Tensor, cap: float) -> None:
+    """x <- cap * tanh(x / cap), in place."""
+    N = x.size(-1)
+    x2 = x.view(-1, N)
+    rc = lib().dg_softcap(x2.size(0), N, _dtype_code(x2), _ptr(x2), x2.stride(0), _ptr(x2), x2.stride(0),
+                          float(cap), _stream(x2))
+    _check(rc, "softcap")
+
+
 # ---------------------------------------------------------------------------
 # torch.ops.dgattn registration (CUDA/HIP kernels + Meta shape functions)
 # ---------------------------------------------------------------------------
@@ -435,6 +509,10 @@ _DEF.define(
 _DEF.define("rms_norm(Tensor x) -> Tensor")
 _DEF.define("rope(Tensor x, Tensor freqs) -> Tensor")
 _DEF.define("copy4d(Tensor src, Tensor(a!) dst) -> ()")
+_DEF.define("attn_res_norm(Tensor[] sources, Tensor w) -> Tensor")
+_DEF.define("gate_(Tensor(a!) y, Tensor g) -> ()")
+_DEF.define("swiglu(Tensor x, float alpha, float limit) -> Tensor")
+_DEF.define("softcap_(Tensor(a!) x, float cap) -> ()")
 
 _IMPL = torch.library.Library("dgattn", "IMPL")
 
@@ -473,6 +551,26 @@ def _rope_impl(x, freqs):
     return out.view(x.shape)
 
 
+def _attn_res_norm_impl(sources, w):
+    out = torch.empty(sources[-1].shape, dtype=sources[-1].dtype, device=sources[-1].device)
+    attn_res_norm_(list(sources), w, out)
+    return out
+
+
+def _swiglu_impl(x, alpha, limit):
+    out = torch.empty((*x.shape[:-1], x.size(-1) // 2), dtype=x.dtype, device=x.device)
+    swiglu_(x, out, alpha, limit)
+    return out
+
+
+_IMPL.impl("attn_res_norm", _attn_res_norm_impl, "CUDA")
+_IMPL.impl("gate_", gate_, "CUDA")
+_IMPL.impl("swiglu", _swiglu_impl, "CUDA")
+_IMPL.impl("softcap_", softcap_, "CUDA")
+_IMPL.impl("attn_res_norm", lambda sources, w: torch.empty_like(sources[-1]), "Meta")
+_IMPL.impl(
+    "swiglu", lambda x, alpha, limit: x.new_empty((*x.shape[:-1], x.size(-1) // 2)), "Meta"
+)
 _IMPL.impl("rope_qknorm_append", rope_qknorm_append_, "CUDA")
 _IMPL.impl("attention", _attention_impl, "CUDA")
 _IMPL.impl("rms_norm", _rms_norm_impl, "CUDA")

@@ -3,13 +3,17 @@
 Each sub-layer (attention, MLP) reads a per-token softmax mixture over the
 committed block states plus the running partial sum, weighted by a learned
 pseudo-query; a block boundary every ``layers_per_block`` layers commits the
-partial sum.  The mixture is small torch math; its RMSNorm is dg_rms_norm and
-the attention sub-layer is the HIP path of MultiHeadAttention.
+partial sum.  In Block.forward the mixture and the RMSNorm after it are one
+dg_attn_res_norm launch, the clamped SwiGLU of the MLP one dg_swiglu launch,
+and the attention sub-layer is the HIP path of MultiHeadAttention.
+``block_attn_res`` keeps the reference's torch formulation for direct callers.
 """
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
+from diff_gpt import _native
 from diff_gpt.model.feed_forward import FeedForward
 from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.model.mha import MultiHeadAttention
@@ -30,6 +34,18 @@ def block_attn_res(
     scores = rms_norm(V).matmul(proj.weight.view(-1))  # (N+1, B, T)
     weights = scores.softmax(dim=0).unsqueeze(-1)
     return (weights * V).sum(dim=0)
+
+
+def attn_res_norm(
+    blocks: tuple[torch.Tensor, ...],
+    partial_block: torch.Tensor,
+    proj: nn.Linear,
+) -> torch.Tensor:
+    """rms_norm(block_attn_res(blocks, partial_block, proj)) in one launch
+    (dg_attn_res_norm), with block_attn_res's single-block short cut."""
+    if len(blocks) == 1 and partial_block is blocks[0]:
+        return rms_norm(partial_block)
+    return _native.ops().attn_res_norm([*blocks, partial_block], proj.weight)
 
 
 class Block(nn.Module):
@@ -64,13 +80,16 @@ class Block(nn.Module):
         freqs_cis: torch.Tensor,
         kv_cache: KVCache | None,
     ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
-        h = block_attn_res(blocks, partial_block, self.attn_res_proj)
+        _native.require_device("Block", partial_block)
+        xn = attn_res_norm(blocks, partial_block, self.attn_res_proj)
         committed = self._at_boundary()
         if committed:
             blocks = (*blocks, partial_block)
-        attn_out = self.sa(rms_norm(h), freqs_cis=freqs_cis, kv_cache=kv_cache)
+        attn_out = self.sa(xn, freqs_cis=freqs_cis, kv_cache=kv_cache)
         partial_block = attn_out if committed else partial_block + attn_out
 
-        h = block_attn_res(blocks, partial_block, self.mlp_res_proj)
-        partial_block = partial_block + self.ffwd(rms_norm(h))
+        xn = attn_res_norm(blocks, partial_block, self.mlp_res_proj)
+        up, swiglu, down = self.ffwd.net
+        hidden = _native.ops().swiglu(F.linear(xn, up.weight), swiglu.alpha, swiglu.limit)
+        partial_block = partial_block + F.linear(hidden, down.weight)
         return blocks, partial_block

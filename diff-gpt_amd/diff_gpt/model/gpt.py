@@ -12,6 +12,7 @@ import torch
 import torch.nn as nn
 from torch.nn import functional as F
 
+from diff_gpt import _native
 from diff_gpt.model.block import Block
 from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.model.rms_norm import rms_norm
@@ -166,8 +167,7 @@ class GPT(BaseGPT):
 
         logits = self.lm_head(rms_norm(partial))
         if self.logit_softcap > 0:
-            cap = self.logit_softcap
-            logits = cap * torch.tanh(logits / cap)
+            _native.ops().softcap_(logits, float(self.logit_softcap))  # cap * tanh(logits / cap)
 
         loss = None
         if targets is not None:

@@ -1,7 +1,10 @@
 """Gated multi-head self-attention (src/diff_gpt/model/mha.py:10-86).
 
-Projections, the sigmoid gate and the output projection stay on hipBLASLt via
-nn.Linear.  Everything between the projections and the gate runs in libdgattn:
+The q, k, v and g projections are one GEMM (hipBLASLt) against the four
+weights concatenated (cached while the parameters are unchanged); q, k, v and
+g are column slices of its output, which the kernels read through strides.
+The sigmoid gate is one dg_gate launch and the output projection a GEMM.
+Everything between the projections and the gate runs in libdgattn:
 
   one dg_rope_qknorm_append launch  -- RoPE on q and k, QK-norm, and the K/V
                                        append into the cache page at ``pos``
@@ -20,6 +23,7 @@ rows share a broadcast prefix (two launches otherwise).
 import math
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from diff_gpt import _native
@@ -48,6 +52,18 @@ class MultiHeadAttention(nn.Module):
         self.c_v = nn.Linear(self.n_embd, inner, bias=False)
         self.c_g = nn.Linear(self.n_embd, self.n_embd, bias=False)
         self.c_proj = nn.Linear(self.n_embd, self.n_embd, bias=False)
+        self._qkvg_key = None
+        self._qkvg_weight = None
+
+    def _projection_weight(self) -> torch.Tensor:
+        """[c_q; c_k; c_v; c_g] weights stacked on the output dim, rebuilt when
+        a parameter is replaced or modified in place."""
+        ws = (self.c_q.weight, self.c_k.weight, self.c_v.weight, self.c_g.weight)
+        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
+        if key != self._qkvg_key:
+            self._qkvg_weight = torch.cat([w.detach() for w in ws], dim=0)
+            self._qkvg_key = key
+        return self._qkvg_weight
 
     def forward(
         self,
@@ -61,10 +77,12 @@ class MultiHeadAttention(nn.Module):
         H, D = self.n_head, self.head_dim
         ops = _native.ops()
 
-        q = self.c_q(x).view(B, T, H, D)
-        k = self.c_k(x).view(B, T, H, D)
-        v = self.c_v(x).view(B, T, H, D)
-        g = self.c_g(x)
+        inner = H * D
+        qkvg = F.linear(x, self._projection_weight())  # (B, T, 3*inner + C)
+        q = qkvg[..., :inner].view(B, T, H, D)
+        k = qkvg[..., inner : 2 * inner].view(B, T, H, D)
+        v = qkvg[..., 2 * inner : 3 * inner].view(B, T, H, D)
+        g = qkvg[..., 3 * inner :]
 
         if kv_cache is not None and T == 1:
             return self._decode_step(q, k, v, g, freqs_cis, kv_cache)
@@ -97,7 +115,7 @@ class MultiHeadAttention(nn.Module):
         prefix_len, group = (0, 1) if kv_cache is None or shared is None else shared
         y = ops.attention(q_rot, keys, values, 1.0 / math.sqrt(D), prefix_len, group)
         y = y.view(B, T, H * D)
-        y = y * torch.sigmoid(g)
+        ops.gate_(y, g)  # y * sigmoid(g)
         return self.c_proj(y)
 
     def _decode_step(self, q, k, v, g, freqs, kv_cache: KVCache) -> torch.Tensor:
@@ -124,5 +142,6 @@ class MultiHeadAttention(nn.Module):
         y = torch.empty_like(q)
         _native.decode_step_(q, k, v, freqs, k_cache, v_cache, y, 1.0 / math.sqrt(D), pos, prefix_len, group)
         kv_cache.advance(self.layer_idx, t1)
-        y = y.view(B, T, H * D) * torch.sigmoid(g)
+        y = y.view(B, T, H * D)
+        _native.ops().gate_(y, g)  # y * sigmoid(g)
         return self.c_proj(y)

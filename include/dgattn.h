@@ -234,6 +234,41 @@ DG_API int dg_copy4d(int dtype, const int64_t* shape, const void* src,
               const int64_t* src_st, void* dst, const int64_t* dst_st,
               void* stream);
 
+/*
+ * The layers around attention in a decode step, one launch each (the torch
+ * op sequences they replace launch several).  All take M rows with element
+ * row strides (*_ld), compute in fp32 and round to dtype wherever the torch
+ * sequence returns a tensor, so bf16 follows the same rounding steps.
+ */
+
+/*
+ * rms_norm(block_attn_res(V, w)): block.py:10-44 (stack, rms_norm(V) . w,
+ * softmax over the sources, weighted sum) followed by rms_norm.py:5-7, for the
+ * nsrc sources V_n = src[n] (rows of C elements, row stride src_ld[n]) in the
+ * order block_attn_res stacks them (committed blocks, then the partial sum).
+ * The RMSNorms give dg_rms_norm's bits for the same row.
+ * Supported: C <= 2048, 1 <= nsrc <= 32.
+ */
+DG_API int dg_attn_res_norm(int64_t M, int C, int dtype, int nsrc, const void* const* src,
+                     const int64_t* src_ld, const void* w, void* out, int64_t out_ld,
+                     void* stream);
+
+/* out = y * sigmoid(g) (mha.py:84); out may alias y. */
+DG_API int dg_gate(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g,
+            int64_t g_ld, void* out, int64_t out_ld, void* stream);
+
+/*
+ * Clamped SwiGLU (swi_glu.py:11-19) on rows of 2N interleaved (gate, linear)
+ * elements: gate = min(x[2j], limit), lin = clamp(x[2j+1], -limit, limit),
+ * out[j] = gate * sigmoid(alpha * gate) * (lin + 1).
+ */
+DG_API int dg_swiglu(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
+              int64_t out_ld, float alpha, float limit, void* stream);
+
+/* Logit soft cap cap * tanh(x / cap) (gpt.py:182-186); out may alias x. */
+DG_API int dg_softcap(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
+               int64_t out_ld, float cap, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

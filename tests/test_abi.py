@@ -104,3 +104,34 @@ def test_workspace_sizes():
     assert ws > 0 and ws % (130 * 4) == 0
     # prefill never splits
     assert lib.dg_attention_workspace_size(1, 1, 512, 512, 64, 1) == 0
+
+
+def test_block_kernel_argument_errors():
+    """The decode-step neighbour kernels reject bad sizes before any launch."""
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    nul = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)
+    ptrs = (ctypes.c_void_p * 33)(*([0x1000] * 33))
+    lds = (ctypes.c_int64 * 33)(*([64] * 33))
+    # no sources / too many sources
+    assert lib.dg_attn_res_norm(4, 64, 0, 0, ptrs, lds, fake, fake, 64, nul) == -1
+    assert b"sources" in lib.dg_last_error()
+    assert lib.dg_attn_res_norm(4, 64, 0, 33, ptrs, lds, fake, fake, 64, nul) == -1
+    # row longer than supported, unsupported dtype
+    assert lib.dg_attn_res_norm(4, 4096, 0, 2, ptrs, lds, fake, fake, 4096, nul) == -2
+    assert lib.dg_attn_res_norm(4, 64, 9, 2, ptrs, lds, fake, fake, 64, nul) == -2
+    # a source row stride shorter than C
+    short = (ctypes.c_int64 * 2)(64, 32)
+    assert lib.dg_attn_res_norm(4, 64, 0, 2, ptrs, short, fake, fake, 64, nul) == -1
+    assert b"stride" in lib.dg_last_error()
+    # swiglu input rows hold 2N elements
+    assert lib.dg_swiglu(4, 64, 0, fake, 64, fake, 64, 1.702, 7.0, nul) == -1
+    # soft cap must be positive
+    assert lib.dg_softcap(4, 64, 0, fake, 64, fake, 64, 0.0, nul) == -1
+    assert b"cap" in lib.dg_last_error()
+    # gate with a short row stride
+    assert lib.dg_gate(4, 64, 0, fake, 64, fake, 8, fake, 64, nul) == -1
+    # zero rows is a no-op
+    assert lib.dg_gate(0, 64, 0, nul, 64, nul, 64, nul, 64, nul) == 0

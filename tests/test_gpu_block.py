@@ -1,0 +1,140 @@
+"""The decode-step neighbour kernels (dg_block.hip) through the C-ABI, against
+the oracle's torch-on-CPU restatement on the same inputs.
+
+Bars: fp32 max-abs error <= 1e-5 * max|ref|,
+bf16 within 2e-2 * max|ref|; the one-source Block-AttnRes is dg_rms_norm bit
+for bit (the softmax of one score is 1)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import torch_ref as tr
+
+pytestmark = pytest.mark.gpu
+
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16}
+TOL = {"f32": 1e-5, "bf16": 2e-2}
+
+
+def _randn(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(TDT[dtype])
+
+
+def _rel(got: torch.Tensor, ref: torch.Tensor) -> float:
+    g, r = got.double().cpu(), ref.double()
+    return ((g - r).abs().max() / r.abs().max()).item()
+
+
+RES = [  # (rows, C, sources)
+    (6400, 64, 3),    # cfg1 decode, layer 0 MLP mixture (x, x, a0)
+    (6400, 64, 4),
+    (37, 64, 7),      # ragged row count
+    (512, 512, 10),   # cfg3 width, eight layers deep
+    (5, 1024, 5),     # cfg4 width
+    (9, 48, 3),       # C not a power of two
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", RES, ids=lambda s: "x".join(map(str, s)))
+def test_attn_res_norm_matches_reference(dev, dtype, shape):
+    from diff_gpt import _native
+
+    M, C, n = shape
+    srcs = [_randn((M, C), 100 + i, dtype, 1.0 + 0.5 * i) for i in range(n)]
+    w = _randn((1, C), 7, dtype, 0.5)
+    got = _native.ops().attn_res_norm([s.to(dev) for s in srcs], w.to(dev))
+    ref = tr.rms(tr.attn_res(tuple(srcs[:-1]), srcs[-1], w))
+    assert got.dtype == ref.dtype and got.shape == ref.shape
+    assert _rel(got, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_attn_res_norm_one_source_is_rms_norm(dev, dtype):
+    from diff_gpt import _native
+
+    x = _randn((300, 64), 3, dtype, 3.0).to(dev)
+    w = _randn((1, 64), 4, dtype).to(dev)
+    a = _native.ops().attn_res_norm([x], w)
+    b = _native.ops().rms_norm(x)
+    assert torch.equal(a, b)
+
+
+def test_attn_res_norm_strided_sources(dev):
+    """Sources that are column slices of wider rows (row stride > C)."""
+    from diff_gpt import _native
+
+    wide = _randn((50, 3, 128), 11, "f32").to(dev)
+    srcs = [wide[:, i, 32:96] for i in range(3)]
+    w = _randn((1, 64), 12, "f32").to(dev)
+    got = _native.ops().attn_res_norm(srcs, w)
+    ref = tr.rms(tr.attn_res(tuple(s.cpu() for s in srcs[:-1]), srcs[-1].cpu(), w.cpu()))
+    assert _rel(got, ref) <= TOL["f32"]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_gate_matches_reference(dev, dtype):
+    from diff_gpt import _native
+
+    y = _randn((6400, 64), 21, dtype)
+    wide = _randn((6400, 256), 22, dtype, 3.0)
+    g = wide[:, 192:]  # the g slice of a fused projection output
+    yd = y.to(dev)
+    _native.ops().gate_(yd, wide.to(dev)[:, 192:])
+    ref = y * torch.sigmoid(g)
+    assert _rel(yd, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("rows", [6400, 3])
+def test_swiglu_matches_reference(dev, dtype, rows):
+    from diff_gpt import _native
+
+    alpha, limit = 1.702, 7.0
+    h = _randn((rows, 256), 31 + rows, dtype, 5.0)  # crosses the clamp limits
+    got = _native.ops().swiglu(h.to(dev), alpha, limit)
+    gl = h[..., ::2].clamp(max=limit)
+    ln = h[..., 1::2].clamp(min=-limit, max=limit)
+    ref = gl * torch.sigmoid(alpha * gl) * (ln + 1)
+    assert got.shape == (rows, 128)
+    assert _rel(got, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_softcap_matches_reference(dev, dtype):
+    from diff_gpt import _native
+
+    x = _randn((6400, 256), 41, dtype, 20.0)
+    xd = x.to(dev)
+    _native.ops().softcap_(xd, 15.0)
+    ref = 15.0 * torch.tanh(x / 15.0)
+    assert _rel(xd, ref) <= TOL[dtype]
+    assert xd.float().abs().max().item() <= 15.0
+
+
+def test_gpt_forward_uses_one_projection_gemm_and_matches_reference(dev):
+    """GPT.forward with the fused neighbours against the oracle forward on the
+    same weights (fp32, prefill of 2 x 24 tokens)."""
+    from diff_gpt.model.gpt import GPT
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=64, n_head=4, n_layer=3,
+                use_checkpoint=False).eval()
+    p = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=64, n_head=4, n_layer=3)
+    idx = torch.randint(0, 256, (2, 24), generator=torch.Generator().manual_seed(5))
+    model = model.to(dev)
+    with torch.inference_mode():
+        got, _ = model(idx.to(dev))
+        ref = tr.forward(p, cfg, idx)
+    assert _rel(got, ref) <= TOL["f32"]
+    # the concatenated projection weight is reused until a parameter changes
+    sa = model.blocks[0].sa
+    w0 = sa._projection_weight()
+    assert sa._projection_weight() is w0
+    with torch.no_grad():
+        sa.c_g.weight.mul_(2.0)
+    assert sa._projection_weight() is not w0
+    assert np.array_equal(sa._projection_weight()[192:].cpu().numpy(), sa.c_g.weight.detach().cpu().numpy())
