@@ -78,19 +78,38 @@ class _DecodeGraph:
         self.cache.pos += 1
         return self.logits
 
+    def rewind(self) -> None:
+        """Start over at the cache's (refilled) host position."""
+        self.cache.pos_dev.fill_(self.cache.pos)
+
     def close(self) -> None:
         self.cache.pos_dev = None
 
 
+# A captured decode step (and the cache it writes) is kept for the next call
+# when the cache is at most this large.
+_KEEP_GRAPH_BYTES = 1 << 30
+
+
 class Engine:
-    __slots__ = ("model", "use_graph")
+    __slots__ = ("model", "use_graph", "_kept")
 
     def __init__(self, model: BaseGPT, use_graph: bool = True) -> None:
         """use_graph: replay the decode step as a captured HIP graph (same
         kernels and arithmetic as the eager forward, no per-step launch
-        overhead); False runs every step eagerly."""
+        overhead); False runs every step eagerly.  The captured step and its
+        cache (up to 1 GiB) are kept after a call and reused by the next call
+        with the same rows, prompt length and budget while the model's
+        parameters are unchanged (same storage, no in-place update)."""
         self.model = model
         self.use_graph = use_graph
+        self._kept = None  # (key, cache, _DecodeGraph), free for the next call
+
+    def _graph_key(self, num_samples: int, prompt_len: int, steps: int) -> tuple:
+        model = self.model
+        params = tuple((p.data_ptr(), p._version) for p in model.parameters())
+        buffers = tuple(b.data_ptr() for b in model.buffers())
+        return (id(model), num_samples, prompt_len, steps, params, buffers)
 
     def _budget(self, prompt_len: int, max_tokens: int | None) -> int:
         # RoPE table covers 2*block_size positions (engine.py:55-64)
@@ -166,14 +185,25 @@ class Engine:
         logits = logits[:, -1, :].expand(num_samples, -1)
 
         # 2) every row starts from the same prompt cache (read once per
-        #    decode step thanks to the recorded shared prefix)
-        cache = KVCache(batch_size=num_samples, seq_len=len(tokens) + steps, **geometry)
-        cache.prefill(prompt_cache)
+        #    decode step thanks to the recorded shared prefix); a step captured
+        #    by an earlier call with the same key replays into its own cache
+        use_graph = self.use_graph and steps > 1 and torch.device(device).type == "cuda"
+        key = self._graph_key(num_samples, len(tokens), steps) if use_graph else None
+        kept, self._kept = self._kept, None  # taken: a concurrent call builds its own
+        decode = None
+        if kept is not None and kept[0] == key:
+            _, cache, decode = kept
+            cache._refill(prompt_cache)
+            decode.rewind()
+        else:
+            if kept is not None:
+                kept[2].close()
+            cache = KVCache(batch_size=num_samples, seq_len=len(tokens) + steps, **geometry)
+            cache.prefill(prompt_cache)
+            if use_graph:
+                decode = _DecodeGraph(model, cache, num_samples, torch.device(device))
         del prompt_cache
 
-        decode = None
-        if self.use_graph and steps > 1 and torch.device(device).type == "cuda":
-            decode = _DecodeGraph(model, cache, num_samples, torch.device(device))
         try:
             for step in range(steps):
                 forced = None if force_schedule is None else force_schedule[step]
@@ -198,7 +228,10 @@ class Engine:
                     logits = logits[:, -1, :]
         finally:
             if decode is not None:
-                decode.close()
+                if cache.kv_cache.numel() * cache.kv_cache.element_size() <= _KEEP_GRAPH_BYTES:
+                    self._kept = (key, cache, decode)
+                else:
+                    decode.close()
 
     @torch.inference_mode()
     def generate_batch(

@@ -74,6 +74,16 @@ class KVCache:
     # -- prefill: batch-1 prompt cache -> num_samples rows (kv_cache.py:35-81) --
     def prefill(self, other: "KVCache") -> None:
         assert self.kv_cache.size(0) == 0, "Cannot prefill a non-empty KV cache"
+        self._fill_from(other, reuse=False)
+
+    def _refill(self, other: "KVCache") -> None:
+        """prefill() into the tensor this cache already holds (same shape,
+        dtype and device as a fresh prefill would allocate), so the pointers
+        a captured decode step baked in stay valid."""
+        assert self.kv_cache.size(0) != 0, "_refill needs an allocated cache"
+        self._fill_from(other, reuse=True)
+
+    def _fill_from(self, other: "KVCache", reuse: bool) -> None:
         assert other.kv_cache.size(0) != 0, "Cannot prefill with a None KV cache"
         sl, skv, sb, sh, st, sd = self.kv_shape
         ol, okv, ob, oh, ot, od = other.kv_shape
@@ -88,7 +98,13 @@ class KVCache:
 
         src = other.kv_cache
         _native.require_device("KVCache.prefill", src)
-        self.kv_cache = torch.empty(self.kv_shape, dtype=src.dtype, device=src.device)
+        if reuse:
+            dst = self.kv_cache
+            assert tuple(dst.shape) == tuple(self.kv_shape) and dst.dtype == src.dtype and dst.device == src.device, (
+                "_refill: the held cache does not match the prompt cache"
+            )
+        else:
+            self.kv_cache = torch.empty(self.kv_shape, dtype=src.dtype, device=src.device)
         n = other.pos
         if n > 0:
             dst4 = _pages(self.kv_cache, n)

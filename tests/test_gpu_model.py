@@ -505,3 +505,33 @@ def test_engine_graph_replay_equals_eager(dev, dtype):
         a = Engine(model).generate_batch(prompt, num_samples=12, max_tokens=8, **kw)
         b = Engine(model, use_graph=False).generate_batch(prompt, num_samples=12, max_tokens=8, **kw)
         assert a == b, kw
+
+
+def test_engine_reuses_the_captured_step_across_calls(dev):
+    """A second call with the same rows, prompt length and budget replays the
+    step captured by the first into the same cache, and gives a fresh Engine's
+    tokens; a different prompt length or an in-place weight change captures
+    anew."""
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    model = _gpt(dev, vocab_size=64, n_embd=32, block_size=32, n_head=4, n_layer=2)
+    hot = TemperatureSampler(temperature=3.0)
+    prompts = ([5, 8, 12, 1], [7, 7, 2, 30], [9, 1])
+    e = Engine(model)
+    for seed, p in zip((1, 2, 3), prompts):
+        got, _ = e.generate_batch(tokens=p, num_samples=24, max_tokens=9, seed=seed, sampler=hot)
+        ref, _ = Engine(model).generate_batch(tokens=p, num_samples=24, max_tokens=9, seed=seed, sampler=hot)
+        assert got == ref
+    graph = e._kept[2]
+    e.generate_batch(tokens=[9, 3], num_samples=24, max_tokens=9, seed=4, sampler=hot)
+    assert e._kept[2] is graph  # same key: the captured step was replayed
+    e.generate_batch(tokens=[9, 3, 4], num_samples=24, max_tokens=9, seed=4, sampler=hot)
+    assert e._kept[2] is not graph  # another prompt length: captured anew
+    graph = e._kept[2]
+    with torch.no_grad():
+        model.blocks[1].sa.c_v.weight.mul_(-1.5)
+    got, _ = e.generate_batch(tokens=[9, 3, 4], num_samples=24, max_tokens=9, seed=5, sampler=hot)
+    assert e._kept[2] is not graph  # parameters changed in place: captured anew
+    ref, _ = Engine(model).generate_batch(tokens=[9, 3, 4], num_samples=24, max_tokens=9, seed=5, sampler=hot)
+    assert got == ref
