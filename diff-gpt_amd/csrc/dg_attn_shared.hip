@@ -8,13 +8,15 @@
 // P V_prefix: this kernel runs both on MFMA, reading the prefix (L2-resident,
 // shared by the tiles of a group) once per 16-row tile.  The rows' own keys,
 // positions prefix_len .. Tk-1, differ from row to row and go through the
-// vector ALUs.  Both parts share one softmax offset per row and merge in
-// registers.
+// vector ALUs.  The two parts run at the same time on two wavefronts and merge
+// at the end.
 //
-// Work unit = one wavefront = (group, tile of 16 rows of the group, head).
-// Lane l: c = l & 15 is the tile row, g = l >> 4 one of four lanes per row.
+// Work unit = one block of two wavefronts = (group, tile of 16 rows of the
+// group, head).  Wave 0 takes the prefix, wave 1 the own keys.
 //
-// Prefix (MFMA, v_mfma_f32_16x16x4_f32 or v_mfma_f32_16x16x16_{bf16,f16}):
+// Prefix (wave 0, MFMA: v_mfma_f32_16x16x4_f32 or
+// v_mfma_f32_16x16x16_{bf16,f16}); lane l: c = l & 15 is the tile row,
+// g = l >> 4 one of four lanes per row:
 //   S^T (16 keys x 16 rows) = K_tile Q^T: lane (c, g) feeds key row c and
 //   query row c of the tile, each with the D/4 contiguous elements
 //   g*D/4 .. g*D/4 + D/4 - 1 (a fixed permutation of the contraction index,
@@ -25,12 +27,15 @@
 //   O^T (D x 16 rows) += V^T P^T in steps of 4 keys: lane (c, g) feeds
 //   V[4g+s][16t+c] and its own probability of key 4g+s, and holds O^T for
 //   row c, columns 16t + 4g .. 16t + 4g + 3.
-// Own keys (VALU): lane (c, g) takes keys prefix_len + g + 4u of row c with
-//   the whole q, k and v rows in registers (D FMAs for q.k, D for p.v, no
-//   cross-lane traffic), starting from the prefix's softmax offset; the four
-//   lanes of a row merge at the end (max, rescale, then a two-step
-//   reduce-scatter with v_permlane32_swap / v_permlane16_swap that leaves each
-//   lane the columns its O^T registers hold).
+// Own keys (wave 1, VALU): a quad of lanes holds one tile row, 16 bytes of a
+//   cache row per lane (OwnCfg), so every quad reads whole cache rows; the
+//   lanes of a key row add their partial dot products with DPP, and each
+//   lane accumulates p * v for its slice of the row.  The wave streams its
+//   keys from the start of the launch, two register sets in flight, while
+//   wave 0's prefix phase (a few dependent cache round trips) runs.
+// Merge: wave 1 writes each row's softmax offset, sum and weighted values to
+//   LDS; after one barrier wave 0 rescales both parts to the larger offset,
+//   adds them and stores its O^T columns.
 //
 // Fused decode step (FUSED = true; mha.py:44-68 for one new token): the same
 // kernel first applies RoPE and QK-norm to the step's q and k projections
@@ -167,31 +172,41 @@ __device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
   }
 }
 
-// At most 256 VGPRs (two workgroups per CU): decode grids here have few waves,
-// and one wave per SIMD would leave some of them for a second round.
+// Two wavefronts per work unit, running at the same time: wave 0 takes the
+// prefix on the matrix cores, wave 1 streams the rows' own keys on the vector
+// ALUs from the start of the launch, so the prefix phase (latency-bound: a few
+// dependent cache round trips) overlaps the HBM-bound own-key stream instead of
+// preceding it.  Wave 1 hands its partial (offset, sum and weighted values of
+// each row) to wave 0 through LDS; wave 0 merges and stores.  At most 128
+// VGPRs (four waves per SIMD), so that decode grids of a few thousand waves
+// are resident at once.
 template <typename T, int D, bool FUSED, typename FT>
-__global__ __launch_bounds__(256, 2) void attn_shared_kernel(const SharedArgs a) {
+__global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a) {
   constexpr int DQ = D / 4;   // contraction elements per lane and key tile
   constexpr int DT = D / 16;  // 16-column tiles of the output
   constexpr int NT = 4;       // prefix key tiles (16 keys) per softmax chunk
   using O = OwnCfg<T, D>;
-  constexpr int LPK = O::LPK, KPQ = O::KPQ, EPL = O::EPL, UO = O::UO, STEP = O::STEP;
+  constexpr int LPK = O::LPK, KPQ = O::KPQ, EPL = O::EPL;
   using Op = RowRegs<T, DQ>;
   using Slice = RowRegs<T, EPL>;
+  constexpr int UO = 16 / Slice::WORDS;  // key slots per register set: two sets of K+V = 64 VGPRs
+  constexpr int STEP = UO * KPQ;         // keys per row and register set
+  constexpr int RS = D + 4;              // floats per row of the hand-over buffer (16-byte rows)
+  __shared__ __attribute__((aligned(16))) float part[16 * RS];
 
   const int lane = threadIdx.x & 63;
+  const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 0: prefix, 1: own keys
   // the tiles and heads of one group run on one XCD, whose L2 keeps the prefix
-  int blk = blockIdx.x;
-  if ((gridDim.x & 7) == 0) blk = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
-  const int unit = blk * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (unit >= a.units) return;  // whole wave exits; no barriers below
+  int unit = blockIdx.x;
+  if ((gridDim.x & 7) == 0) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
+  if (unit >= a.units) return;  // both waves of the block; no barrier reached
   const int h = unit % a.H;
   const int rest = unit / a.H;
   const int tile = rest % a.tiles;
   const int grp = rest / a.tiles;
 
   const int64_t b0 = (int64_t)grp * a.group;  // the group's first row holds the prefix
-  // tile row r of the wave -> batch row (rows past the group compute on b0
+  // tile row r of the unit -> batch row (rows past the group compute on b0
   // and store nothing)
   auto row_of = [&](int r, bool& ok) __attribute__((always_inline)) {
     const int rin = tile * 16 + r;
@@ -212,6 +227,7 @@ __global__ __launch_bounds__(256, 2) void attn_shared_kernel(const SharedArgs a)
     if (a.pos_dev != nullptr) Tk = min(*a.pos_dev + 1, a.Tk);
     Tc = Tk;
   }
+  (void)Tk;
   const int P = min(a.prefix_len, Tc);
   const float cl = a.scale_log2;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
@@ -219,253 +235,299 @@ __global__ __launch_bounds__(256, 2) void attn_shared_kernel(const SharedArgs a)
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)h * a.vh;
   const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * a.qh;
 
-  // --- own keys: quad layout -------------------------------------------------
+  // --- query rows in the quad layout: a quad of lanes holds one tile row -----
   const int orow = lane >> 2, kk = (lane & 3) / LPK, piece = (lane & 3) % LPK;
   bool ovalid;
   const int64_t bo = row_of(orow, ovalid);
-  Slice qs;  // the attention query of row orow (this lane's EPL elements)
-  Slice knew, vnew;  // fused: the appended key and value
-  if constexpr (FUSED) {
-    // RoPE + QK-norm of the new token (mha.py:44-48), rounded to T as the
-    // standalone kernel stores it, then the append (kv_cache.py:108-109)
-    float xq[EPL], xk[EPL], cs[EPL];
-    load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
-    load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
-    load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
-    load_vec<FT, EPL>(static_cast<const FT*>(a.freqs) + (int64_t)Tc * a.fpos + piece * EPL, cs);
+  // RoPE + QK-norm of the new token's q (mha.py:44-48), rounded to T as the
+  // standalone kernel stores it; both waves compute it (same bits)
+  auto rotate_q = [&](float (&xq)[EPL], const float (&cs)[EPL], Slice& qs) __attribute__((always_inline)) {
     rope_rotate<T, EPL>(xq, cs);
-    rope_rotate<T, EPL>(xk, cs);
-    if (a.qknorm) {
-      qk_rms_norm<EPL, LPK>(xq, D);
-      qk_rms_norm<EPL, LPK>(xk, D);
-    }
+    if (a.qknorm) qk_rms_norm<EPL, LPK>(xq, D);
     pack_row<T, EPL>(qs, xq);
-    pack_row<T, EPL>(knew, xk);
-    if (ovalid && kk == 0) {
-      store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
-      store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
-    }
-  } else {
-    load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
-  }
-  const T* kown = kbase + bo * a.kb + piece * EPL;
-  const T* vown = vbase + bo * a.vb + piece * EPL;
-  Slice kA[UO], vA[UO], kB[UO], vB[UO];
-  auto load_set = [&](Slice (&kr)[UO], Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < UO; ++u) {
-      if (j0 + KPQ * u >= Tc) break;  // wave-uniform
-      const int j = min(j0 + KPQ * u + kk, Tc - 1);  // past Tc: a valid row, masked below
-      load_row<T, EPL>(kr[u], kown + j * kt);
-      load_row<T, EPL>(vr[u], vown + j * vt);
-    }
   };
-  // the first own-key set streams in under the prefix phase; the second is
-  // issued after it (both at once would exceed the register budget)
-  if (P < Tc) load_set(kA, vA, P);
+  const FT* fbase = FUSED ? static_cast<const FT*>(a.freqs) + (int64_t)Tc * a.fpos + piece * EPL : nullptr;
 
-  // --- prefix on MFMA: lane (c, g) ---------------------------------------------
-  const int c = lane & 15, g = lane >> 4;
+  // wave 0's state, merged after the hand-over
+  const int c = lane & 15, g = lane >> 4;  // MFMA layout: tile row c, lane group g
   bool cvalid;
   const int64_t bc = row_of(c, cvalid);
-  const T* kpre = kbase + b0 * a.kb;
-  const T* vpre = vbase + b0 * a.vb;
-  Op qop;  // q row c, elements g*DQ .. g*DQ + DQ - 1
-  if constexpr (FUSED) {
-    // gathered from the quad layout: own lane 4c + (g*DQ)/EPL (key lane 0)
-    // holds them at word (g*DQ % EPL) * sizeof(T) / 4 of its slice
-    constexpr int OPW = Op::WORDS, SW = Slice::WORDS;
-    const int src = 4 * c + (g * DQ) / EPL;
-    const int wo = ((g * DQ) % EPL) * (int)sizeof(T) / 4;
-#pragma unroll
-    for (int w = 0; w < OPW; ++w) {
-      uint32_t x = 0;
-#pragma unroll
-      for (int cand = 0; cand + OPW <= SW; cand += OPW) {
-        const uint32_t y = lane_get_u(qs.w[cand + w], src);
-        x = (wo == cand) ? y : x;
-      }
-      qop.w[w] = x;
-    }
-  } else {
-    load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
-  }
   float m = kNegInf, lp = 0.f;
   f32x4_t oacc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // The K operand and the V values of a 64-key chunk are loaded together (V
-  // does not depend on the softmax), and the next chunk's while the current
-  // one computes: the prefix costs about one cache round trip, not two per
-  // chunk.
-  Op kopA[NT], kopB[D == 16 ? NT : 1];
-  T vvA[NT][4][DT], vvB[D == 16 ? NT : 1][4][DT];
-  auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+  // Each wave issues its first cache loads right behind its query loads, as a
+  // fixed number of loads (rows clamped to ones that exist, position 0 at
+  // least; the extra rows are masked), so that waiting for the query does not
+  // wait for them.
+  if (role == 0) {
+    // --- prefix on MFMA: lane (c, g) -------------------------------------------
+    const T* kpre = kbase + b0 * a.kb;
+    const T* vpre = vbase + b0 * a.vb;
+    Op kopA[NT], kopB[D == 16 ? NT : 1];
+    T vvA[NT][4][DT], vvB[D == 16 ? NT : 1][4][DT];
+    // the first 128 prefix keys (64 at D = 32)
+    auto first_chunks = [&]() __attribute__((always_inline)) {
+      const int last = max(P - 1, 0);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int base = c0 + 16 * j;
-      if (base >= P) break;  // wave-uniform
-      load_row<T, DQ>(kop[j], kpre + min(base + c, P - 1) * kt + g * DQ);
+      for (int half = 0; half < (D == 16 ? 2 : 1); ++half) {
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const T* vq = vpre + min(base + 4 * g + s4, P - 1) * vt + c;
+        for (int j = 0; j < NT; ++j) {
+          const int base = 16 * NT * half + 16 * j;
+          Op& kop = half ? kopB[D == 16 ? j : 0] : kopA[j];
+          load_row<T, DQ>(kop, kpre + min(base + c, last) * kt + g * DQ);
 #pragma unroll
-        for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
+          for (int s4 = 0; s4 < 4; ++s4) {
+            const T* vq = vpre + min(base + 4 * g + s4, last) * vt + c;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+              T& dst = half ? vvB[D == 16 ? j : 0][s4][t] : vvA[j][s4][t];
+              dst = vq[16 * t];
+            }
+          }
+        }
+      }
+    };
+    Op qop;  // q row c, elements g*DQ .. g*DQ + DQ - 1
+    if constexpr (FUSED) {
+      float xq[EPL], cs[EPL];
+      load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
+      load_vec<FT, EPL>(fbase, cs);
+      first_chunks();
+      Slice qs;
+      rotate_q(xq, cs, qs);
+      // gathered from the quad layout: own lane 4c + (g*DQ)/EPL (key lane 0)
+      // holds them at word (g*DQ % EPL) * sizeof(T) / 4 of its slice
+      constexpr int OPW = Op::WORDS, SW = Slice::WORDS;
+      const int src = 4 * c + (g * DQ) / EPL;
+      const int wo = ((g * DQ) % EPL) * (int)sizeof(T) / 4;
+#pragma unroll
+      for (int w = 0; w < OPW; ++w) {
+        uint32_t x = 0;
+#pragma unroll
+        for (int cand = 0; cand + OPW <= SW; cand += OPW) {
+          const uint32_t y = lane_get_u(qs.w[cand + w], src);
+          x = (wo == cand) ? y : x;
+        }
+        qop.w[w] = x;
+      }
+    } else {
+      load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
+      first_chunks();
+    }
+    auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int base = c0 + 16 * j;
+        if (base >= P) break;  // wave-uniform
+        load_row<T, DQ>(kop[j], kpre + min(base + c, P - 1) * kt + g * DQ);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const T* vq = vpre + min(base + 4 * g + s4, P - 1) * vt + c;
+#pragma unroll
+          for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
+        }
+      }
+    };
+    auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+      f32x4_t sc[NT];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        sc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (c0 + 16 * j >= P) continue;  // wave-uniform
+        sc[j] = qk_mfma<T, DQ>(kop[j], qop, sc[j]);
+      }
+      float mx = kNegInf;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool in = c0 + 16 * j + 4 * g + r < P;
+          sc[j][r] = in ? sc[j][r] : kNegInf;
+          mx = fmaxf(mx, sc[j][r]);
+        }
+      }
+      mx = row_max4(mx);  // every chunk holds a prefix key: finite
+      if (mx > m + a.lazy_raw) {
+        const float alpha = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - mx) * cl);
+        m = mx;
+        lp *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+      }
+      const float moff = m * cl;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], cl, -moff));
+          sc[j][r] = p;
+          lp += p;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        if (c0 + 16 * j >= P) continue;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+            oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
+        }
+      }
+    };
+    if constexpr (D == 16) {  // two chunk buffers fit the register budget at D = 16
+      for (int c0 = 0; c0 < P; c0 += 32 * NT) {
+        if (c0 > 0 && c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB);
+        prefix_chunk(c0, kopA, vvA);
+        if (c0 + 16 * NT >= P) break;
+        if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA);
+        prefix_chunk(c0 + 16 * NT, kopB, vvB);
+      }
+    } else {
+      for (int c0 = 0; c0 < P; c0 += 16 * NT) {
+        if (c0 > 0) load_chunk(c0, kopA, vvA);
+        prefix_chunk(c0, kopA, vvA);
       }
     }
-  };
-  auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
-    f32x4_t sc[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      sc[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (c0 + 16 * j >= P) continue;  // wave-uniform
-      sc[j] = qk_mfma<T, DQ>(kop[j], qop, sc[j]);
-    }
-    float mx = kNegInf;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const bool in = c0 + 16 * j + 4 * g + r < P;
-        sc[j][r] = in ? sc[j][r] : kNegInf;
-        mx = fmaxf(mx, sc[j][r]);
-      }
-    }
-    mx = row_max4(mx);  // every chunk holds a prefix key: finite
-    if (mx > m + a.lazy_raw) {
-      const float alpha = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - mx) * cl);
-      m = mx;
-      lp *= alpha;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
-    }
-    const float moff = m * cl;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], cl, -moff));
-        sc[j][r] = p;
-        lp += p;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      if (c0 + 16 * j >= P) continue;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-          oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
-      }
-    }
-  };
-  if constexpr (D == 16) {  // two chunk buffers fit the register budget at D = 16
-    if (P > 0) load_chunk(0, kopA, vvA);
-    for (int c0 = 0; c0 < P; c0 += 32 * NT) {
-      if (c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB);
-      prefix_chunk(c0, kopA, vvA);
-      if (c0 + 16 * NT >= P) break;
-      if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA);
-      prefix_chunk(c0 + 16 * NT, kopB, vvB);
-    }
+
   } else {
-    for (int c0 = 0; c0 < P; c0 += 16 * NT) {
-      load_chunk(c0, kopA, vvA);
-      prefix_chunk(c0, kopA, vvA);
+    // --- own keys on the vector ALUs: lane (orow, kk, piece) --------------------
+    const T* kown = kbase + bo * a.kb + piece * EPL;
+    const T* vown = vbase + bo * a.vb + piece * EPL;
+    Slice kA[UO], vA[UO], kB[UO], vB[UO];
+    auto load_set = [&](Slice (&kr)[UO], Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < UO; ++u) {
+        if (j0 + KPQ * u >= Tc) break;  // wave-uniform
+        const int j = min(j0 + KPQ * u + kk, Tc - 1);  // past Tc: a valid row, masked below
+        load_row<T, EPL>(kr[u], kown + j * kt);
+        load_row<T, EPL>(vr[u], vown + j * vt);
+      }
+    };
+    // the first two sets
+    auto first_sets = [&]() __attribute__((always_inline)) {
+      const int last = max(Tc - 1, 0);
+#pragma unroll
+      for (int u = 0; u < 2 * UO; ++u) {
+        const int j = min(P + KPQ * u + kk, last);
+        load_row<T, EPL>(u < UO ? kA[u] : kB[u - UO], kown + j * kt);
+        load_row<T, EPL>(u < UO ? vA[u] : vB[u - UO], vown + j * vt);
+      }
+    };
+    Slice qs;
+    Slice knew, vnew;  // fused: the appended key and value
+    if constexpr (FUSED) {
+      float xq[EPL], xk[EPL], cs[EPL];
+      load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
+      load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
+      load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
+      load_vec<FT, EPL>(fbase, cs);
+      first_sets();
+      rotate_q(xq, cs, qs);
+      rope_rotate<T, EPL>(xk, cs);
+      if (a.qknorm) qk_rms_norm<EPL, LPK>(xk, D);
+      pack_row<T, EPL>(knew, xk);
+      // the append (kv_cache.py:108-109)
+      if (ovalid && kk == 0) {
+        store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
+        store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
+      }
+    } else {
+      load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
+      first_sets();
+    }
+    float mo = kNegInf, lo = 0.f;
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+    // raise the quad's offset to mt when a score exceeds it by more than the
+    // lazy margin (one offset per quad row)
+    auto raise_offset = [&](float mt) __attribute__((always_inline)) {
+      if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
+      if (mt > mo + a.lazy_raw) {
+        const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
+        mo = mt;
+        lo *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+      }
+    };
+    auto add_key = [&](float score, const Slice& vr, float moff) __attribute__((always_inline)) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(score, cl, -moff));
+      lo += p;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr, e), acc[e]);
+    };
+    auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
+      float sv[UO];
+      float mt = kNegInf;
+#pragma unroll
+      for (int u = 0; u < UO; ++u) {
+        sv[u] = kNegInf;
+        if (j0 + KPQ * u >= Tc) continue;  // slot not loaded (wave-uniform)
+        const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
+        sv[u] = (j0 + KPQ * u + kk < Tc) ? dot : kNegInf;
+        mt = fmaxf(mt, sv[u]);
+      }
+      raise_offset(mt);
+      const float moff = mo * cl;
+#pragma unroll
+      for (int u = 0; u < UO; ++u) {
+        if (j0 + KPQ * u >= Tc) continue;
+        add_key(sv[u], vr[u], moff);
+      }
+    };
+    for (int j0 = P; j0 < Tc;) {
+      process(kA, vA, j0);
+      j0 += STEP;
+      if (j0 + STEP < Tc) load_set(kA, vA, j0 + STEP);
+      if (j0 >= Tc) break;
+      process(kB, vB, j0);
+      j0 += STEP;
+      if (j0 + STEP < Tc) load_set(kB, vB, j0 + STEP);
+    }
+    if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
+      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
+      const float sn = kk == 0 ? dot : kNegInf;
+      raise_offset(sn);
+      add_key(sn, vnew, mo * cl);
+    }
+    if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
+      lo += dpp<kDppQuadXor2>(lo);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] += dpp<kDppQuadXor2>(acc[e]);
+    }
+    // hand-over: row orow's offset, sum and weighted values
+    if (kk == 0) {
+      float* pr = part + orow * RS;
+#pragma unroll
+      for (int e4 = 0; e4 < EPL / 4; ++e4)
+        *reinterpret_cast<f32x4_t*>(pr + piece * EPL + 4 * e4) =
+            f32x4_t{acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]};
+      if (piece == 0) {
+        pr[D] = mo;
+        pr[D + 1] = lo;
+      }
     }
   }
+  __syncthreads();
+  if (role == 1) return;
 
-  if (P + STEP < Tc) load_set(kB, vB, P + STEP);
-
-  // --- own keys on the vector ALUs, from the prefix's offset (rescales stay rare)
-  float mo = lane_get(m, orow), lo = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  // raise the quad's offset to mt when a score exceeds it by more than the
-  // lazy margin (one offset per quad row)
-  auto raise_offset = [&](float mt) __attribute__((always_inline)) {
-    if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
-    if (mt > mo + a.lazy_raw) {
-      const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
-      mo = mt;
-      lo *= alpha;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
-    }
-  };
-  auto add_key = [&](float score, const Slice& vr, float moff) __attribute__((always_inline)) {
-    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(score, cl, -moff));
-    lo += p;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr, e), acc[e]);
-  };
-  auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
-    float sv[UO];
-    float mt = kNegInf;
-#pragma unroll
-    for (int u = 0; u < UO; ++u) {
-      sv[u] = kNegInf;
-      if (j0 + KPQ * u >= Tc) continue;  // slot not loaded (wave-uniform)
-      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
-      sv[u] = (j0 + KPQ * u + kk < Tc) ? dot : kNegInf;
-      mt = fmaxf(mt, sv[u]);
-    }
-    raise_offset(mt);
-    const float moff = mo * cl;
-#pragma unroll
-    for (int u = 0; u < UO; ++u) {
-      if (j0 + KPQ * u >= Tc) continue;
-      add_key(sv[u], vr[u], moff);
-    }
-  };
-  for (int j0 = P; j0 < Tc;) {
-    process(kA, vA, j0);
-    j0 += STEP;
-    if (j0 + STEP < Tc) load_set(kA, vA, j0 + STEP);
-    if (j0 >= Tc) break;
-    process(kB, vB, j0);
-    j0 += STEP;
-    if (j0 + STEP < Tc) load_set(kB, vB, j0 + STEP);
-  }
-  if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
-    const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
-    const float sn = kk == 0 ? dot : kNegInf;
-    raise_offset(sn);
-    add_key(sn, vnew, mo * cl);
-  }
-  if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
-    lo += dpp<kDppQuadXor2>(lo);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += dpp<kDppQuadXor2>(acc[e]);
-  }
-
-  // --- merge in the MFMA layout: lane (c, g) holds columns 16t + 4g + r -------
-  const float m_own = lane_get(mo, 4 * c), l_own = lane_get(lo, 4 * c);
+  // --- merge (wave 0): lane (c, g) holds columns 16t + 4g + r of row c ---------
+  const float* pr = part + c * RS;
+  const float m_own = pr[D], l_own = pr[D + 1];
   const float M = fmaxf(m, m_own);
   const float ao = (m_own == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m_own - M) * cl);
   const float ap = (m == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - M) * cl);
   const float inv = 1.0f / (row_sum4(lp) * ap + l_own * ao);
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
-    // column 16t + 4g + r sits in own lane 4c + (16t + 4g) / EPL, element
-    // (16t + 4g) % EPL + r
-    const int src = 4 * c + (16 * t + 4 * g) / EPL;
-    const int sel = (4 * g % EPL) / 4;
+    const f32x4_t own = *reinterpret_cast<const f32x4_t*>(pr + 16 * t + 4 * g);
     float out[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float own = 0.f;
-#pragma unroll
-      for (int s4 = 0; s4 < EPL / 4; ++s4) {
-        const float x = lane_get(acc[4 * s4 + r], src);
-        own = (s4 == sel) ? x : own;
-      }
-      out[r] = __builtin_fmaf(oacc[t][r], ap, own * ao) * inv;
-    }
+    for (int r = 0; r < 4; ++r) out[r] = __builtin_fmaf(oacc[t][r], ap, own[r] * ao) * inv;
     if (cvalid)
       store_vec<T, 4>(static_cast<T*>(a.y) + bc * a.yb + (int64_t)h * a.yh + 16 * t + 4 * g, out);
   }
@@ -480,8 +542,7 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 template <typename T, int D, bool FUSED, typename FT>
 int launch_shared(const SharedArgs& a, hipStream_t s) {
-  const int64_t blocks = (a.units + 3) / 4;
-  hipLaunchKernelGGL((attn_shared_kernel<T, D, FUSED, FT>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_shared_kernel<T, D, FUSED, FT>), dim3((unsigned)a.units), dim3(128), 0, s, a);
   return check_launch("attn_shared_kernel");
 }
 
