@@ -196,10 +196,13 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
 
 def prefill_leg(reps: int = 10):
     """B=256, T=1024, H=8, D=64 bf16, q/k/v in (B,T,H,D) projection
-    layout, RoPE base 1e4 + QK-norm fused in the first launch, causal attention
-    in the second.  attn_ms: mean over `reps` back-to-back attention launches
-    (one graph replay, HIP events on its stream); with_rope_ms: the same for
-    the two-launch step."""
+    layout, RoPE base 1e4 + QK-norm.  The model's step: RoPE + QK-norm of k in
+    a first launch, then dg_prefill_rope (causal attention that rotates and
+    normalises q as it loads it).  attn_ms: mean over `reps` back-to-back
+    dg_attention launches on the rotated q (one graph replay, HIP events on its
+    stream); with_rope_ms: the same for the model's two-launch step;
+    with_rope_unfused_ms: RoPE on q and k in the first launch, dg_attention in
+    the second."""
     import torch
 
     from diff_gpt import _native
@@ -214,7 +217,12 @@ def prefill_leg(reps: int = 10):
     ops = _native.ops()
     flop = 2.0 * B * H * D * T * (T + 1)
 
-    def step(with_rope: bool):
+    def step(with_rope):
+        if with_rope == "fused":
+            ops.rope_qknorm_append(None, k, None, fc, None, k_rot, None, True)
+            if not _native.prefill_rope_(q, fc, k_rot, v, y, 1.0 / D**0.5, True):
+                raise RuntimeError("configs[2] prefill is not taken by dg_prefill_rope")
+            return
         if with_rope:
             ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
         _native.attention_(q_rot, k_rot, v, y, 1.0 / D**0.5)
@@ -225,18 +233,22 @@ def prefill_leg(reps: int = 10):
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         step(True)
+        step("fused")
     torch.cuda.synchronize()
-    full, attn_only = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    full, attn_only, fused = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(full, stream=side):
         for _ in range(reps):
             step(True)
     with torch.cuda.graph(attn_only, stream=side):
         for _ in range(reps):
             step(False)
-    times, attn = [], []
+    with torch.cuda.graph(fused, stream=side):
+        for _ in range(reps):
+            step("fused")
+    times, attn, fused_t = [], [], []
     with torch.cuda.stream(side):
         for _ in range(3):
-            for graph, out in ((full, times), (attn_only, attn)):
+            for graph, out in ((full, times), (attn_only, attn), (fused, fused_t)):
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record(side)
                 graph.replay()
@@ -245,13 +257,15 @@ def prefill_leg(reps: int = 10):
                 out.append(a.elapsed_time(b) / 1e3 / reps)
     t_attn = sorted(attn)[len(attn) // 2]
     t_all = sorted(times)[len(times) // 2]
+    t_fused = sorted(fused_t)[len(fused_t) // 2]
     tf = flop / t_attn / 1e12
     return {
         "workload": "configs[2] causal prefill B=256 H=8 T=1024 D=64 bf16, RoPE+QK-norm",
         "tflops": tf,
         "attn_ms": t_attn * 1e3,
-        "with_rope_ms": t_all * 1e3,
-        "tflops_with_rope": flop / t_all / 1e12,
+        "with_rope_ms": t_fused * 1e3,
+        "tflops_with_rope": flop / t_fused / 1e12,
+        "with_rope_unfused_ms": t_all * 1e3,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS, "traffic": None},
     }

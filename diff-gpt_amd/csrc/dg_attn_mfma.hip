@@ -44,7 +44,7 @@
 // (b, h) run on the same XCD (blockIdx round-robins over the 8 XCDs), keeping
 // that head's K/V resident in one L2, and the longest (last) query blocks of a
 // head start first.
-#include "dg_common.h"
+#include "dg_rope_math.h"
 
 #ifndef DG_PREFILL_QW_D64
 #define DG_PREFILL_QW_D64 1
@@ -78,6 +78,11 @@ struct PrefillArgs {
   int win;     // (b, h) pairs per scheduling window
   float scale_log2;  // SDPA scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2: allowed growth of a row max in raw score units
+  // ROPE instances: (cos, sin) pairs of query row (b, i, h) at
+  // freqs + b*fb + i*ft + h*fh (D/2 pairs, contiguous), and the QK-norm flag
+  const void* freqs;
+  int64_t fb, ft, fh;
+  int qknorm;
 };
 
 template <typename T>
@@ -185,7 +190,7 @@ constexpr int prefill_wgs_per_cu() {
   return D == 64 ? 4 : 2;
 }
 
-template <typename T, int D, int QW>
+template <typename T, int D, int QW, bool ROPE, typename FT>
 __global__ __launch_bounds__(256, prefill_wgs_per_cu<D>())
 void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
@@ -231,38 +236,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   const T* kp = static_cast<const T*>(a.k) + b * a.kb + (int64_t)head * a.kh;
   const T* vp = static_cast<const T*>(a.v) + b * a.vb + (int64_t)head * a.vh;
 
-  // Q^T fragments (B operand): lane holds Q[qi][16c + 8hh .. +8]
-  vec8 qf[QW][NC];
-#pragma unroll
-  for (int qb = 0; qb < QW; ++qb) {
-    const int qi = qw + 32 * qb + r32;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      uint4 raw = make_uint4(0, 0, 0, 0);
-      if (qi < a.Tq) raw = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * a.qt + 16 * c + 8 * hh);
-      qf[qb][c] = __builtin_bit_cast(vec8, raw);
-    }
-  }
-
-  const int kv_end = min(a.Tk, q0 + C::BM + qoff);
-  const int ntiles = (kv_end + kBN - 1) / kBN;
-  const bool wave_live = qw < a.Tq;
-  const int wave_last_key = qw + 32 * QW - 1 + qoff;  // largest key any query of this wave sees
-
-  floatx16_t o[QW][NB];
-#pragma unroll
-  for (int qb = 0; qb < QW; ++qb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qb][nb][r] = 0.f;
-  float m[QW], l[QW];
-#pragma unroll
-  for (int qb = 0; qb < QW; ++qb) {
-    m[qb] = kNegInf;
-    l[qb] = 0.f;
-  }
-
   // ---- global -> LDS copy of one key tile (no registers involved) -----------
   // Wave wv copies DMA_PER_WAVE blocks of 1 KB of K and of V; lane l of a block
   // fills slot l % PPR of row l / PPR with the piece that the swizzle puts
@@ -285,6 +258,98 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_s_barrier();
   };
+
+  // Q^T fragments (B operand): lane holds Q[qi][16c + 8hh .. +8].  The first
+  // key tile's copies go out right behind the query loads.
+  vec8 qf[QW][NC];
+  if constexpr (ROPE) {
+    // RoPE + QK-norm of the query rows as they are loaded (mha.py:44-48), with
+    // the arithmetic and roundings of dg_rope_qknorm_append, so the operand
+    // has the bits that kernel would store: each 8-element chunk 16c + 8hh
+    // rotates with its (cos, sin) pairs; the norm's sum of squares follows the
+    // same pairwise tree over the row (chunk sums, the partner lane l^32 for
+    // 16-element sums, then across chunks).  Rows past Tq load zeros.
+#pragma clang fp contract(off)
+    float x[QW][NC][8], cs[QW][NC][8];
+#pragma unroll
+    for (int qb = 0; qb < QW; ++qb) {
+      const int qi = min(qw + 32 * qb + r32, a.Tq - 1);
+      const T* qrow = qp + (int64_t)qi * a.qt;
+      const FT* frow = static_cast<const FT*>(a.freqs) + b * a.fb + (int64_t)qi * a.ft + (int64_t)head * a.fh;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        load_vec<T, 8>(qrow + 16 * c + 8 * hh, x[qb][c]);
+        load_vec<FT, 8>(frow + 16 * c + 8 * hh, cs[qb][c]);
+      }
+    }
+    dma_tile(ks0, vs0, 0);
+#pragma unroll
+    for (int qb = 0; qb < QW; ++qb) {
+      const bool row_live = qw + 32 * qb + r32 < a.Tq;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        rope_rotate<T, 8>(x[qb][c], cs[qb][c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[qb][c][i] = row_live ? x[qb][c][i] : 0.f;
+      }
+      if (a.qknorm) {  // lanes l and l^32 hold the same row: both take this branch  // lanes l and l^32 hold the same row: both take this branch
+        float s16[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float sq[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sq[i] = x[qb][c][i] * x[qb][c][i];
+          s16[c] = half_pair_sum(tree_sum<8>(sq));
+        }
+        const float mean = tree_sum<NC>(s16) / (float)D;
+        const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[qb][c][i] = x[qb][c][i] * r;
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)from_f32<T>(x[qb][c][2 * i]).bits |
+                 ((uint32_t)from_f32<T>(x[qb][c][2 * i + 1]).bits << 16);
+        qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int qb = 0; qb < QW; ++qb) {
+      const int qi = qw + 32 * qb + r32;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (qi < a.Tq) raw = *reinterpret_cast<const uint4*>(qp + (int64_t)qi * a.qt + 16 * c + 8 * hh);
+        qf[qb][c] = __builtin_bit_cast(vec8, raw);
+      }
+    }
+    dma_tile(ks0, vs0, 0);
+  }
+
+  const int kv_end = min(a.Tk, q0 + C::BM + qoff);
+  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const bool wave_live = qw < a.Tq;
+  const int wave_last_key = qw + 32 * QW - 1 + qoff;  // largest key any query of this wave sees
+
+  floatx16_t o[QW][NB];
+#pragma unroll
+  for (int qb = 0; qb < QW; ++qb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qb][nb][r] = 0.f;
+  float m[QW], l[QW];
+#pragma unroll
+  for (int qb = 0; qb < QW; ++qb) {
+    m[qb] = kNegInf;
+    l[qb] = 0.f;
+  }
 
   // per-lane parts of the LDS operand addresses
   const int kswz = piece_swz<D>(r32);  // rows 32mb + r32 share it
@@ -397,8 +462,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     }
   };
 
-  if (ntiles > 0) dma_tile(ks0, vs0, 0);
-  stage_ready();
+  stage_ready();  // the first tile (Tk >= Tq >= 1, so every workgroup has one)
   for (int tile = 0; tile < ntiles; tile += 2) {
     const int kt0 = tile * kBN;
     if (tile + 1 < ntiles) dma_tile(ks1, vs1, kt0 + kBN);
@@ -444,7 +508,7 @@ constexpr int qw_for() {
   return D == 64 ? DG_PREFILL_QW_D64 : DG_PREFILL_QW_D128;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool ROPE = false, typename FT = T>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   constexpr int QW = qw_for<D>();
   constexpr int BM = PrefillCfg<T, D, QW>::BM;
@@ -452,7 +516,7 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
   const int64_t nwg = (int64_t)(a.nwg) * a.nqb;  // a.nwg holds B*H on entry
   DG_REQUIRE(nwg <= 0x7fffffffLL, DG_EINVAL, "prefill: too many workgroups");
   a.nwg = (int)nwg;
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW>), dim3((unsigned)a.nwg),
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW, ROPE, FT>), dim3((unsigned)a.nwg),
                      dim3(PrefillCfg<T, D, QW>::NT), 0, s, a);
   return check_launch("prefill_mfma_kernel");
 }
@@ -477,10 +541,10 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
          strides8(k_st) && strides8(v_st) && strides8(y_st);
 }
 
-int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
-                 const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
-                 const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                 hipStream_t s) {
+namespace {
+PrefillArgs prefill_args(int B, int H, int Tq, int Tk, const void* q, const dg_stride3* q_st, const void* k,
+                         const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+                         const dg_stride3* y_st, float scale) {
   PrefillArgs a{};
   a.q = q; a.k = k; a.v = v; a.y = y;
   a.qb = q_st->b; a.qt = q_st->t; a.qh = q_st->h;
@@ -495,8 +559,50 @@ int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.win = B * H < kPrefillWindow ? B * H : kPrefillWindow;
   a.scale_log2 = scale * 1.44269504088896340736f;
   a.lazy_raw = kLazyLog2 / a.scale_log2;
+  return a;
+}
+}  // namespace
+
+int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                 const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
+                 const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
+                 hipStream_t s) {
+  const PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
   if (dtype == DG_BF16) return D == 64 ? launch_prefill<bf16_t, 64>(a, s) : launch_prefill<bf16_t, 128>(a, s);
   return D == 64 ? launch_prefill<f16_t, 64>(a, s) : launch_prefill<f16_t, 128>(a, s);
+}
+
+// The fused form takes what the plain MFMA prefill takes, with (cos, sin) rows
+// that are 16-byte aligned, in the data's dtype or fp32.
+bool mfma_prefill_rope_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                                  const dg_stride3* q_st, const void* freqs, const dg_stride3* f_st,
+                                  int fdtype, const void* k, const dg_stride3* k_st, const void* v,
+                                  const dg_stride3* v_st, const void* y, const dg_stride3* y_st,
+                                  float scale) {
+  if (!mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale)) return false;
+  if (fdtype != dtype && fdtype != DG_F32) return false;
+  const int64_t fes = fdtype == DG_F32 ? 4 : 2;
+  if (!freqs || !aligned16(freqs)) return false;
+  for (int64_t st : {f_st->b, f_st->t, f_st->h})
+    if (st < 0 || (st * fes) % 16 != 0) return false;
+  return true;
+}
+
+int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
+                      const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, const void* k,
+                      const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+                      const dg_stride3* y_st, float scale, hipStream_t s) {
+  PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
+  a.freqs = freqs;
+  a.fb = f_st->b; a.ft = f_st->t; a.fh = f_st->h;
+  a.qknorm = qknorm;
+  const bool f32 = fdtype == DG_F32;
+  if (dtype == DG_BF16) {
+    if (D == 64) return f32 ? launch_prefill<bf16_t, 64, true, float>(a, s) : launch_prefill<bf16_t, 64, true, bf16_t>(a, s);
+    return f32 ? launch_prefill<bf16_t, 128, true, float>(a, s) : launch_prefill<bf16_t, 128, true, bf16_t>(a, s);
+  }
+  if (D == 64) return f32 ? launch_prefill<f16_t, 64, true, float>(a, s) : launch_prefill<f16_t, 64, true, f16_t>(a, s);
+  return f32 ? launch_prefill<f16_t, 128, true, float>(a, s) : launch_prefill<f16_t, 128, true, f16_t>(a, s);
 }
 
 }  // namespace dg

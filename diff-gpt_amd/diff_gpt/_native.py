@@ -28,6 +28,7 @@ LIB_PATH = Path(
 
 DG_F32, DG_BF16, DG_F16 = 0, 1, 2
 DG_QKNORM = 1
+DG_EUNSUPPORTED = -2
 _DTYPE_CODE = {torch.float32: DG_F32, torch.bfloat16: DG_BF16, torch.float16: DG_F16}
 
 
@@ -61,6 +62,14 @@ _SIGNATURES = {
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4
         + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
            ctypes.c_void_p],
+    ),
+    "dg_prefill_rope": (
+        ctypes.c_int,
+        [ctypes.c_int] * 6
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 2  # q, freqs
+        + [ctypes.c_int, ctypes.c_int]  # freqs dtype, flags
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 3  # k, v, y
+        + [ctypes.c_float, ctypes.c_void_p],
     ),
     "dg_rope_qknorm_append_at": (
         ctypes.c_int,
@@ -287,6 +296,37 @@ def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tenso
         float(scale), int(prefix_len), int(group), _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "attention")
+
+
+def prefill_rope_(q: torch.Tensor, freqs: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
+                  scale: float, qknorm: bool) -> bool:
+    """dg_prefill_rope: attention over k, v (B,Tk,H,D) views of the query rows
+    q (B,Tq,H,D) after RoPE (freqs (B|1,Tq,H|1,D/2,2)) and, with qknorm, the
+    QK-norm -- applied as the kernel loads q -- into y.  Returns False, having
+    done nothing, when the fused kernel does not take the shape (the caller
+    then makes the two calls); raises on any other error."""
+    B, Tq, H, D = q.shape
+    Tk = k.size(1)
+    if k.shape != (B, Tk, H, D) or v.shape != (B, Tk, H, D) or y.shape != q.shape:
+        raise ValueError("prefill_rope: inconsistent q/k/v/y shapes")
+    if not (q.dtype == k.dtype == v.dtype == y.dtype):
+        raise TypeError("prefill_rope: q/k/v/y must share one dtype")
+    if freqs.dim() != 5 or freqs.shape[-2:] != (D // 2, 2):
+        raise ValueError(f"freqs must be (B,T,H,D/2,2)-broadcastable, got {tuple(freqs.shape)}")
+    if freqs.stride(-1) != 1 or freqs.stride(-2) != 2:
+        freqs = freqs.contiguous()
+    if freqs.size(1) not in (1, Tq) or freqs.size(0) not in (1, B) or freqs.size(2) not in (1, H):
+        raise ValueError("freqs does not broadcast against (B,Tq,H)")
+    f_st = Stride3(*(0 if freqs.size(i) == 1 else freqs.stride(i) for i in range(3)))
+    st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
+    rc = lib().dg_prefill_rope(
+        B, H, Tq, Tk, D, _dtype_code(q), _ptr(q), st(q), _ptr(freqs), ctypes.pointer(f_st), _dtype_code(freqs),
+        DG_QKNORM if qknorm else 0, _ptr(k), st(k), _ptr(v), st(v), _ptr(y), st(y), float(scale), _stream(q),
+    )
+    if rc == DG_EUNSUPPORTED:
+        return False
+    _check(rc, "prefill_rope")
+    return True
 
 
 def rope_qknorm_append_at_(

@@ -14,6 +14,11 @@ Everything between the projections and the gate runs in libdgattn:
                                        straight into the (B,T,H*D) layout that
                                        mha.py:83 re-assembles.
 
+A prefill that the MFMA kernel takes (bf16/fp16, head_dim 64 or 128, at
+least 16 tokens) leaves q to the attention launch instead: dg_prefill_rope
+rotates and normalises the query rows as it loads them, with the bits the
+first launch would have stored.
+
 A decode step over a KV cache (one new token per row) makes one
 dg_decode_step call instead: the same RoPE, QK-norm and append, and the
 attention over the cache including the new token, in one launch where the
@@ -87,12 +92,16 @@ class MultiHeadAttention(nn.Module):
         if kv_cache is not None and T == 1:
             return self._decode_step(q, k, v, g, freqs_cis, kv_cache)
         assert kv_cache is None or kv_cache.pos_dev is None, "a captured decode step takes one token per row"
-        q_rot = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
+        # Prefills the MFMA kernel takes rotate and normalise q as they load it
+        # (dg_prefill_rope); the first launch then handles k and v only.
+        fuse_q = T >= 16 and D in (64, 128) and q.dtype in (torch.bfloat16, torch.float16)
+        q_rot = None if fuse_q else torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
+        q_in = None if fuse_q else q
         if kv_cache is None:
             # no cache: normalised keys go to a scratch tensor, values are read
             # in place from the projection output
-            k_rot = torch.empty_like(q_rot)
-            ops.rope_qknorm_append(q, k, None, freqs_cis, q_rot, k_rot, None, True)
+            k_rot = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
+            ops.rope_qknorm_append(q_in, k, None, freqs_cis, q_rot, k_rot, None, True)
             keys, values = k_rot, v
         else:
             t0, t1 = kv_cache.ensure_window(T, k.dtype, k.device)
@@ -104,7 +113,7 @@ class MultiHeadAttention(nn.Module):
             # (B,H,T,D) cache pages seen as (B,T,H,D) views
             k_dst = cache[self.layer_idx, 0, :, :, t0:t1, :].transpose(1, 2)
             v_dst = cache[self.layer_idx, 1, :, :, t0:t1, :].transpose(1, 2)
-            ops.rope_qknorm_append(q, k, v, freqs_cis, q_rot, k_dst, v_dst, True)
+            ops.rope_qknorm_append(q_in, k, v, freqs_cis, q_rot, k_dst, v_dst, True)
             k_all, v_all = kv_cache.layer_views(self.layer_idx, t1)
             keys, values = k_all.transpose(1, 2), v_all.transpose(1, 2)
             kv_cache.advance(self.layer_idx, t1)
@@ -113,7 +122,17 @@ class MultiHeadAttention(nn.Module):
         # SDPA default scale 1/sqrt(head_dim); the mask follows from Tq vs Tk.
         # A broadcast prefix (KVCache.prefill) is read once per row group.
         prefix_len, group = (0, 1) if kv_cache is None or shared is None else shared
-        y = ops.attention(q_rot, keys, values, 1.0 / math.sqrt(D), prefix_len, group)
+        scale = 1.0 / math.sqrt(D)
+        y = None
+        if fuse_q:
+            y = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
+            if not _native.prefill_rope_(q, freqs_cis, keys, values, y, scale, True):
+                # a layout the fused kernel does not take (alignment): rotate q apart
+                q_rot = torch.empty_like(y)
+                ops.rope_qknorm_append(q, None, None, freqs_cis, q_rot, None, None, True)
+                y = None
+        if y is None:
+            y = ops.attention(q_rot, keys, values, scale, prefix_len, group)
         y = y.view(B, T, H * D)
         ops.gate_(y, g)  # y * sigmoid(g)
         return self.c_proj(y)

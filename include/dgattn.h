@@ -120,6 +120,26 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Prefill attention with RoPE and QK-norm of the queries fused in: "Prefill
+ * fuses RoPE" of mha.py:44-48 + 61-81.  y = dg_attention(norm(rope(q)), k, v)
+ * where norm(rope(q)) is what dg_rope_qknorm_append would store for q (the
+ * same roundings and reduction order, so y is dg_attention's on that q bit
+ * for bit) and k, v are the cache views (keys already rotated, e.g. by
+ * dg_rope_qknorm_append with q = NULL appending them).  freqs / f_st /
+ * freqs_dtype as in dg_rope_qknorm_append, for the Tq query rows; flags:
+ * DG_QKNORM or 0.  Only the MFMA prefill kernel's shapes are taken (bf16 or
+ * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
+ * freqs in the data's dtype or fp32): anything else returns DG_EUNSUPPORTED
+ * and does nothing, and the caller makes the two calls.
+ */
+DG_API int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype,
+                           const void* q, const dg_stride3* q_st,
+                           const void* freqs, const dg_stride3* f_st, int freqs_dtype, int flags,
+                           const void* k, const dg_stride3* k_st,
+                           const void* v, const dg_stride3* v_st,
+                           void* y, const dg_stride3* y_st, float scale, void* stream);
+
+/*
  * dg_attention over a batch whose rows come in groups sharing a prefix: for
  * row b, keys j < prefix_len are read from row (b / group) * group of k and v
  * instead of row b; keys j >= prefix_len from row b itself.  This is the

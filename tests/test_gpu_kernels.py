@@ -163,6 +163,60 @@ def test_prefill_attention_parity(dev, dtype, shape):
     assert err <= TOL[dtype], err
 
 
+PREFILL_ROPE = [  # (B, H, Tq, Tk, D)
+    (2, 3, 200, 200, 64),   # causal, ragged last query block
+    (1, 2, 130, 330, 128),  # chunked (bottom-right mask), D = 128
+    (2, 2, 16, 16, 64),     # smallest prefill the fused kernel takes
+    (1, 2, 640, 640, 128),  # several query blocks per head
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("fdt", ["f32", "data"])
+@pytest.mark.parametrize("qknorm", [True, False], ids=["qknorm", "rope"])
+@pytest.mark.parametrize("shape", PREFILL_ROPE, ids=lambda s: "x".join(map(str, s)))
+def test_prefill_rope_equals_rope_then_attention(dev, dtype, fdt, qknorm, shape):
+    """dg_prefill_rope rotates (and normalises) q as it loads it; y must be
+    bit-identical to dg_rope_qknorm_append on q followed by dg_attention.  q is
+    a column slice of a wider projection row (strided), as in the model."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, Tq, Tk, D = shape
+    wide = _randn((B, Tq, 3 * H * D), 50 + D, dtype, 2.0).to(dev)
+    q = wide[..., H * D : 2 * H * D].view(B, Tq, H, D)
+    k = _randn((B, Tk, H, D), 51 + D, dtype).to(dev)
+    v = _randn((B, Tk, H, D), 52 + D, dtype).to(dev)
+    table = precompute_freqs_cis(D, 2 * Tk, 10000).to(dev)
+    freqs = table[Tk - Tq : Tk].view(1, Tq, 1, D // 2, 2)
+    if fdt == "data":
+        freqs = freqs.to(TDT[dtype])
+    scale = 1.0 / D**0.5
+    y = torch.empty((B, Tq, H, D), dtype=TDT[dtype], device=dev)
+    assert _native.prefill_rope_(q, freqs, k, v, y, scale, qknorm)
+    q_rot = torch.empty_like(y)
+    _native.rope_qknorm_append_(q, None, None, freqs, q_rot, None, None, qknorm)
+    y2 = torch.empty_like(y)
+    _native.attention_(q_rot, k, v, y2, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 64), "f32"),
+                                         ((1, 2, 8, 8, 64), "bf16")])
+def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
+    """Shapes the MFMA kernel does not take return False and leave y alone."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, Tq, Tk, D = shape
+    q, k, v = (_randn((B, Tq, H, D), 60 + i, dtype).to(dev) for i in range(3))
+    freqs = precompute_freqs_cis(D, 2 * Tk, 10000).to(dev)[:Tq].view(1, Tq, 1, D // 2, 2)
+    y = torch.full((B, Tq, H, D), 7.0, dtype=TDT[dtype], device=dev)
+    assert not _native.prefill_rope_(q, freqs, k, v, y, 1.0 / D**0.5, True)
+    assert bool((y == 7.0).all())
+
+
 def test_decode_without_workspace_matches_split(dev):
     """A NULL workspace forces the single-pass path; both agree with fp64."""
     from diff_gpt import _native

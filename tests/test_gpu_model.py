@@ -211,6 +211,45 @@ def test_mha_chunked_prefill_then_decode(dev):
     assert_close(torch.cat([a, b, c], 1), full, atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_mha_bf16_prefill_fused_rope_equals_two_calls(dev, monkeypatch, D):
+    """A bf16 prefill with head_dim 64/128 and >= 16 tokens rotates q inside
+    the attention launch (dg_prefill_rope); forcing the two-call path (the
+    fallback for layouts the fused kernel declines) must give the same bits,
+    without a cache and with a chunk over a KV cache."""
+    from diff_gpt import _native
+    from diff_gpt.model.kv_cache import KVCache
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(4)
+    H = 2
+    m = MultiHeadAttention(H * D, H, 0).to(dev).to(torch.bfloat16).eval()
+    x = torch.randn(2, 48, H * D, device=dev).to(torch.bfloat16)
+    fc = _fc(48, D, dev, seed=4)
+    calls = []
+    real = _native.prefill_rope_
+
+    def spy(*a, **k):
+        calls.append(1)
+        return real(*a, **k)
+
+    def run():
+        kv = KVCache(batch_size=2, num_heads=H, seq_len=64, head_dim=D, num_layers=1)
+        with torch.no_grad():
+            full = m(x, fc, None)
+            a = m(x[:, :20], fc[:, :20], kv)
+            b = m(x[:, 20:], fc[:, 20:], kv)
+        return full, a, b
+
+    monkeypatch.setattr(_native, "prefill_rope_", spy)
+    fused = run()
+    assert len(calls) == 3
+    monkeypatch.setattr(_native, "prefill_rope_", lambda *a, **k: False)
+    plain = run()
+    for f, p in zip(fused, plain):
+        assert torch.equal(f, p)
+
+
 def test_block_kv_step_consistency(dev):
     # test_block.py:129-166 (AttnRes active, layers_per_block=2)
     from diff_gpt.model.block import Block
