@@ -3,7 +3,8 @@
 //
 // Workgroup = 4 wavefronts; each wavefront owns QW blocks of 32 queries of one
 // (b, h), so a workgroup covers BM = 128*QW queries.  Keys stream through two
-// LDS stages in tiles of BN = 64: every wave copies its share of the next tile
+// LDS stages in tiles of BN keys (64 at D = 64, 32 at D = 128; the text below
+// writes BN = 64): every wave copies its share of the next tile
 // straight from global memory into LDS (global_load_lds_dwordx4: no registers,
 // no shuffles) while the current tile is computed, then waits for its own
 // copies and meets the others at one barrier per tile.  K and V tiles are kept
@@ -125,7 +126,26 @@ struct MfmaOps<f16_t> {
   }
 };
 
-constexpr int kBN = 64;             // keys per tile
+#ifndef DG_PREFILL_BN_D64
+#define DG_PREFILL_BN_D64 64
+#endif
+#ifndef DG_PREFILL_WGS_D64
+#define DG_PREFILL_WGS_D64 4
+#endif
+#ifndef DG_PREFILL_BN_D128
+#define DG_PREFILL_BN_D128 32
+#endif
+#ifndef DG_PREFILL_WGS_D128
+#define DG_PREFILL_WGS_D128 3
+#endif
+
+// Keys per tile: 64 at D = 64; 32 at D = 128, which halves the S and P
+// registers (168 VGPRs) and the LDS stages (32 KB per workgroup), so three
+// workgroups share a CU instead of two (+4 to +10 % at configs[4]'s shapes).
+template <int D>
+constexpr int prefill_bn() {
+  return D == 64 ? DG_PREFILL_BN_D64 : DG_PREFILL_BN_D128;
+}
 constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
@@ -152,9 +172,13 @@ struct PrefillCfg {
   static constexpr int NC = D / 16;               // 16-wide contraction chunks of QK^T
   static constexpr int NB = D / 32;               // 32-row blocks of O^T
   static constexpr int PPR = D / 8;               // 16-byte pieces per K/V row
-  static constexpr int TILE = kBN * D;            // elements of one K or V tile
+  static constexpr int BN = prefill_bn<D>();       // keys per tile
+  static constexpr int MB = BN / 32;              // 32-key blocks of S^T per tile
+  static constexpr int PC = BN / 16;              // 16-key chunks of P^T per tile
+  static constexpr int TILE = BN * D;             // elements of one K or V tile
   static constexpr int ROWS_PER_DMA = 64 / PPR;   // rows one wave-wide 1 KB copy covers
-  static constexpr int DMA_PER_WAVE = kBN / ROWS_PER_DMA / WAVES;
+  static constexpr int DMA_PER_WAVE = BN / ROWS_PER_DMA / WAVES;
+  static_assert(DMA_PER_WAVE >= 1 && BN % (ROWS_PER_DMA * WAVES) == 0, "tile copy split");
   static constexpr int LDS_BYTES = 4 * TILE * 2;  // K and V, two stages
 };
 
@@ -184,10 +208,10 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
 
 // Resident workgroups per CU the register allocation must allow: D = 64 fits
 // 4 (<= 128 VGPRs -> 4 waves per SIMD to overlap one wave's MFMAs with
-// another's softmax); D = 128 is LDS-limited to 2.
+// another's softmax); D = 128 with 32-key tiles 3 (<= 168 VGPRs).
 template <int D>
 constexpr int prefill_wgs_per_cu() {
-  return D == 64 ? 4 : 2;
+  return D == 64 ? DG_PREFILL_WGS_D64 : DG_PREFILL_WGS_D128;
 }
 
 template <typename T, int D, int QW, bool ROPE, typename FT>
@@ -196,7 +220,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
   using C = PrefillCfg<T, D, QW>;
-  constexpr int NC = C::NC, NB = C::NB, PPR = C::PPR;
+  constexpr int NC = C::NC, NB = C::NB, PPR = C::PPR, BN = C::BN, MB = C::MB, PC = C::PC;
 
   // two ring stages, K and V each in an array of its own: the compiler can
   // then tell the stage being copied into from the one being read
@@ -333,7 +357,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   }
 
   const int kv_end = min(a.Tk, q0 + C::BM + qoff);
-  const int ntiles = (kv_end + kBN - 1) / kBN;
+  const int ntiles = (kv_end + BN - 1) / BN;
   const bool wave_live = qw < a.Tq;
   const int wave_last_key = qw + 32 * QW - 1 + qoff;  // largest key any query of this wave sees
 
@@ -368,15 +392,15 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 
   auto compute_tile = [&](const uint16_t* Ks, const uint16_t* Vs, int kt0) __attribute__((always_inline)) {
     // S^T = K . Q^T for the two 32-key halves of the tile
-    floatx16_t s[QW][2];
+    floatx16_t s[QW][MB];
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb)
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const uint4 raw =
@@ -388,13 +412,13 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     }
 
     // mask (only on tiles that cross the diagonal or the end of the keys)
-    const bool needs_mask = (kt0 + kBN - 1 > qw + qoff) || (kt0 + kBN > a.Tk);
+    const bool needs_mask = (kt0 + BN - 1 > qw + qoff) || (kt0 + BN > a.Tk);
     if (needs_mask) {
 #pragma unroll
       for (int qb = 0; qb < QW; ++qb) {
         const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
 #pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
@@ -403,13 +427,13 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       }
     }
 
-    vec8 pf[QW][4];
+    vec8 pf[QW][PC];
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb) {
       // tile max of the raw scores (scale > 0, so it commutes with the max)
       float mt = s[qb][0][0];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
       mt = half_pair_max(mt);
@@ -430,7 +454,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       const float moff = m[qb] * a.scale_log2;
       float ls = l[qb];
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           uint32_t w[4];
@@ -452,7 +476,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < PC; ++c) {
         const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
         const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
         const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
@@ -464,13 +488,13 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 
   stage_ready();  // the first tile (Tk >= Tq >= 1, so every workgroup has one)
   for (int tile = 0; tile < ntiles; tile += 2) {
-    const int kt0 = tile * kBN;
-    if (tile + 1 < ntiles) dma_tile(ks1, vs1, kt0 + kBN);
+    const int kt0 = tile * BN;
+    if (tile + 1 < ntiles) dma_tile(ks1, vs1, kt0 + BN);
     if (wave_live && kt0 <= wave_last_key) compute_tile(ks0, vs0, kt0);
     stage_ready();  // stage 1 filled; every wave is done with stage 0
     if (tile + 1 >= ntiles) break;
-    if (tile + 2 < ntiles) dma_tile(ks0, vs0, kt0 + 2 * kBN);
-    if (wave_live && kt0 + kBN <= wave_last_key) compute_tile(ks1, vs1, kt0 + kBN);
+    if (tile + 2 < ntiles) dma_tile(ks0, vs0, kt0 + 2 * BN);
+    if (wave_live && kt0 + BN <= wave_last_key) compute_tile(ks1, vs1, kt0 + BN);
     stage_ready();
   }
 
