@@ -146,7 +146,10 @@ template <int D>
 constexpr int prefill_bn() {
   return D == 64 ? DG_PREFILL_BN_D64 : DG_PREFILL_BN_D128;
 }
-constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
+#ifndef DG_PREFILL_WINDOW
+#define DG_PREFILL_WINDOW 64
+#endif
+constexpr int kPrefillWindow = DG_PREFILL_WINDOW;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
 // max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
