@@ -195,7 +195,6 @@ __device__ __forceinline__ int piece_swz(int r) {
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
 
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 // 16 bytes per lane from global memory straight into LDS: lane l of the wave
 // writes lds + 16*l (lds wave-uniform), no registers involved

@@ -77,35 +77,6 @@ struct SharedArgs {
 constexpr float kSharedLazyLog2 = 8.0f;
 constexpr int kSharedMinGroup = 16;
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
-
-// S^T += A B over one contraction step of 4 (fp32) or 16 (16-bit) elements.
-template <typename T, int DQ>
-__device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowRegs<T, DQ>& qop, f32x4_t acc) {
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int s = 0; s < DQ; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kop.w[s]), __uint_as_float(qop.w[s]), acc,
-                                                 0, 0, 0);
-  } else {
-    static_assert(DQ % 4 == 0, "16-bit operands come in runs of 4");
-#pragma unroll
-    for (int s = 0; s < DQ / 4; ++s) {
-      const uint32_t ka[2] = {kop.w[2 * s], kop.w[2 * s + 1]};
-      const uint32_t qa[2] = {qop.w[2 * s], qop.w[2 * s + 1]};
-      if constexpr (__is_same(T, bf16_t))
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, ka),
-                                                        __builtin_bit_cast(i16x4_t, qa), acc, 0, 0, 0);
-      else
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, ka),
-                                                    __builtin_bit_cast(f16x4_t, qa), acc, 0, 0, 0);
-    }
-  }
-  return acc;
-}
-
 // Max / sum over the four lanes c, c+16, c+32, c+48 of a tile row (identical
 // bits in all four).
 __device__ __forceinline__ float row_max4(float x) {

@@ -11,6 +11,10 @@
 //   swiglu_kernel         clamped SwiGLU on interleaved (gate, linear) pairs
 //                         (swi_glu.py:11-19)
 //   softcap_kernel        cap * tanh(x / cap) (gpt.py:182-186)
+//   lm_head_kernel        the tied lm_head GEMM, the softcap and, for greedy
+//                         sampling, the argmax of each row (gpt.py:181-186,
+//                         temperature.py:22-23) in one pass: the logits are
+//                         written once and not read back
 //
 // Every intermediate is rounded to the storage dtype where the torch op
 // sequence rounds it (each op returns a tensor of the input dtype; fp32
@@ -240,6 +244,129 @@ int res_pick(int npad, const AttnResArgs& a, hipStream_t s) {
   return DG_EUNSUPPORTED;
 }
 
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// lm_head + softcap + greedy argmax.  Block = 4 waves = 16 rows of x; wave w
+// takes the vocabulary entries [w V/4, (w+1) V/4) in NTW tiles of 16.  Per
+// tile, logits^T (16 entries x 16 rows) = W_tile x^T on the matrix cores with
+// qk_mfma's lane mapping: lane (c, g) feeds embedding row 16t + c and x row c,
+// each with the contiguous quarter g of the contraction (chunks of 16
+// elements), and gets back row c's logits for entries 16t + 4g .. 16t + 4g + 3.
+// The logit is rounded to T (F.linear's output), then capped with
+// softcap_kernel's arithmetic and rounding, stored, and compared: the first
+// maximum wins (torch.argmax), across the lane's values in entry order, the
+// four lanes of a row, then the four waves through LDS.
+// ---------------------------------------------------------------------------
+struct LmHeadArgs {
+  const void* x;  // (M, C) rows, already normalised (gpt.py:181 rms_norm)
+  const void* w;  // (V, C) tied embedding table
+  void* logits;   // (M, V)
+  int64_t* ids;   // (M,) or null
+  int64_t x_ld, w_ld, l_ld, M;
+  int C, V;
+  float cap;  // 0: no softcap
+};
+
+template <typename T, int NTW>
+__global__ __launch_bounds__(256) void lm_head_kernel(const LmHeadArgs a) {
+#pragma clang fp contract(off)
+  constexpr int KCH = 16;  // contraction elements per lane and chunk
+  __shared__ float red_v[4][16];
+  __shared__ int red_i[4][16];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const bool row_ok = row0 + c < a.M;
+  const int64_t row = row_ok ? row0 + c : a.M - 1;
+  const int cq = a.C / 4;  // this lane's quarter of the contraction
+  const int vbase = w * (a.V / 4);
+  const T* xr = static_cast<const T*>(a.x) + row * a.x_ld + g * cq;
+  const T* wr = static_cast<const T*>(a.w) + (int64_t)(vbase + c) * a.w_ld + g * cq;
+
+  f32x4_t acc[NTW];
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < cq; k0 += KCH) {
+    RowRegs<T, KCH> xo;
+    load_row<T, KCH>(xo, xr + k0);
+#pragma unroll
+    for (int t = 0; t < NTW; ++t) {
+      RowRegs<T, KCH> wo;
+      load_row<T, KCH>(wo, wr + (int64_t)16 * t * a.w_ld + k0);
+      acc[t] = qk_mfma<T, KCH>(wo, xo, acc[t]);
+    }
+  }
+
+  float best = kNegInf;
+  int bidx = 0x7fffffff;
+  T* lrow = static_cast<T*>(a.logits) + row * a.l_ld + vbase + 4 * g;
+#pragma unroll
+  for (int t = 0; t < NTW; ++t) {
+    float out[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = rt<T>(acc[t][r]);
+      if (a.cap > 0.f) v = rt<T>(a.cap * rt<T>(tanhf(rt<T>(v / a.cap))));
+      out[r] = v;
+      const int e = vbase + 16 * t + 4 * g + r;  // increasing within the lane
+      if (v > best) {
+        best = v;
+        bidx = e;
+      }
+    }
+    if (row_ok) store_vec<T, 4>(lrow + 16 * t, out);
+  }
+  if (a.ids == nullptr) return;  // uniform over the grid
+  // the row's four lanes: larger value, or equal value and smaller entry
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float ov = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bidx, off, 64);
+    if (ov > best || (ov == best && oi < bidx)) {
+      best = ov;
+      bidx = oi;
+    }
+  }
+  if (g == 0) {
+    red_v[w][c] = best;
+    red_i[w][c] = bidx;
+  }
+  __syncthreads();
+  if (w != 0 || g != 0 || !row_ok) return;
+  // waves in entry order: a strictly larger value replaces the earlier one
+  float bv = red_v[0][c];
+  int bi = red_i[0][c];
+#pragma unroll
+  for (int q = 1; q < 4; ++q) {
+    if (red_v[q][c] > bv) {
+      bv = red_v[q][c];
+      bi = red_i[q][c];
+    }
+  }
+  a.ids[row0 + c] = (int64_t)(bi == 0x7fffffff ? 0 : bi);
+}
+
+namespace {
+
+template <typename T>
+int launch_lm_head(const LmHeadArgs& a, hipStream_t s) {
+  const int ntw = a.V / 64;
+  const unsigned blocks = (unsigned)((a.M + 15) / 16);
+  switch (ntw) {
+    case 1: hipLaunchKernelGGL((lm_head_kernel<T, 1>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((lm_head_kernel<T, 2>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((lm_head_kernel<T, 4>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((lm_head_kernel<T, 8>), dim3(blocks), dim3(256), 0, s, a); break;
+    case 16: hipLaunchKernelGGL((lm_head_kernel<T, 16>), dim3(blocks), dim3(256), 0, s, a); break;
+    default:
+      set_error("lm_head: vocabulary %d unsupported (64, 128, 256, 512 or 1024)", a.V);
+      return DG_EUNSUPPORTED;
+  }
+  return check_launch("lm_head_kernel");
+}
+
 // one thread per output element; K<T> for the dtype
 #define DG_LAUNCH_ROWS(K, dtype, a, s)                                                        \
   do {                                                                                        \
@@ -335,4 +462,31 @@ extern "C" int dg_softcap(int64_t M, int N, int dtype, const void* x, int64_t x_
   a.x_ld = x_ld; a.out_ld = out_ld; a.M = M; a.N = N;
   a.p0 = cap;
   DG_LAUNCH_ROWS(softcap_kernel, dtype, a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dg_lm_head(int64_t M, int C, int V, int dtype, const void* x, int64_t x_ld, const void* w,
+                          int64_t w_ld, float cap, void* logits, int64_t logits_ld, int64_t* ids, void* stream) {
+  DG_REQUIRE(M >= 0 && C >= 1 && V >= 1, DG_EINVAL, "lm_head: bad sizes M=%lld C=%d V=%d", (long long)M, C, V);
+  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "lm_head: dtype %d unsupported", dtype);
+  DG_REQUIRE(cap >= 0.f, DG_EINVAL, "lm_head: cap must be >= 0 (got %g)", (double)cap);
+  DG_REQUIRE(C % 64 == 0 && C <= 8192, DG_EUNSUPPORTED, "lm_head: n_embd %d unsupported (a multiple of 64)", C);
+  DG_REQUIRE(V == 64 || V == 128 || V == 256 || V == 512 || V == 1024, DG_EUNSUPPORTED,
+             "lm_head: vocabulary %d unsupported (64, 128, 256, 512 or 1024)", V);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(M <= (int64_t)16 * 0x7fffffffLL, DG_EINVAL, "lm_head: too many rows (%lld)", (long long)M);
+  DG_REQUIRE(x != nullptr && w != nullptr && logits != nullptr, DG_EINVAL, "lm_head: NULL pointer");
+  DG_REQUIRE(x_ld >= C && w_ld >= C && logits_ld >= V, DG_EINVAL, "lm_head: row stride smaller than the row");
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  auto al = [](const void* p, int64_t n) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)n) == 0; };
+  DG_REQUIRE(al(x, 16) && al(w, 16) && al(logits, 4 * es) && (x_ld * es) % 16 == 0 && (w_ld * es) % 16 == 0 &&
+                 (logits_ld * es) % (4 * es) == 0,
+             DG_EUNSUPPORTED, "lm_head: rows must be 16-byte aligned");
+  LmHeadArgs a{};
+  a.x = x; a.w = w; a.logits = logits; a.ids = ids;
+  a.x_ld = x_ld; a.w_ld = w_ld; a.l_ld = logits_ld; a.M = M;
+  a.C = C; a.V = V; a.cap = cap;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == DG_F32) return launch_lm_head<float>(a, s);
+  if (dtype == DG_BF16) return launch_lm_head<bf16_t>(a, s);
+  return launch_lm_head<f16_t>(a, s);
 }

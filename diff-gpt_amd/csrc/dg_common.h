@@ -324,6 +324,42 @@ __device__ __forceinline__ float slice_dot(const RowRegs<T, EPL>& q, const RowRe
   return d;
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+// 16 x 16 tile product D += A B^T over the lanes' slices, on the matrix
+// cores: lane (c, g) = (l & 15, l >> 4) feeds row c of A and row c of B, each
+// with its DQ contiguous elements of the contraction (the same permutation of
+// the contraction index for both operands, so the dot products are
+// unchanged), and gets back D[c][4g .. 4g+3] read as: row 4g + r of A against
+// row c of B, i.e. D^T.  fp32 takes v_mfma_f32_16x16x4_f32 (fp32 products);
+// bf16 / fp16 take v_mfma_f32_16x16x16_{bf16,f16} (exact products of two
+// 16-bit floats, fp32 accumulation).
+template <typename T, int DQ>
+__device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowRegs<T, DQ>& qop, f32x4_t acc) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int s = 0; s < DQ; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kop.w[s]), __uint_as_float(qop.w[s]), acc,
+                                                 0, 0, 0);
+  } else {
+    static_assert(DQ % 4 == 0, "16-bit operands come in runs of 4");
+#pragma unroll
+    for (int s = 0; s < DQ / 4; ++s) {
+      const uint32_t ka[2] = {kop.w[2 * s], kop.w[2 * s + 1]};
+      const uint32_t qa[2] = {qop.w[2 * s], qop.w[2 * s + 1]};
+      if constexpr (__is_same(T, bf16_t))
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, ka),
+                                                        __builtin_bit_cast(i16x4_t, qa), acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, ka),
+                                                    __builtin_bit_cast(f16x4_t, qa), acc, 0, 0, 0);
+    }
+  }
+  return acc;
+}
+
 }  // namespace dg
 
 // ---------------------------------------------------------------------------

@@ -63,6 +63,12 @@ _SIGNATURES = {
         + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
            ctypes.c_void_p],
     ),
+    "dg_lm_head": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_void_p],
+    ),
     "dg_prefill_rope": (
         ctypes.c_int,
         [ctypes.c_int] * 6
@@ -326,6 +332,32 @@ def prefill_rope_(q: torch.Tensor, freqs: torch.Tensor, k: torch.Tensor, v: torc
     if rc == DG_EUNSUPPORTED:
         return False
     _check(rc, "prefill_rope")
+    return True
+
+
+def lm_head_(x: torch.Tensor, w: torch.Tensor, cap: float, logits: torch.Tensor,
+             ids: torch.Tensor | None = None) -> bool:
+    """dg_lm_head: logits (M, V) = softcap(x (M, C) @ w (V, C)^T) with cap
+    (0 = none), and with ids (M,) int64 the first maximum of every logits row.
+    Returns False, having done nothing, when the fused kernel does not take the
+    shape (the caller then runs F.linear + softcap + argmax)."""
+    M, C = x.shape
+    V = w.size(0)
+    if w.shape != (V, C) or logits.shape != (M, V):
+        raise ValueError("lm_head: inconsistent x/w/logits shapes")
+    if not (x.dtype == w.dtype == logits.dtype):
+        raise TypeError("lm_head: x, w and logits must share one dtype")
+    if x.stride(1) != 1 or w.stride(1) != 1 or logits.stride(1) != 1:
+        return False
+    if ids is not None and (ids.shape != (M,) or ids.dtype != torch.int64 or not ids.is_contiguous()):
+        raise ValueError("lm_head: ids must be a contiguous (M,) int64 tensor")
+    rc = lib().dg_lm_head(
+        M, C, V, _dtype_code(x), _ptr(x), x.stride(0), _ptr(w), w.stride(0), float(cap),
+        _ptr(logits), logits.stride(0), _ptr(ids), _stream(x),
+    )
+    if rc == DG_EUNSUPPORTED:
+        return False
+    _check(rc, "lm_head")
     return True
 
 

@@ -18,6 +18,7 @@ from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.model.rms_norm import rms_norm
 from diff_gpt.model.rope import precompute_freqs_cis
 from diff_gpt.sampler.sampler import Sampler
+from diff_gpt.sampler.temperature import TemperatureSampler
 
 
 def _gaussian_soft_ce(
@@ -140,12 +141,37 @@ class GPT(BaseGPT):
         self.logit_softcap = logit_softcap
         self.label_smoothing_sigma = label_smoothing_sigma
 
+    def _head(self, partial: torch.Tensor, argmax_out: torch.Tensor | None) -> torch.Tensor:
+        """rms_norm -> tied lm_head -> softcap (gpt.py:181-186): one dg_lm_head
+        launch after the norm, which also writes each row's argmax into
+        argmax_out (B, T) when given; F.linear + dg_softcap (+ torch.argmax) for
+        shapes it does not take."""
+        xn = rms_norm(partial)
+        B, T, C = xn.shape
+        V = self.lm_head.weight.size(0)
+        cap = float(self.logit_softcap)
+        logits = torch.empty((B, T, V), dtype=xn.dtype, device=xn.device)
+        ids = None if argmax_out is None else argmax_out.view(B * T)
+        if _native.lm_head_(xn.view(B * T, C), self.lm_head.weight, cap, logits.view(B * T, V), ids):
+            return logits
+        logits = self.lm_head(xn)
+        if cap > 0:
+            _native.ops().softcap_(logits, cap)  # cap * tanh(logits / cap)
+        if argmax_out is not None:
+            argmax_out.copy_(torch.argmax(logits, dim=-1))
+        return logits
+
     def forward(
         self,
         idx: torch.Tensor,
         targets: torch.Tensor | None = None,
         kv_cache: KVCache | None = None,
+        *,
+        _argmax_out: torch.Tensor | None = None,
     ) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """gpt.py:140-200.  _argmax_out (B, T) int64, when given, receives the
+        first maximum of every logits row (greedy sampling without a separate
+        argmax launch)."""
         B, T = idx.shape
         start = 0 if kv_cache is None else kv_cache.get_pos()
         end = start + T
@@ -165,9 +191,7 @@ class GPT(BaseGPT):
         for block in self.blocks:
             blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache)
 
-        logits = self.lm_head(rms_norm(partial))
-        if self.logit_softcap > 0:
-            _native.ops().softcap_(logits, float(self.logit_softcap))  # cap * tanh(logits / cap)
+        logits = self._head(partial, _argmax_out)
 
         loss = None
         if targets is not None:
@@ -199,8 +223,15 @@ class GPT(BaseGPT):
         B, T = idx.shape
         out = torch.zeros((B, T + max_new_tokens), dtype=torch.int64, device=device)
         out[:, :T] = idx
+        # greedy: the argmax comes out of the lm_head launch (temperature.py:22-23)
+        greedy = type(sampler) is TemperatureSampler and sampler.temperature == 0
         for cur in range(T, T + max_new_tokens):
             window = out[:, max(0, cur - self.block_size) : cur]
+            if greedy:
+                am = torch.empty(window.shape, dtype=torch.int64, device=device)
+                self(window, _argmax_out=am)
+                out[:, cur] = am[:, -1]
+                continue
             logits, _ = self(window)
             last = logits[:, -1]
             if sampler is not None:

@@ -289,6 +289,22 @@ DG_API int dg_swiglu(int64_t M, int N, int dtype, const void* x, int64_t x_ld, v
 DG_API int dg_softcap(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
                int64_t out_ld, float cap, void* stream);
 
+/*
+ * lm_head + logit soft cap + greedy argmax in one launch (gpt.py:181-186 and
+ * temperature.py:22-23).  logits[m, v] = cap * tanh((x[m] . w[v]) / cap)
+ * (cap = 0: no cap) for the M normalised rows x (M, C) against the tied
+ * embedding table w (V, C), with the matmul's result rounded to the dtype as
+ * F.linear returns it and the cap computed as dg_softcap does; fp32
+ * accumulation on the matrix cores (its summation order is not hipBLASLt's,
+ * so the logits agree with F.linear + dg_softcap within the north-star bars,
+ * not bit for bit).  With ids != NULL, ids[m] (int64) is the first maximum
+ * of the logits row as stored (torch.argmax).  Supported: C a multiple of
+ * 64, V in {64, 128, 256, 512, 1024}, 16-byte aligned rows; anything else
+ * returns DG_EUNSUPPORTED and does nothing.
+ */
+DG_API int dg_lm_head(int64_t M, int C, int V, int dtype, const void* x, int64_t x_ld, const void* w,
+                      int64_t w_ld, float cap, void* logits, int64_t logits_ld, int64_t* ids, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

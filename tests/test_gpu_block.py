@@ -138,3 +138,85 @@ def test_gpt_forward_uses_one_projection_gemm_and_matches_reference(dev):
         sa.c_g.weight.mul_(2.0)
     assert sa._projection_weight() is not w0
     assert np.array_equal(sa._projection_weight()[192:].cpu().numpy(), sa.c_g.weight.detach().cpu().numpy())
+
+
+LM_HEAD = [  # (rows, C, V)
+    (6400, 64, 256),   # cfg1 decode step
+    (37, 512, 256),    # cfg3 width, ragged rows
+    (5, 1024, 256),    # cfg4 width
+    (48, 64, 1024),    # widest vocabulary taken
+    (16, 128, 64),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("cap", [15.0, 0.0], ids=["softcap", "nocap"])
+@pytest.mark.parametrize("shape", LM_HEAD, ids=lambda s: "x".join(map(str, s)))
+def test_lm_head_matches_linear_softcap_argmax(dev, dtype, cap, shape):
+    """dg_lm_head against F.linear + softcap on the same rows (north-star
+    bars), and its argmax equal to torch.argmax of the logits it stored."""
+    from diff_gpt import _native
+
+    M, C, V = shape
+    x = tr.rms(_randn((M, C), 90 + C, dtype, 2.0))
+    w = _randn((V, C), 91 + V, dtype, 1.0)
+    logits = torch.empty((M, V), dtype=TDT[dtype], device=dev)
+    ids = torch.full((M,), -1, dtype=torch.int64, device=dev)
+    assert _native.lm_head_(x.to(dev), w.to(dev), cap, logits, ids)
+    ref = x.float() @ w.float().t()
+    ref = ref.to(TDT[dtype]).float()
+    if cap > 0:
+        ref = cap * torch.tanh(ref / cap)
+    assert _rel(logits, ref) <= TOL[dtype]
+    assert torch.equal(ids, torch.argmax(logits, dim=-1))
+
+
+def test_lm_head_argmax_first_maximum_wins(dev):
+    """Equal maxima (rows of the table repeated) resolve to the first entry,
+    as torch.argmax does, including across the four waves' quarters."""
+    from diff_gpt import _native
+
+    M, C, V = 32, 64, 256
+    x = _randn((M, C), 5, "f32").to(dev)
+    base = _randn((1, C), 6, "f32")
+    w = _randn((V, C), 7, "f32") * 0.01
+    for e in (3, 64, 130, 250):  # the same best row in several quarters
+        w[e] = base[0]
+    w = w.to(dev)
+    x = base.repeat(M, 1).to(dev)  # every row's maximum is at entries 3, 64, 130, 250
+    logits = torch.empty((M, V), device=dev)
+    ids = torch.empty((M,), dtype=torch.int64, device=dev)
+    assert _native.lm_head_(x, w, 15.0, logits, ids)
+    assert bool((ids == 3).all())
+    assert torch.equal(ids, torch.argmax(logits, dim=-1))
+
+
+@pytest.mark.parametrize("shape", [(8, 48, 256), (8, 64, 300), (8, 64, 192)], ids=lambda s: "x".join(map(str, s)))
+def test_lm_head_unsupported_shapes_do_nothing(dev, shape):
+    from diff_gpt import _native
+
+    M, C, V = shape
+    logits = torch.full((M, V), 7.0, device=dev)
+    assert not _native.lm_head_(torch.ones((M, C), device=dev), torch.ones((V, C), device=dev), 15.0, logits)
+    assert bool((logits == 7.0).all())
+
+
+def test_gpt_greedy_generate_uses_fused_argmax(dev, monkeypatch):
+    """GPT.generate with TemperatureSampler(0) takes the argmax from the
+    lm_head launch; the tokens equal those of the unfused path (F.linear +
+    softcap + torch.argmax), which forcing the fallback gives."""
+    from diff_gpt import _native
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=32, n_head=4, n_layer=2, use_checkpoint=False).to(dev).eval()
+    idx = torch.randint(0, 256, (3, 5), generator=torch.Generator().manual_seed(1)).to(dev)
+    with torch.inference_mode():
+        fused = model.generate(idx, 12, TemperatureSampler(0))
+    real = _native.lm_head_
+    monkeypatch.setattr(_native, "lm_head_", lambda *a, **k: False)
+    with torch.inference_mode():
+        plain = model.generate(idx, 12, TemperatureSampler(0))
+    monkeypatch.setattr(_native, "lm_head_", real)
+    assert torch.equal(fused, plain)
