@@ -426,3 +426,64 @@ def test_copy4d_row_vector_path(dev, dtype):
     ref = torch.full((L2, B, H, cap * D), -1.0, dtype=TDT[dtype])
     ref[..., : T * D] = src[..., : T * D].cpu().expand(L2, B, H, T * D)
     assert torch.equal(big.cpu(), ref)
+
+
+# ------------------------------------------------------------------ seeded random shapes
+
+
+def _random_shapes(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rng.choice([16, 32, 64, 128, 48, 10]))
+        kind = rng.choice(["decode", "prefill", "chunk"])
+        B, H = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        if kind == "decode":
+            Tq, Tk = 1, int(rng.integers(1, 1200))
+        elif kind == "prefill":
+            Tq = Tk = int(rng.integers(2, 400))
+        else:
+            Tk = int(rng.integers(3, 500))
+            Tq = int(rng.integers(2, Tk))
+        out.append((B, H, Tq, Tk, D))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", _random_shapes(2024, 16), ids=lambda s: "x".join(map(str, s)))
+def test_attention_random_shapes(dev, dtype, shape):
+    """dg_attention on seeded random (B, H, Tq, Tk, D): decode, causal prefill
+    and chunked prefill, every kernel family, against fp64 brute force."""
+    B, H, Tq, Tk, D = shape
+    err = _attention_case(dev, dtype, B, H, Tq, Tk, D, cache_layout=(Tq != Tk), seed=B * 131 + Tq + Tk + D)
+    assert err <= TOL[dtype], err
+
+
+def _random_groups(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        G = int(rng.choice([16, 20, 37, 64, 100]))
+        B = int(rng.integers(G, 3 * G + 1))
+        P = int(rng.integers(1, 200))
+        Tk = P + int(rng.integers(0, 60))
+        out.append((B, G, int(rng.integers(1, 5)), P, max(Tk, 1), int(rng.choice([16, 32]))))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", _random_groups(7, 10), ids=lambda s: "x".join(map(str, s)))
+def test_grouped_prefix_random_shapes(dev, dtype, shape):
+    """The two-wave shared-prefix kernel on seeded random groups (ragged
+    groups, prefixes not multiples of 16, zero to 59 own keys) against fp64."""
+    from diff_gpt import _native
+
+    B, G, H, P, Tk, D = shape
+    q, cache = _grouped_case(dtype, shape)
+    cd, qd = cache.to(dev), q.to(dev)
+    keys = cd[0, :, :, :Tk].transpose(1, 2)
+    vals = cd[1, :, :, :Tk].transpose(1, 2)
+    y = _native.ops().attention(qd, keys, vals, 1.0 / np.sqrt(D), P, G)
+    ref = on.attention_f64(q.float().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy())
+    err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= TOL[dtype], err
