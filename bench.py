@@ -279,7 +279,9 @@ def shapes_leg(reps: int = 20):
     prefill T=3584).  The cache is (2, B, H, capacity, D), the layout the
     model's KV cache uses.  Each case is `reps` launches captured in one graph,
     timed with events over 5 replays (median); decode bytes per launch =
-    B*H*es*(2*L_kv*D + 2*D), prefill FLOP = 2*B*H*D*T*(T+1)."""
+    B*H*es*(2*L_kv*D + 2*D), prefill FLOP = 2*B*H*D*T*(T+1).  The D = 16 fp32
+    prefills of configs[0] (B=32) and configs[1] (one series, B=1), T=96,
+    H=4, are launch-bound and report latency only."""
     import torch
 
     from diff_gpt import _native
@@ -332,6 +334,17 @@ def shapes_leg(reps: int = 20):
         tf = 2.0 * B * H * D * T * (T + 1) / t / 1e12
         out.append({"workload": f"{name} causal prefill attention B={B} H={H} T={T} D={D} bf16",
                     "ms": t * 1e3, "tflops": tf, "frac": tf / BF16_PEAK_TFLOPS})
+        log(f"shapes: {out[-1]}")
+        del q, k, v, y
+    # configs[0] and configs[1] prefill (D = 16, fp32): launch-bound, so the
+    # figure is latency per launch, with no roofline
+    for name, B in (("configs[0]", 32), ("configs[1] per series", 1)):
+        H, D, T = 4, 16, 96
+        q, k, v = (torch.randn((B, T, H, D), generator=g, device=dev) for _ in range(3))
+        y = torch.empty_like(q)
+        t = timed(lambda: _native.attention_(q, k, v, y, D ** -0.5))
+        out.append({"workload": f"{name} causal prefill attention B={B} H={H} T={T} D={D} fp32",
+                    "us": t * 1e6, "bound": "latency"})
         log(f"shapes: {out[-1]}")
         del q, k, v, y
     return out
