@@ -194,7 +194,7 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
     }
 
 
-def prefill_leg(reps: int = 10):
+def prefill_leg(reps: int = 10, traffic_json: str | None = None):
     """B=256, T=1024, H=8, D=64 bf16, q/k/v in (B,T,H,D) projection
     layout, RoPE base 1e4 + QK-norm.  The model's step: RoPE + QK-norm of k in
     a first launch, then dg_prefill_rope (causal attention that rotates and
@@ -259,6 +259,10 @@ def prefill_leg(reps: int = 10):
     t_all = sorted(times)[len(times) // 2]
     t_fused = sorted(fused_t)[len(fused_t) // 2]
     tf = flop / t_attn / 1e12
+    # HBM bytes per attention launch, from the committed rocprofv3 counter runs
+    traffic = None
+    if traffic_json and Path(traffic_json).exists():
+        traffic = json.loads(Path(traffic_json).read_text()).get("prefill_cfg2_bf16")
     return {
         "workload": "configs[2] causal prefill B=256 H=8 T=1024 D=64 bf16, RoPE+QK-norm",
         "tflops": tf,
@@ -267,7 +271,7 @@ def prefill_leg(reps: int = 10):
         "tflops_with_rope": flop / t_fused / 1e12,
         "with_rope_unfused_ms": t_all * 1e3,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS, "traffic": traffic},
     }
 
 
@@ -560,7 +564,7 @@ def main():
         "frac": res["achieved_gbs"] / HBM_PEAK_GBS,
         "traffic": traffic,
     }
-    prefill = None if args.no_prefill else prefill_leg()
+    prefill = None if args.no_prefill else prefill_leg(traffic_json=args.traffic_json)
     if prefill:
         log(f"prefill: {prefill}")
     shapes = None if args.no_shapes else shapes_leg()
