@@ -171,6 +171,20 @@ def test_lm_head_matches_linear_softcap_argmax(dev, dtype, cap, shape):
     assert torch.equal(ids, torch.argmax(logits, dim=-1))
 
 
+def _random_lm_heads(seed, n):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 3000)), int(rng.choice([64, 128, 192, 320, 512, 1024])),
+             int(rng.choice([64, 128, 256, 512, 1024]))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", _random_lm_heads(31, 8), ids=lambda s: "x".join(map(str, s)))
+def test_lm_head_random_shapes(dev, dtype, shape):
+    """Seeded random (rows, width, vocabulary) within the kernel's range, with
+    the softcap: logits within the bars, argmax equal to torch.argmax."""
+    test_lm_head_matches_linear_softcap_argmax(dev, dtype, 15.0, shape)
+
+
 def test_lm_head_argmax_first_maximum_wins(dev):
     """Equal maxima (rows of the table repeated) resolve to the first entry,
     as torch.argmax does, including across the four waves' quarters."""

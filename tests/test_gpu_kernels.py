@@ -202,6 +202,27 @@ def test_prefill_rope_equals_rope_then_attention(dev, dtype, fdt, qknorm, shape)
     assert torch.equal(y, y2)
 
 
+def _random_rope_prefills(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rng.choice([64, 128]))
+        B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        Tk = int(rng.integers(16, 700))
+        Tq = Tk if rng.random() < 0.5 else int(rng.integers(16, Tk + 1))
+        out.append((B, H, Tq, Tk, D))
+    return out
+
+
+@pytest.mark.parametrize("qknorm", [True, False])
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("shape", _random_rope_prefills(77, 10), ids=lambda s: "x".join(map(str, s)))
+def test_prefill_rope_random_shapes(dev, dtype, qknorm, shape):
+    """Seeded random causal (Tq = Tk) and chunked (Tq < Tk) shapes: the fused
+    RoPE prefill stays bit-identical to RoPE followed by dg_attention."""
+    test_prefill_rope_equals_rope_then_attention(dev, dtype, "f32", qknorm, shape)
+
+
 @pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 64), "f32"),
                                          ((1, 2, 8, 8, 64), "bf16")])
 def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
