@@ -36,14 +36,36 @@ def _randn(shape, seed, dtype, scale=1.0):
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("D", [8, 16, 64, 128, 256, 12])
 def test_rope_qknorm_append_bit_exact(dev, dtype, D):
+    _rope_append_case(dev, dtype, 3, 5, 4, D, 7, 16)
+
+
+def _random_rope_appends(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rng.choice([8, 12, 16, 32, 48, 64, 128, 256]))
+        B, T, H = int(rng.integers(1, 9)), int(rng.integers(1, 300)), int(rng.integers(1, 9))
+        pos = int(rng.integers(0, 200))
+        out.append((B, T, H, D, pos, pos + T + int(rng.integers(0, 30))))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", _random_rope_appends(99, 10), ids=lambda s: "x".join(map(str, s)))
+def test_rope_qknorm_append_random_shapes(dev, dtype, shape):
+    """Seeded random (B, T, H, D, position, capacity): rotated and normalised
+    q and k bit-exact against the oracle, v copied, the rest untouched."""
+    _rope_append_case(dev, dtype, *shape)
+
+
+def _rope_append_case(dev, dtype, B, T, H, D, pos, cap):
     from diff_gpt import _native
     from diff_gpt.model.rope import precompute_freqs_cis
 
-    B, T, H, pos, cap = 3, 5, 4, 7, 16
     q = _randn((B, T, H, D), 10 + D, dtype, 2.0)
     k = _randn((B, T, H, D), 20 + D, dtype, 2.0)
     v = _randn((B, T, H, D), 30 + D, dtype)
-    table = precompute_freqs_cis(D, 64, 10000).to(TDT[dtype])
+    table = precompute_freqs_cis(D, max(64, cap), 10000).to(TDT[dtype])
     fc = table[pos:pos + T].view(1, T, 1, D // 2, 2)
 
     cache = torch.full((2, 2, B, H, cap, D), 7.0, dtype=TDT[dtype])
