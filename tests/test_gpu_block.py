@@ -51,6 +51,19 @@ def test_attn_res_norm_matches_reference(dev, dtype, shape):
     assert _rel(got, ref) <= TOL[dtype]
 
 
+def _random_res(seed, n):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 7000)), int(rng.choice([16, 32, 48, 64, 96, 128, 256, 512, 1024])),
+             int(rng.integers(2, 13))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", _random_res(17, 8), ids=lambda s: "x".join(map(str, s)))
+def test_attn_res_norm_random_shapes(dev, dtype, shape):
+    """Seeded random (rows, width, sources) through the same check."""
+    test_attn_res_norm_matches_reference(dev, dtype, shape)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_attn_res_norm_one_source_is_rms_norm(dev, dtype):
     from diff_gpt import _native
