@@ -494,6 +494,41 @@ def test_copy4d_row_vector_path(dev, dtype):
     assert torch.equal(big.cpu(), ref)
 
 
+def _random_copies(seed, n):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        shape = tuple(int(x) for x in rng.integers(1, 9, size=3)) + (int(rng.choice([1, 3, 8, 16, 24, 64, 200])),)
+        bcast = tuple(bool(b) for b in rng.random(4) < 0.3)  # broadcast (stride 0) source dims
+        perm = tuple(int(x) for x in rng.permutation(4))    # destination storage order
+        out.append((shape, bcast, perm))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("case", _random_copies(5, 12), ids=lambda c: "x".join(map(str, c[0])) + "-" + "".join(
+    "b" if b else "." for b in c[1]) + "-" + "".join(map(str, c[2])))
+def test_copy4d_random_strides(dev, dtype, case):
+    """Seeded random shapes, broadcast source dims and destination layouts
+    (a permuted storage order, then a slice of a wider buffer): exact, and
+    nothing outside the destination view is written."""
+    from diff_gpt import _native
+
+    shape, bcast, perm = case
+    src_shape = tuple(1 if b else n for n, b in zip(shape, bcast))
+    src = _randn(src_shape, sum(shape) + 7 * sum(bcast), dtype).to(dev).expand(shape)
+    store = [shape[i] for i in perm]
+    store[-1] += 5  # wider rows: the view's last storage dimension is a slice
+    buf = torch.full(store, -3.0, dtype=TDT[dtype], device=dev)
+    view = buf[..., : shape[perm[-1]]]
+    inv = [perm.index(i) for i in range(4)]
+    dst = view.permute(*inv)
+    assert dst.shape == shape
+    _native.ops().copy4d(src, dst)
+    assert torch.equal(dst.cpu(), src.cpu())
+    assert bool((buf[..., shape[perm[-1]]:] == -3.0).all())
+
+
 # ------------------------------------------------------------------ seeded random shapes
 
 
