@@ -19,6 +19,9 @@ from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.model.mha import MultiHeadAttention
 from diff_gpt.model.rms_norm import rms_norm
 
+# dg_attn_res_norm takes at most this many sources of at most this width
+ATTN_RES_MAX_SOURCES = 32
+ATTN_RES_MAX_WIDTH = 2048
 
 def block_attn_res(
     blocks: tuple[torch.Tensor, ...],
@@ -45,6 +48,10 @@ def attn_res_norm(
     (dg_attn_res_norm), with block_attn_res's single-block short cut."""
     if len(blocks) == 1 and partial_block is blocks[0]:
         return rms_norm(partial_block)
+    if len(blocks) + 1 > ATTN_RES_MAX_SOURCES or partial_block.size(-1) > ATTN_RES_MAX_WIDTH:
+        # beyond the fused kernel's limits: the mixture as device torch ops,
+        # then the RMSNorm kernel
+        return rms_norm(block_attn_res(blocks, partial_block, proj))
     return _native.ops().attn_res_norm([*blocks, partial_block], proj.weight)
 
 

@@ -21,24 +21,30 @@ from diff_gpt.sampler.sampler import Sampler
 from diff_gpt.sampler.temperature import TemperatureSampler
 
 
-def _gaussian_soft_ce(
+def _ordinal_target_table(V: int, sigma: float, dtype: torch.dtype, device) -> torch.Tensor:
+    """(V, V) table whose row t is the soft target for token t: a discretised
+    Gaussian over the bin indices centred on t with standard deviation sigma
+    (in bins), normalised to sum to 1."""
+    bins = torch.arange(V, device=device, dtype=torch.float64)
+    z = (bins[None, :] - bins[:, None]) / sigma
+    return torch.softmax(-0.5 * z * z, dim=-1).to(dtype)
+
+
+def _ordinal_soft_ce(
     logits: torch.Tensor,
     targets: torch.Tensor,
     sigma: float,
     ignore_index: int = -100,
 ) -> torch.Tensor:
-    """Cross-entropy against a Gaussian over bin indices, N(target, sigma^2),
-    normalised over the vocabulary; ignore_index rows are skipped
-    (gpt.py:15-35)."""
-    keep = targets != ignore_index
-    if not keep.any():
-        return logits.sum() * 0.0
-    lg = logits[keep]
-    tg = targets[keep].to(lg.dtype)
-    bins = torch.arange(logits.shape[-1], device=logits.device, dtype=lg.dtype)
-    dist2 = (bins[None, :] - tg[:, None]).pow(2)
-    soft = F.softmax(-dist2 / (2.0 * sigma * sigma), dim=-1)
-    return -(soft * F.log_softmax(lg, dim=-1)).sum(dim=-1).mean()
+    """Mean over the rows whose target is not ignore_index of the cross-entropy
+    between the row's log-softmax and its Gaussian soft target (the training
+    loss of gpt.py:15-35 for label_smoothing_sigma > 0); 0 when every row is
+    ignored."""
+    valid = targets != ignore_index
+    soft = _ordinal_target_table(logits.size(-1), sigma, logits.dtype, logits.device)
+    rows = soft[torch.where(valid, targets, 0)]
+    per_row = -(rows * F.log_softmax(logits, dim=-1)).sum(dim=-1)
+    return torch.where(valid, per_row, 0.0).sum() / valid.sum().clamp(min=1)
 
 
 class BaseGPT(nn.Module, ABC):
@@ -198,7 +204,7 @@ class GPT(BaseGPT):
             flat_logits = logits.view(B * T, -1)
             flat_targets = targets.view(B * T)
             if self.label_smoothing_sigma > 0:
-                loss = _gaussian_soft_ce(
+                loss = _ordinal_soft_ce(
                     flat_logits, flat_targets, sigma=self.label_smoothing_sigma
                 )
             else:

@@ -1,8 +1,8 @@
 """Gated multi-head self-attention (src/diff_gpt/model/mha.py:10-86).
 
-The q, k, v and g projections are one GEMM (hipBLASLt) against the four
-weights concatenated (cached while the parameters are unchanged); q, k, v and
-g are column slices of its output, which the kernels read through strides.
+The q, k, v and g projections are one GEMM (hipBLASLt) against one storage
+that the four weight parameters are row views of; q, k, v and g are column
+slices of its output, which the kernels read through strides.
 The sigmoid gate is one dg_gate launch and the output projection a GEMM.
 Everything between the projections and the gate runs in libdgattn:
 
@@ -57,18 +57,58 @@ class MultiHeadAttention(nn.Module):
         self.c_v = nn.Linear(self.n_embd, inner, bias=False)
         self.c_g = nn.Linear(self.n_embd, self.n_embd, bias=False)
         self.c_proj = nn.Linear(self.n_embd, self.n_embd, bias=False)
-        self._qkvg_key = None
-        self._qkvg_weight = None
+        self._qkvg: torch.Tensor | None = None
+        self._tie_projections()
+
+    def _weights4(self) -> tuple[torch.Tensor, ...]:
+        return (self.c_q.weight, self.c_k.weight, self.c_v.weight, self.c_g.weight)
+
+    def _tie_projections(self) -> None:
+        """Place the c_q, c_k, c_v and c_g weights in one (3*inner + C, C)
+        storage, rows in that order, and make each parameter a view of its
+        rows.  The four projections are then one GEMM against that storage,
+        and any update of a parameter -- in place, through .data, or by
+        load_state_dict -- is an update of the storage itself: there is no
+        second copy that could go stale."""
+        ws = self._weights4()
+        fused = torch.cat([w.detach() for w in ws], dim=0)
+        row = 0
+        for w in ws:
+            n = w.size(0)
+            w.data = fused[row : row + n]
+            row += n
+        self._qkvg = fused
+
+    def _is_tied(self) -> bool:
+        fused = self._qkvg
+        if fused is None:
+            return False
+        row_bytes = fused.stride(0) * fused.element_size()
+        row = 0
+        for w in self._weights4():
+            if (
+                w.dtype != fused.dtype
+                or w.device != fused.device
+                or w.stride() != fused.stride()
+                or w.data_ptr() != fused.data_ptr() + row * row_bytes
+            ):
+                return False
+            row += w.size(0)
+        return row == fused.size(0)
+
+    def _apply(self, fn, recurse=True):
+        # .to() / .cuda() / .bfloat16() convert each parameter on its own;
+        # gather the converted weights into one storage again
+        super()._apply(fn, recurse)
+        self._tie_projections()
+        return self
 
     def _projection_weight(self) -> torch.Tensor:
-        """[c_q; c_k; c_v; c_g] weights stacked on the output dim, rebuilt when
-        a parameter is replaced or modified in place."""
-        ws = (self.c_q.weight, self.c_k.weight, self.c_v.weight, self.c_g.weight)
-        key = tuple((w.data_ptr(), w._version, w.dtype) for w in ws)
-        if key != self._qkvg_key:
-            self._qkvg_weight = torch.cat([w.detach() for w in ws], dim=0)
-            self._qkvg_key = key
-        return self._qkvg_weight
+        """The (3*inner + C, C) storage that c_q, c_k, c_v and c_g view; re-tied
+        first if a parameter was replaced by another tensor."""
+        if not self._is_tied():
+            self._tie_projections()
+        return self._qkvg
 
     def forward(
         self,

@@ -167,6 +167,31 @@ def attention_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | No
     return np.einsum("bhij,bjhd->bihd", p, v)
 
 
+def attention_head_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float | None = None,
+                       rows: slice | None = None) -> np.ndarray:
+    """attention_f64 for one (row, head): q (Tq, D), k and v (Tk, D) -> (Tq, D),
+    as float64 matrix products (BLAS), so sequences of a few thousand keys
+    take seconds.  ``rows`` restricts the result to a slice of the queries
+    (their mask rows are those of the full Tq x Tk problem).
+
+    Pinned by: equality with attention_f64 within float64 rounding on causal,
+    chunked and single-query shapes (tests/test_oracle.py)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    Tq, Tk, D = q.shape[0], k.shape[0], q.shape[1]
+    if scale is None:
+        scale = 1.0 / np.sqrt(D)
+    sel = slice(0, Tq) if rows is None else rows
+    s = (q[sel] @ k.T) * scale
+    mask = visible_mask(Tq, Tk)[sel]
+    s = np.where(mask, s, -np.inf)
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ v
+
+
 # ---------------------------------------------------------------------------
 # KV cache bookkeeping  (kv_cache.py:4-116)
 # ---------------------------------------------------------------------------

@@ -143,14 +143,42 @@ def test_gpt_forward_uses_one_projection_gemm_and_matches_reference(dev):
         got, _ = model(idx.to(dev))
         ref = tr.forward(p, cfg, idx)
     assert _rel(got, ref) <= TOL["f32"]
-    # the concatenated projection weight is reused until a parameter changes
+    # the four projection weights are views of the one GEMM operand: an update
+    # through .data (which leaves _version alone) reaches the next forward
     sa = model.blocks[0].sa
     w0 = sa._projection_weight()
     assert sa._projection_weight() is w0
-    with torch.no_grad():
-        sa.c_g.weight.mul_(2.0)
-    assert sa._projection_weight() is not w0
-    assert np.array_equal(sa._projection_weight()[192:].cpu().numpy(), sa.c_g.weight.detach().cpu().numpy())
+    sa.c_g.weight.data.mul_(2.0)
+    sa.c_q.weight.data.copy_(sa.c_q.weight.data * 0.5)
+    assert sa._projection_weight() is w0
+    assert np.array_equal(w0[192:].cpu().numpy(), sa.c_g.weight.detach().cpu().numpy())
+    p["blocks.0.sa.c_g.weight"] *= 2.0
+    p["blocks.0.sa.c_q.weight"] *= 0.5
+    with torch.inference_mode():
+        got, _ = model(idx.to(dev))
+        ref = tr.forward(p, cfg, idx)
+    assert _rel(got, ref) <= TOL["f32"]
+
+
+@pytest.mark.parametrize("n_embd,n_head,n_layer", [(32, 2, 33), (2304, 18, 2)], ids=["deep", "wide"])
+def test_gpt_beyond_attn_res_kernel_limits(dev, n_embd, n_head, n_layer):
+    """33 layers (the last sub-layers mix up to 36 sources) and n_embd 2304
+    exceed dg_attn_res_norm's 32 sources / 2048 columns: the mixture then runs
+    as device torch ops followed by dg_rms_norm, and the forward still matches
+    the oracle."""
+    from diff_gpt.model.gpt import GPT
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=n_embd, block_size=32, n_head=n_head, n_layer=n_layer,
+                use_checkpoint=False).eval()
+    p = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=n_embd, block_size=32, n_head=n_head, n_layer=n_layer)
+    idx = torch.randint(0, 256, (2, 12), generator=torch.Generator().manual_seed(7))
+    model = model.to(dev)
+    with torch.inference_mode():
+        got, _ = model(idx.to(dev))
+        ref = tr.forward(p, cfg, idx)
+    assert _rel(got, ref) <= TOL["f32"]
 
 
 LM_HEAD = [  # (rows, C, V)

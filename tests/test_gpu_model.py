@@ -409,8 +409,10 @@ def _cfg0_model(dev, dtype=torch.float32):
 def test_cfg0_greedy_ids_and_logits_match_oracle(dev):
     """fp32, 32 prompts of 96 ids, 48 greedy KV-cache decode
     steps.  Teacher-forced on the oracle's greedy tokens, every step's logits
-    agree within 1e-4 and the argmax equals the oracle's token wherever the
-    oracle's top-1/top-2 margin exceeds 1e-3 (ties aside, ids are identical)."""
+    agree within 1e-5 * max|ref| (the bar of test_gpt.py:76), and the argmax
+    equals the oracle's token for every row whose top-1/top-2 margin exceeds
+    twice that bar; rows inside it are near-ties, counted and reported (none
+    are expected at these sizes)."""
     from diff_gpt.model.kv_cache import KVCache
 
     model = _cfg0_model(dev)
@@ -420,21 +422,25 @@ def test_cfg0_greedy_ids_and_logits_match_oracle(dev):
     ref_tokens, ref_logits = tr.greedy_decode(params, cfg, prompts, 48)
 
     kv = KVCache(batch_size=32, num_heads=4, seq_len=144, head_dim=16, num_layers=2)
+    worst, near_ties = 0.0, 0
     with torch.no_grad():
         logits, _ = model(prompts.to(dev), kv_cache=kv)
         logits = logits[:, -1]
-        checked = 0
         for s in range(48):
             ref = ref_logits[s]
-            assert_close(logits.cpu(), ref, atol=1e-4, rtol=1e-4)
+            bar = 1e-5 * ref.abs().max().item()
+            err = (logits.cpu() - ref).abs().max().item()
+            worst = max(worst, err / ref.abs().max().item())
+            assert err <= bar, (s, err, bar)
             top2 = ref.topk(2, dim=-1).values
-            clear = (top2[:, 0] - top2[:, 1]) > 1e-3
+            clear = (top2[:, 0] - top2[:, 1]) > 2 * bar
+            near_ties += int((~clear).sum())
             ours = logits.argmax(-1).cpu()
             assert torch.equal(ours[clear], ref_tokens[clear, s])
-            checked += int(clear.sum())
             logits, _ = model(ref_tokens[:, s:s + 1].to(dev), kv_cache=kv)
             logits = logits[:, -1]
-    assert checked > 0.95 * 32 * 48
+    print(f"cfg0: worst logit error {worst:.3g} x max|ref|, near-ties {near_ties} of {32 * 48}")
+    assert near_ties <= 3
     assert kv.get_pos() == 96 + 48
 
 
@@ -462,7 +468,7 @@ def test_bf16_model_logits_close_to_oracle(dev):
     relative to that noise: against the same bf16 weights evaluated in fp32
     (the exact model), the HIP path may deviate at most 1.5x as much as the
     reference's own bf16 CPU evaluation does, and stays within 2e-2 of the
-    logit range."""
+    largest exact logit."""
     from diff_gpt.model.kv_cache import KVCache
 
     model = _cfg0_model(dev, torch.bfloat16)
@@ -482,8 +488,10 @@ def test_bf16_model_logits_close_to_oracle(dev):
             worst_ref = max(worst_ref, (bf_logits[s].float() - exact[s]).abs().max().item())
             logits = model(tokens[:, s:s + 1].to(dev), kv_cache=kv)[0][:, -1]
     span = max(e.abs().max().item() for e in exact)
+    print(f"bf16 cfg0 model: worst |logit err| ours {worst_ours:.4g}, reference bf16 {worst_ref:.4g}, "
+          f"max|exact| {span:.4g}")
     assert worst_ours <= 1.5 * worst_ref + 1e-3, (worst_ours, worst_ref)
-    assert worst_ours <= 2e-2 * 2 * span, (worst_ours, span)
+    assert worst_ours <= 2e-2 * span, (worst_ours, span)
 
 
 # ------------------------------------------------------------------ captured decode step

@@ -120,3 +120,77 @@ def test_gpt_constructor_assertions():
     GPT(vocab_size=70, n_embd=16, block_size=8, n_layer=1, n_head=2, pad_vocab_size_to=1)
     with pytest.raises(AssertionError, match="label_smoothing_sigma"):
         GPT(vocab_size=64, n_embd=16, n_layer=1, n_head=2, label_smoothing_sigma=-0.1)
+
+
+def test_projection_weights_are_views_of_one_storage():
+    """c_q, c_k, c_v and c_g view one (3*inner + C, C) storage, so no copy of
+    them can go stale: updates through .data, in-place ops and load_state_dict
+    all land in the GEMM operand, and dtype conversion or a replaced parameter
+    re-ties the views."""
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(0)
+    sa = MultiHeadAttention(n_embd=32, n_head=4, layer_idx=0)
+    ws = [sa.c_q.weight, sa.c_k.weight, sa.c_v.weight, sa.c_g.weight]
+    fused = sa._projection_weight()
+    assert fused.shape == (4 * 32, 32)
+    assert all(w.untyped_storage().data_ptr() == fused.untyped_storage().data_ptr() for w in ws)
+    assert torch.equal(fused, torch.cat([w.detach() for w in ws]))
+
+    sa.c_k.weight.data.mul_(3.0)  # .data: no _version bump
+    with torch.no_grad():
+        sa.c_v.weight.add_(1.0)
+    assert sa._projection_weight() is fused
+    assert torch.equal(fused[32:64], sa.c_k.weight.detach())
+    assert torch.equal(fused[64:96], sa.c_v.weight.detach())
+
+    sd = {k: torch.randn_like(v) for k, v in sa.state_dict().items()}
+    sa.load_state_dict(sd)
+    assert sa._projection_weight() is fused
+    assert torch.equal(fused[96:], sd["c_g.weight"]) and torch.equal(fused[:32], sd["c_q.weight"])
+
+    sa = sa.to(torch.bfloat16)
+    fused16 = sa._projection_weight()
+    assert fused16.dtype == torch.bfloat16
+    assert torch.equal(fused16[96:], sd["c_g.weight"].to(torch.bfloat16))
+    assert sa.c_q.weight.data_ptr() == fused16.data_ptr()
+
+    new_q = torch.nn.Parameter(torch.ones(32, 32, dtype=torch.bfloat16))
+    sa.c_q.weight = new_q
+    fused_new = sa._projection_weight()
+    assert fused_new is not fused16 and bool((fused_new[:32] == 1).all())
+    assert sa.c_q.weight.data_ptr() == fused_new.data_ptr()
+    assert list(sa.state_dict()) == ["c_q.weight", "c_k.weight", "c_v.weight", "c_g.weight", "c_proj.weight"]
+
+
+def test_ordinal_soft_ce_against_float64_loop():
+    """The label_smoothing_sigma > 0 loss (gpt.py:15-35): for each kept row,
+    -sum_i w_i log softmax(l)_i with w_i proportional to exp(-(i - y)^2 /
+    (2 sigma^2)); rows with ignore_index are left out of the mean.  Checked
+    against a float64 loop over rows; sigma -> 0 gives the plain
+    cross-entropy."""
+    import math
+
+    from diff_gpt.model.gpt import _ordinal_soft_ce
+
+    g = torch.Generator().manual_seed(0)
+    logits = torch.randn(40, 64, generator=g, dtype=torch.float64) * 3
+    targets = torch.randint(0, 64, (40,), generator=g)
+    targets[::7] = -100
+    for sigma in (0.5, 2.0, 10.0):
+        total, n = 0.0, 0
+        for row, y in zip(logits.tolist(), targets.tolist()):
+            if y == -100:
+                continue
+            m = max(row)
+            lse = m + math.log(sum(math.exp(v - m) for v in row))
+            w = [math.exp(-((i - y) ** 2) / (2 * sigma * sigma)) for i in range(64)]
+            sw = sum(w)
+            total += -sum(wi / sw * (v - lse) for wi, v in zip(w, row))
+            n += 1
+        got = _ordinal_soft_ce(logits, targets, sigma).item()
+        assert abs(got - total / n) <= 1e-12 * max(1.0, abs(total / n))
+    keep = targets != -100
+    plain = torch.nn.functional.cross_entropy(logits[keep], targets[keep]).item()
+    assert abs(_ordinal_soft_ce(logits, targets, 1e-3).item() - plain) <= 1e-9
+    assert _ordinal_soft_ce(logits, torch.full((40,), -100), 1.0).item() == 0.0

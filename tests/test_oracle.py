@@ -186,6 +186,19 @@ def test_attention_f64_closed_forms():
     assert np.allclose(on.attention_f64(q2, k2, v2)[0, 0], v2[0, 0])
 
 
+@pytest.mark.parametrize("Tq,Tk", [(40, 40), (1, 37), (13, 50)])
+def test_attention_head_f64_equals_brute_force(Tq, Tk):
+    """The per-head matrix-product form against attention_f64 (causal, decode
+    and chunked masks), whole and restricted to a slice of the queries."""
+    rng = np.random.default_rng(Tq + 7 * Tk)
+    D = 16
+    q, k, v = rng.standard_normal((Tq, D)), rng.standard_normal((Tk, D)), rng.standard_normal((Tk, D))
+    ref = on.attention_f64(q[None, :, None], k[None, :, None], v[None, :, None])[0, :, 0]
+    assert np.abs(on.attention_head_f64(q, k, v) - ref).max() < 1e-12
+    sl = slice(Tq // 2, Tq)
+    assert np.abs(on.attention_head_f64(q, k, v, rows=sl) - ref[sl]).max() < 1e-12
+
+
 # ---------------------------------------------------------------- KV cache model
 
 
