@@ -101,6 +101,15 @@ _SIGNATURES = {
         + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.c_int, ctypes.c_int,
            ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
+    "dg_decode_step_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "dg_decode_step_noalloc": (
+        ctypes.c_int,
+        [ctypes.c_int] * 4
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 5  # q, k, v, k_cache, v_cache
+        + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.c_int, ctypes.c_int,
+           ctypes.c_int, ctypes.c_void_p],
+    ),
     "dg_rms_norm": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
@@ -445,13 +454,16 @@ def decode_step_(
     prefix_len: int = 0,
     group: int = 1,
     qknorm: bool = True,
+    noalloc: bool = False,
 ) -> None:
     """dg_decode_step: RoPE + QK-norm of the step's q, k (B,1,H,D), the K/V
     append at position p of the (B,Tcap,H,D) cache views (at position 0), and
     the decode attention over positions 0 .. p into y (B,1,H,D).  pos is p as a
     Python int, with freqs the (D/2, 2) (cos, sin) row of position p; or a
     one-element int32 device tensor holding p, with freqs the whole contiguous
-    (Tmax, D/2, 2) table."""
+    (Tmax, D/2, 2) table.  noalloc=True calls dg_decode_step_noalloc, whose
+    key-split partials live in the library's static device scratch instead of
+    a workspace allocated here."""
     B, T, H, D = q.shape
     if T != 1 or k.shape != q.shape or v.shape != q.shape or y.shape != q.shape:
         raise ValueError("decode_step: q, k, v, y must be (B, 1, H, D)")
@@ -471,17 +483,19 @@ def decode_step_(
         fstride, pos_host, pos_ptr = 0, int(pos), None
     code = _dtype_code(q)
     L = lib()
-    ws_bytes = L.dg_decode_step_workspace_size(B, H, max_pos, D, code)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
-    rc = L.dg_decode_step(
+    args = (
         B, H, D, code, _ptr(q), st(q), _ptr(k), st(k), _ptr(v), st(v),
         _ptr(k_cache), st(k_cache), _ptr(v_cache), st(v_cache),
         _ptr(freqs), fstride, _dtype_code(freqs), pos_host, pos_ptr, max_pos,
         _ptr(y), st(y), float(scale), int(prefix_len), int(group), DG_QKNORM if qknorm else 0,
-        _ptr(ws), ws_bytes, _stream(q),
     )
-    _check(rc, "decode_step")
+    if noalloc:
+        _check(L.dg_decode_step_noalloc(*args, _stream(q)), "decode_step_noalloc")
+        return
+    ws_bytes = L.dg_decode_step_workspace_size(B, H, max_pos, D, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
+    _check(L.dg_decode_step(*args, _ptr(ws), ws_bytes, _stream(q)), "decode_step")
 
 
 def rms_norm_(x: torch.Tensor, out: torch.Tensor) -> None:

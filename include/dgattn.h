@@ -236,6 +236,33 @@ DG_API int dg_decode_step(int B, int H, int D, int dtype,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * dg_decode_step without a workspace argument: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture that must not allocate, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * dg_decode_step; the key-split partials live in a static device array of
+ * dg_decode_step_noalloc_scratch_bytes() bytes (16 MiB) that the library
+ * holds on every GPU it runs on until the process ends.  Sizes whose split
+ * workspace (dg_decode_step_workspace_size) exceeds it return DG_EWORKSPACE
+ * before any GPU work; head_dim <= 128 always fits.  It allocates nothing
+ * and frees nothing.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (other streams, other host threads) race and must be
+ * serialised by the caller.  The stream must belong to the current device.
+ */
+DG_API size_t dg_decode_step_noalloc_scratch_bytes(void);
+
+DG_API int dg_decode_step_noalloc(int B, int H, int D, int dtype,
+                                  const void* q, const dg_stride3* q_st,
+                                  const void* k, const dg_stride3* k_st,
+                                  const void* v, const dg_stride3* v_st,
+                                  void* k_cache, const dg_stride3* kc_st,
+                                  void* v_cache, const dg_stride3* vc_st,
+                                  const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
+                                  int pos, const int32_t* pos_dev, int max_pos,
+                                  void* y, const dg_stride3* y_st, float scale,
+                                  int prefix_len, int group, int flags, void* stream);
+
+/*
  * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with
  * eps=None, i.e. FLT_EPSILON, computed in fp32 and rounded once to dtype).
  * x and out are M rows of N elements with row strides x_ld / out_ld.

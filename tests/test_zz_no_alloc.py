@@ -1,0 +1,95 @@
+"""dg_decode_step_noalloc (the decode step whose key-split partials live in
+the library's static device scratch) against dg_decode_step with a
+caller-allocated workspace, through the C-ABI.
+
+Both run the same kernels with the same number of key splits, so the cache
+writes and the attention output are compared bit for bit.  Two calls in a
+row, the second smaller than the first (the scratch keeps the first call's
+partials, which the second must not see), then the device-position form and
+a shared-prefix step, and the rejection of a size whose split workspace
+exceeds the scratch (checked on the host, before any GPU work)."""
+
+import ctypes
+
+import pytest
+import torch
+
+from oracle import numerics as on  # noqa: F401  (tests share the oracle import path)
+
+CASES = [  # (B, H, D, dtype, max_pos, pos, group, prefix_len)
+    (4, 8, 128, torch.bfloat16, 3200, 3000, 1, 0),  # configs[4]-like rows: 25 key splits
+    (2, 4, 64, torch.float32, 1500, 1300, 1, 0),    # smaller second call: 11 splits
+]
+
+
+def _inputs(dev, B, H, D, dtype, max_pos, seed):
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q, k, v = (torch.randn((B, 1, H, D), generator=g, device=dev).to(dtype) for _ in range(3))
+    cache = torch.randn((2, B, H, max_pos, D), generator=g, device=dev).to(dtype)
+    table = precompute_freqs_cis(D, max_pos, 10000).to(dev).to(dtype)
+    return q, k, v, cache, table
+
+
+def _step(dev, case, seed, noalloc, device_pos=False):
+    from diff_gpt import _native
+
+    B, H, D, dtype, max_pos, pos, group, prefix = case
+    q, k, v, cache, table = _inputs(dev, B, H, D, dtype, max_pos, seed)
+    y = torch.empty_like(q)
+    kc, vc = cache[0].transpose(1, 2), cache[1].transpose(1, 2)
+    if device_pos:
+        p, freqs = torch.tensor([pos], dtype=torch.int32, device=dev), table
+    else:
+        p, freqs = pos, table[pos]
+    _native.decode_step_(q, k, v, freqs, kc, vc, y, D ** -0.5, p, prefix, group, noalloc=noalloc)
+    torch.cuda.synchronize()
+    return y, cache
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_step_equals_workspace_form(dev):
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    for case in CASES:
+        B, H, D, dtype, max_pos, _, _, _ = case
+        code = {torch.float32: 0, torch.bfloat16: 1}[dtype]
+        need = lib.dg_decode_step_workspace_size(B, H, max_pos, D, code)
+        assert 0 < need <= lib.dg_decode_step_noalloc_scratch_bytes()  # the scratch is used
+    for i, case in enumerate(CASES):  # large call, then a smaller one
+        print(f"noalloc case {i}: {case}", flush=True)
+        y1, c1 = _step(dev, case, 10 + i, noalloc=True)
+        y0, c0 = _step(dev, case, 10 + i, noalloc=False)
+        assert torch.equal(c1, c0), i
+        assert torch.equal(y1, y0), i
+    # device-position form (graph-replayable), after the two calls above
+    y1, c1 = _step(dev, CASES[0], 20, noalloc=True, device_pos=True)
+    y0, c0 = _step(dev, CASES[0], 20, noalloc=False, device_pos=True)
+    assert torch.equal(c1, c0) and torch.equal(y1, y0)
+    # shared-prefix step (one fused launch, no scratch involved)
+    shared = (32, 4, 16, torch.float32, 144, 120, 32, 96)
+    y1, c1 = _step(dev, shared, 30, noalloc=True)
+    y0, c0 = _step(dev, shared, 30, noalloc=False)
+    assert torch.equal(c1, c0) and torch.equal(y1, y0)
+
+
+def test_noalloc_rejects_sizes_beyond_the_scratch():
+    """B*H = 8191 rows of head_dim 256 would split the keys in two: 16382
+    partials of 258 floats, more than the 16 MiB scratch.  The call returns
+    DG_EWORKSPACE with a message before it touches the device (so this runs
+    without a GPU); dg_decode_step would take that size with a workspace."""
+    from diff_gpt import _native
+    from diff_gpt._native import Stride3
+
+    lib = _native.lib()
+    cap = lib.dg_decode_step_noalloc_scratch_bytes()
+    assert cap == 16 << 20
+    need = lib.dg_decode_step_workspace_size(8191, 1, 300, 256, 1)
+    assert need > cap
+    fake, nul = ctypes.c_void_p(0x1000), ctypes.c_void_p(0)
+    s3 = lambda: ctypes.pointer(Stride3(0, 0, 0))  # noqa: E731
+    rc = lib.dg_decode_step_noalloc(8191, 1, 256, 1, fake, s3(), fake, s3(), fake, s3(), fake, s3(), fake, s3(),
+                                    fake, 0, 1, 10, nul, 300, fake, s3(), 0.0625, 0, 1, 1, nul)
+    assert rc == -4 and b"scratch" in lib.dg_last_error()
