@@ -68,8 +68,8 @@ bool mfma_prefill_rope_applicable(int B, int H, int Tq, int Tk, int D, int dtype
                                   const dg_stride3* v_st, const void* y, const dg_stride3* y_st,
                                   float scale);
 int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
-                      const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, const void* k,
-                      const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+                      const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, int keys_normed,
+                      const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
                       const dg_stride3* y_st, float scale, hipStream_t s);
 
 // ---------------------------------------------------------------------------
@@ -176,7 +176,9 @@ extern "C" int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, c
   DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == DG_BF16 || freqs_dtype == DG_F16, DG_EUNSUPPORTED,
              "prefill_rope: freqs dtype %d unsupported", freqs_dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "prefill_rope: head_dim must be even (got %d)", D);
-  DG_REQUIRE((flags & ~DG_QKNORM) == 0, DG_EINVAL, "prefill_rope: unknown flags 0x%x", flags);
+  DG_REQUIRE((flags & ~(DG_QKNORM | DG_KEYS_NORMED)) == 0, DG_EINVAL, "prefill_rope: unknown flags 0x%x", flags);
+  DG_REQUIRE(!(flags & DG_KEYS_NORMED) || (flags & DG_QKNORM), DG_EINVAL,
+             "prefill_rope: DG_KEYS_NORMED needs DG_QKNORM (bounded scores need both rows normalised)");
   if ((int64_t)B * H * Tq == 0) return DG_OK;
   DG_REQUIRE(Tk >= Tq, DG_EINVAL, "prefill_rope: Tk (%d) < Tq (%d)", Tk, Tq);
   DG_REQUIRE(q && freqs && k && v && y && q_st && f_st && k_st && v_st && y_st, DG_EINVAL,
@@ -186,8 +188,9 @@ extern "C" int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, c
              DG_EUNSUPPORTED,
              "prefill_rope: not taken by the fused kernel (bf16/fp16, head_dim 64 or 128, Tq >= 16, "
              "16-byte aligned rows); use dg_rope_qknorm_append + dg_attention");
-  return mfma_prefill_rope(B, H, Tq, Tk, D, dtype, q, q_st, freqs, f_st, freqs_dtype, flags & DG_QKNORM, k, k_st,
-                           v, v_st, y, y_st, scale, static_cast<hipStream_t>(stream));
+  return mfma_prefill_rope(B, H, Tq, Tk, D, dtype, q, q_st, freqs, f_st, freqs_dtype, (flags & DG_QKNORM) != 0,
+                           (flags & DG_KEYS_NORMED) != 0, k, k_st, v, v_st, y, y_st, scale,
+                           static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t dg_decode_attention_at_workspace_size(int B, int H, int max_keys, int D, int dtype) {

@@ -135,6 +135,12 @@ struct MfmaOps<f16_t> {
 #ifndef DG_PREFILL_BN_D128
 #define DG_PREFILL_BN_D128 32
 #endif
+#ifndef DG_PREFILL_WGS_BND_D64
+#define DG_PREFILL_WGS_BND_D64 4
+#endif
+#ifndef DG_PREFILL_WGS_BND_D128
+#define DG_PREFILL_WGS_BND_D128 3
+#endif
 #ifndef DG_PREFILL_WGS_D128
 #define DG_PREFILL_WGS_D128 3
 #endif
@@ -151,6 +157,34 @@ constexpr int prefill_bn() {
 #endif
 constexpr int kPrefillWindow = DG_PREFILL_WINDOW;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
+// Schedule of the bounded form's 32-key blocks, per head_dim (measured at
+// configs[2] / [4]: D = 64 gains 3-4 % from the prefetch, while the
+// prefetched V^T fragments do not fit D = 128's register budget and halve
+// its rate; the in-wave overlap is neutral at D = 64 and kept at D = 128):
+//   pipe     -- the S products of block mb + 1 are issued before the softmax
+//               of block mb (two S blocks live)
+//   prefetch -- a block's K fragments are all read before its S products and
+//               its V^T fragments before its softmax (one LDS wait each)
+#ifndef DG_PREFILL_BND_PIPE_D64
+#define DG_PREFILL_BND_PIPE_D64 0
+#endif
+#ifndef DG_PREFILL_BND_PREFETCH_D64
+#define DG_PREFILL_BND_PREFETCH_D64 1
+#endif
+#ifndef DG_PREFILL_BND_PIPE_D128
+#define DG_PREFILL_BND_PIPE_D128 1
+#endif
+#ifndef DG_PREFILL_BND_PREFETCH_D128
+#define DG_PREFILL_BND_PREFETCH_D128 0
+#endif
+template <int D>
+constexpr bool prefill_pipe() {
+  return D == 64 ? DG_PREFILL_BND_PIPE_D64 != 0 : DG_PREFILL_BND_PIPE_D128 != 0;
+}
+template <int D>
+constexpr bool prefill_prefetch() {
+  return D == 64 ? DG_PREFILL_BND_PREFETCH_D64 != 0 : DG_PREFILL_BND_PREFETCH_D128 != 0;
+}
 
 // max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
 // value in both operands leaves every lane holding its own value in one
@@ -211,18 +245,21 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
 // Resident workgroups per CU the register allocation must allow: D = 64 fits
 // 4 (<= 128 VGPRs -> 4 waves per SIMD to overlap one wave's MFMAs with
 // another's softmax); D = 128 with 32-key tiles 3 (<= 168 VGPRs).
-template <int D>
+template <int D, bool BND>
 constexpr int prefill_wgs_per_cu() {
+  if constexpr (BND) return D == 64 ? DG_PREFILL_WGS_BND_D64 : DG_PREFILL_WGS_BND_D128;
   return D == 64 ? DG_PREFILL_WGS_D64 : DG_PREFILL_WGS_D128;
 }
 
-template <typename T, int D, int QW, bool ROPE, typename FT>
-__global__ __launch_bounds__(256, prefill_wgs_per_cu<D>())
+template <typename T, int D, int QW, bool ROPE, typename FT, bool BND>
+__global__ __launch_bounds__(256, (prefill_wgs_per_cu<D, BND>()))
 void prefill_mfma_kernel(const PrefillArgs a) {
   using Ops = MfmaOps<T>;
   using vec8 = typename Ops::vec8;
   using C = PrefillCfg<T, D, QW>;
   constexpr int NC = C::NC, NB = C::NB, PPR = C::PPR, BN = C::BN, MB = C::MB, PC = C::PC;
+  constexpr bool kPrefillPipe = prefill_pipe<D>();
+  constexpr bool kPrefillPrefetch = prefill_prefetch<D>();
 
   // two ring stages, K and V each in an array of its own: the compiler can
   // then tell the stage being copied into from the one being read
@@ -334,6 +371,14 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[qb][c][i] = x[qb][c][i] * r;
       }
+      if constexpr (BND) {
+        // bounded form: the operand is the normalised row times scale*log2(e),
+        // rounded once, so the scores come out of the MFMA in log2 units
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) x[qb][c][i] = x[qb][c][i] * a.scale_log2;
+      }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         uint32_t w[4];
@@ -392,98 +437,215 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     }
   }
 
-  auto compute_tile = [&](const uint16_t* Ks, const uint16_t* Vs, int kt0) __attribute__((always_inline)) {
-    // S^T = K . Q^T for the two 32-key halves of the tile
-    floatx16_t s[QW][MB];
+  // Bounded form (BND): q and k rows are RMS-normalised and the scale is
+  // folded into q, so every score s is a log2-unit logit with
+  // |s| <= log2(e) * sqrt(D) * (1 + 2^-7) (11.7 at D = 64, 16.5 at D = 128)
+  // and p = exp2(s) can neither overflow nor underflow: no running maximum,
+  // no rescale.  Without a tile-wide maximum each 32-key block goes from S to
+  // P to the PV products on its own, and the S products of block mb + 1 are
+  // issued before the exponentials of block mb, so one wave's MFMAs overlap
+  // its own softmax.
+  auto s_block = [&](const uint16_t* Ks, int mb, floatx16_t (&s)[QW]) __attribute__((always_inline)) {
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+      for (int r = 0; r < 16; ++r) s[qb][r] = 0.f;
+    if constexpr (kPrefillPrefetch) {
+      // all NC fragments of the block in flight before the first product
+      vec8 kf[NC];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
+      for (int c = 0; c < NC; ++c)
+        kf[c] = __builtin_bit_cast(vec8, *reinterpret_cast<const uint4*>(
+                                             &Ks[(32 * mb + r32) * D + 8 * ((2 * c + hh) ^ kswz)]));
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int qb = 0; qb < QW; ++qb) s[qb] = Ops::mma(kf[c], qf[qb][c], s[qb]);
+    } else {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const uint4 raw =
-            *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * D + 8 * ((2 * c + hh) ^ kswz)]);
+        const uint4 raw = *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * D + 8 * ((2 * c + hh) ^ kswz)]);
         const vec8 kf = __builtin_bit_cast(vec8, raw);
 #pragma unroll
-        for (int qb = 0; qb < QW; ++qb) s[qb][mb] = Ops::mma(kf, qf[qb][c], s[qb][mb]);
+        for (int qb = 0; qb < QW; ++qb) s[qb] = Ops::mma(kf, qf[qb][c], s[qb]);
       }
     }
-
-    // mask (only on tiles that cross the diagonal or the end of the keys)
-    const bool needs_mask = (kt0 + BN - 1 > qw + qoff) || (kt0 + BN > a.Tk);
-    if (needs_mask) {
+  };
+  auto compute_tile_bounded = [&](const uint16_t* Ks, const uint16_t* Vs, int kt0) __attribute__((always_inline)) {
+    floatx16_t sbuf[2][QW];
+    if constexpr (kPrefillPipe) s_block(Ks, 0, sbuf[0]);
 #pragma unroll
-      for (int qb = 0; qb < QW; ++qb) {
-        const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
-            if (rel > lim) s[qb][mb][r] = kNegInf;
-          }
+    for (int mb = 0; mb < MB; ++mb) {
+      if constexpr (!kPrefillPipe) {
+        if (kt0 + 32 * mb > wave_last_key) break;
+        s_block(Ks, mb, sbuf[mb & 1]);
       }
-    }
-
-    vec8 pf[QW][PC];
-#pragma unroll
-    for (int qb = 0; qb < QW; ++qb) {
-      // tile max of the raw scores (scale > 0, so it commutes with the max)
-      float mt = s[qb][0][0];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
-      mt = half_pair_max(mt);
-      // raise the exponent offset only when some row of the wave would
-      // otherwise produce probabilities above 2^kLazyLog2
-      const float mnew = fmaxf(m[qb], mt);
-      if (__builtin_amdgcn_ballot_w64(mnew > m[qb] + a.lazy_raw) != 0) {
-        // m == -inf only before the first tile; key 0 is visible to every
-        // query, so mnew is finite from then on
-        const float alpha = (m[qb] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m[qb] - mnew) * a.scale_log2);
-        m[qb] = mnew;
-        l[qb] *= alpha;
+      floatx16_t(&s)[QW] = sbuf[mb & 1];
+      // the next block holds a key visible to some query of the wave
+      const bool more = mb + 1 < MB && kt0 + 32 * (mb + 1) <= wave_last_key;
+      if constexpr (kPrefillPipe) {
+        if (more) s_block(Ks, mb + 1, sbuf[(mb + 1) & 1]);
+      }
+      // V^T fragments of the block's PV products, read before the softmax so
+      // that their LDS latency passes under the exponentials
+      vec8 vfr[kPrefillPrefetch ? NB : 1][2];
+      if constexpr (kPrefillPrefetch) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) o[qb][nb][r] *= alpha;
+          for (int c2 = 0; c2 < 2; ++c2) {
+            const int c = 2 * mb + c2;
+            const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
+            const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
+            vfr[nb][c2] = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          }
       }
-      const float moff = m[qb] * a.scale_log2;
-      float ls = l[qb];
+      const int kb0 = kt0 + 32 * mb;
+      if (kb0 + 31 > qw + qoff || kb0 + 32 > a.Tk) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+        for (int qb = 0; qb < QW; ++qb) {
+          const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kb0 - 4 * hh;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = kNegInf;
+        }
+      }
+      vec8 pf[QW][2];
+#pragma unroll
+      for (int qb = 0; qb < QW; ++qb) {
+        float ls = l[qb];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           uint32_t w[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i], a.scale_log2, -moff));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i + 1], a.scale_log2, -moff));
-            w[i] = Ops::pack2(p0, p1);
+            w[i] = Ops::pack2(__builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i]),
+                              __builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i + 1]));
             ls = Ops::add_pair(w[i], ls);
           }
-          pf[qb][2 * mb + c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+          pf[qb][c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+        l[qb] = ls;
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          vec8 vf;
+          if constexpr (kPrefillPrefetch) {
+            vf = vfr[nb][c2];
+          } else {
+            const int c = 2 * mb + c2;
+            const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
+            const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
+            vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          }
+#pragma unroll
+          for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c2], o[qb][nb]);
         }
       }
-      l[qb] = ls;
+      if constexpr (kPrefillPipe) {
+        if (!more) break;
+      }
     }
+  };
 
-    // O^T += V^T . P^T; the V^T operand comes straight from the row-major V
-    // tile through the transposing LDS read (4 keys x 16 dims per 16 lanes)
+  auto compute_tile = [&](const uint16_t* Ks, const uint16_t* Vs, int kt0) __attribute__((always_inline)) {
+    if constexpr (BND) {
+      compute_tile_bounded(Ks, Vs, kt0);
+    } else {
+      // S^T = K . Q^T for the two 32-key halves of the tile
+      floatx16_t s[QW][MB];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+      for (int qb = 0; qb < QW; ++qb)
 #pragma unroll
-      for (int c = 0; c < PC; ++c) {
-        const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
-        const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
-        const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c], o[qb][nb]);
+          for (int r = 0; r < 16; ++r) s[qb][mb][r] = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const uint4 raw =
+              *reinterpret_cast<const uint4*>(&Ks[(32 * mb + r32) * D + 8 * ((2 * c + hh) ^ kswz)]);
+          const vec8 kf = __builtin_bit_cast(vec8, raw);
+#pragma unroll
+          for (int qb = 0; qb < QW; ++qb) s[qb][mb] = Ops::mma(kf, qf[qb][c], s[qb][mb]);
+        }
+      }
+
+      // mask (only on tiles that cross the diagonal or the end of the keys)
+      const bool needs_mask = (kt0 + BN - 1 > qw + qoff) || (kt0 + BN > a.Tk);
+      if (needs_mask) {
+#pragma unroll
+        for (int qb = 0; qb < QW; ++qb) {
+          const int lim = min(qw + 32 * qb + r32 + qoff, a.Tk - 1) - kt0 - 4 * hh;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int rel = 32 * mb + 8 * (r >> 2) + (r & 3);  // key - kt0 - 4hh
+              if (rel > lim) s[qb][mb][r] = kNegInf;
+            }
+        }
+      }
+
+      vec8 pf[QW][PC];
+#pragma unroll
+      for (int qb = 0; qb < QW; ++qb) {
+        // tile max of the raw scores (scale > 0, so it commutes with the max)
+        float mt = s[qb][0][0];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int r = (mb == 0 ? 1 : 0); r < 16; ++r) mt = fmaxf(mt, s[qb][mb][r]);
+        mt = half_pair_max(mt);
+        // raise the exponent offset only when some row of the wave would
+        // otherwise produce probabilities above 2^kLazyLog2
+        const float mnew = fmaxf(m[qb], mt);
+        if (__builtin_amdgcn_ballot_w64(mnew > m[qb] + a.lazy_raw) != 0) {
+          // m == -inf only before the first tile; key 0 is visible to every
+          // query, so mnew is finite from then on
+          const float alpha = (m[qb] == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m[qb] - mnew) * a.scale_log2);
+          m[qb] = mnew;
+          l[qb] *= alpha;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[qb][nb][r] *= alpha;
+        }
+        const float moff = m[qb] * a.scale_log2;
+        float ls = l[qb];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            uint32_t w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i], a.scale_log2, -moff));
+              const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][mb][8 * c2 + 2 * i + 1], a.scale_log2, -moff));
+              w[i] = Ops::pack2(p0, p1);
+              ls = Ops::add_pair(w[i], ls);
+            }
+            pf[qb][2 * mb + c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+          }
+        }
+        l[qb] = ls;
+      }
+
+      // O^T += V^T . P^T; the V^T operand comes straight from the row-major V
+      // tile through the transposing LDS read (4 keys x 16 dims per 16 lanes)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int c = 0; c < PC; ++c) {
+          const uint2 lo = lds_read_tr16(Vs + 16 * c * D + voff[0][nb]);
+          const uint2 hi = lds_read_tr16(Vs + 16 * c * D + voff[1][nb]);
+          const vec8 vf = __builtin_bit_cast(vec8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+          for (int qb = 0; qb < QW; ++qb) o[qb][nb] = Ops::mma(vf, pf[qb][c], o[qb][nb]);
+        }
       }
     }
   };
@@ -534,7 +696,7 @@ constexpr int qw_for() {
   return D == 64 ? DG_PREFILL_QW_D64 : DG_PREFILL_QW_D128;
 }
 
-template <typename T, int D, bool ROPE = false, typename FT = T>
+template <typename T, int D, bool ROPE = false, typename FT = T, bool BND = false>
 int launch_prefill(PrefillArgs a, hipStream_t s) {
   constexpr int QW = qw_for<D>();
   constexpr int BM = PrefillCfg<T, D, QW>::BM;
@@ -542,7 +704,7 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
   const int64_t nwg = (int64_t)(a.nwg) * a.nqb;  // a.nwg holds B*H on entry
   DG_REQUIRE(nwg <= 0x7fffffffLL, DG_EINVAL, "prefill: too many workgroups");
   a.nwg = (int)nwg;
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW, ROPE, FT>), dim3((unsigned)a.nwg),
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW, ROPE, FT, BND>), dim3((unsigned)a.nwg),
                      dim3(PrefillCfg<T, D, QW>::NT), 0, s, a);
   return check_launch("prefill_mfma_kernel");
 }
@@ -614,21 +776,30 @@ bool mfma_prefill_rope_applicable(int B, int H, int Tq, int Tk, int D, int dtype
   return true;
 }
 
+namespace {
+template <typename T, bool BND>
+int launch_rope_prefill(int D, bool f32, const PrefillArgs& a, hipStream_t s) {
+  if (D == 64) return f32 ? launch_prefill<T, 64, true, float, BND>(a, s) : launch_prefill<T, 64, true, T, BND>(a, s);
+  return f32 ? launch_prefill<T, 128, true, float, BND>(a, s) : launch_prefill<T, 128, true, T, BND>(a, s);
+}
+}  // namespace
+
 int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
-                      const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, const void* k,
-                      const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+                      const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, int keys_normed,
+                      const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
                       const dg_stride3* y_st, float scale, hipStream_t s) {
   PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
   a.freqs = freqs;
   a.fb = f_st->b; a.ft = f_st->t; a.fh = f_st->h;
   a.qknorm = qknorm;
   const bool f32 = fdtype == DG_F32;
-  if (dtype == DG_BF16) {
-    if (D == 64) return f32 ? launch_prefill<bf16_t, 64, true, float>(a, s) : launch_prefill<bf16_t, 64, true, bf16_t>(a, s);
-    return f32 ? launch_prefill<bf16_t, 128, true, float>(a, s) : launch_prefill<bf16_t, 128, true, bf16_t>(a, s);
-  }
-  if (D == 64) return f32 ? launch_prefill<f16_t, 64, true, float>(a, s) : launch_prefill<f16_t, 64, true, f16_t>(a, s);
-  return f32 ? launch_prefill<f16_t, 128, true, float>(a, s) : launch_prefill<f16_t, 128, true, f16_t>(a, s);
+  // normalised queries (here) and keys (the caller's guarantee): bounded
+  // scores.  bf16 only: p = exp2(s) reaches 2^16.5 at D = 128, beyond fp16's
+  // range, while bf16 has fp32's exponent range
+  const bool bounded = qknorm && keys_normed && dtype == DG_BF16;
+  if (dtype == DG_BF16)
+    return bounded ? launch_rope_prefill<bf16_t, true>(D, f32, a, s) : launch_rope_prefill<bf16_t, false>(D, f32, a, s);
+  return launch_rope_prefill<f16_t, false>(D, f32, a, s);
 }
 
 }  // namespace dg

@@ -28,6 +28,7 @@ LIB_PATH = Path(
 
 DG_F32, DG_BF16, DG_F16 = 0, 1, 2
 DG_QKNORM = 1
+DG_KEYS_NORMED = 2
 DG_EUNSUPPORTED = -2
 _DTYPE_CODE = {torch.float32: DG_F32, torch.bfloat16: DG_BF16, torch.float16: DG_F16}
 
@@ -314,10 +315,12 @@ def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tenso
 
 
 def prefill_rope_(q: torch.Tensor, freqs: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
-                  scale: float, qknorm: bool) -> bool:
+                  scale: float, qknorm: bool, keys_normed: bool = False) -> bool:
     """dg_prefill_rope: attention over k, v (B,Tk,H,D) views of the query rows
     q (B,Tq,H,D) after RoPE (freqs (B|1,Tq,H|1,D/2,2)) and, with qknorm, the
-    QK-norm -- applied as the kernel loads q -- into y.  Returns False, having
+    QK-norm -- applied as the kernel loads q -- into y.  keys_normed (with
+    qknorm) declares every key row RMS-normalised, which bounds the scores and
+    lets the kernel drop the softmax's running maximum.  Returns False, having
     done nothing, when the fused kernel does not take the shape (the caller
     then makes the two calls); raises on any other error."""
     B, Tq, H, D = q.shape
@@ -336,7 +339,8 @@ def prefill_rope_(q: torch.Tensor, freqs: torch.Tensor, k: torch.Tensor, v: torc
     st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
     rc = lib().dg_prefill_rope(
         B, H, Tq, Tk, D, _dtype_code(q), _ptr(q), st(q), _ptr(freqs), ctypes.pointer(f_st), _dtype_code(freqs),
-        DG_QKNORM if qknorm else 0, _ptr(k), st(k), _ptr(v), st(v), _ptr(y), st(y), float(scale), _stream(q),
+        (DG_QKNORM if qknorm else 0) | (DG_KEYS_NORMED if qknorm and keys_normed else 0),
+        _ptr(k), st(k), _ptr(v), st(v), _ptr(y), st(y), float(scale), _stream(q),
     )
     if rc == DG_EUNSUPPORTED:
         return False

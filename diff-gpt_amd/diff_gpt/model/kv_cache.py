@@ -41,6 +41,7 @@ class KVCache:
         "pos",
         "shared_prefix",
         "pos_dev",
+        "keys_normed",
     )
 
     def __init__(
@@ -63,10 +64,16 @@ class KVCache:
         # use: the graph-replayable kernels read the position from it, and the
         # step advances both copies.  None in ordinary (eager) use.
         self.pos_dev: torch.Tensor | None = None
+        # True while every key below pos was written by the model's attention
+        # (RoPE + QK-norm, mha.py:44-48), i.e. every key row is RMS-normalised;
+        # the prefill kernel then runs its softmax without a running maximum.
+        # insert_kv with caller-supplied keys clears it.
+        self.keys_normed = True
 
     def reset(self) -> None:
         self.pos = 0
         self.shared_prefix = None
+        self.keys_normed = True
 
     def get_pos(self) -> int:
         return self.pos
@@ -114,6 +121,7 @@ class KVCache:
             _native.ops().copy4d(src4, dst4)
         self.pos = n
         self.shared_prefix = (n, sb) if (ob == 1 and sb > 1 and n > 0) else None
+        self.keys_normed = other.keys_normed
 
     # -- capacity management shared by insert_kv and the fused MHA path --
     def ensure_window(
@@ -167,6 +175,7 @@ class KVCache:
             v = v.to(cache.dtype)
         _native.ops().copy4d(k, cache[layer_idx, 0, :, :, t0:t1, :])
         _native.ops().copy4d(v, cache[layer_idx, 1, :, :, t0:t1, :])
+        self.keys_normed = False  # keys from the caller: no norm to rely on
         key_view, value_view = self.layer_views(layer_idx, t1)
         self.advance(layer_idx, t1)
         return key_view, value_view

@@ -143,6 +143,7 @@ class MultiHeadAttention(nn.Module):
             k_rot = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
             ops.rope_qknorm_append(q_in, k, None, freqs_cis, q_rot, k_rot, None, True)
             keys, values = k_rot, v
+            keys_normed = True
         else:
             t0, t1 = kv_cache.ensure_window(T, k.dtype, k.device)
             cache = kv_cache.kv_cache
@@ -158,6 +159,7 @@ class MultiHeadAttention(nn.Module):
             keys, values = k_all.transpose(1, 2), v_all.transpose(1, 2)
             kv_cache.advance(self.layer_idx, t1)
             shared = kv_cache.shared_prefix
+            keys_normed = kv_cache.keys_normed
 
         # SDPA default scale 1/sqrt(head_dim); the mask follows from Tq vs Tk.
         # A broadcast prefix (KVCache.prefill) is read once per row group.
@@ -166,7 +168,8 @@ class MultiHeadAttention(nn.Module):
         y = None
         if fuse_q:
             y = torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
-            if not _native.prefill_rope_(q, freqs_cis, keys, values, y, scale, True):
+            # every key normalised (mha.py:48): the kernel's bounded softmax
+            if not _native.prefill_rope_(q, freqs_cis, keys, values, y, scale, True, keys_normed):
                 # a layout the fused kernel does not take (alignment): rotate q apart
                 q_rot = torch.empty_like(y)
                 ops.rope_qknorm_append(q, None, None, freqs_cis, q_rot, None, None, True)

@@ -55,8 +55,14 @@ enum dg_status {
   DG_EWORKSPACE = -4    /* workspace missing or smaller than required        */
 };
 
-/* Flags of dg_rope_qknorm_append. */
+/* Flags of dg_rope_qknorm_append and dg_prefill_rope. */
 #define DG_QKNORM 1 /* apply the parameter-free RMSNorm after RoPE (mha.py:48) */
+/* dg_prefill_rope only, with DG_QKNORM: every key row of k is RMS-normalised
+ * (as dg_rope_qknorm_append with DG_QKNORM writes it, mha.py:48).  With both
+ * rows normalised every scaled score lies within log2(e)*sqrt(D)*(1+2^-7) in
+ * log2 units, and for bf16 data the kernel drops the running maximum of the
+ * softmax (fp16 data keeps it: exp2 of that bound can exceed fp16's range). */
+#define DG_KEYS_NORMED 2
 
 /* Element strides of a (B,T,H,D) view; the D stride is always 1. */
 typedef struct dg_stride3 {
@@ -127,7 +133,11 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * for bit) and k, v are the cache views (keys already rotated, e.g. by
  * dg_rope_qknorm_append with q = NULL appending them).  freqs / f_st /
  * freqs_dtype as in dg_rope_qknorm_append, for the Tq query rows; flags:
- * DG_QKNORM or 0.  Only the MFMA prefill kernel's shapes are taken (bf16 or
+ * DG_QKNORM or 0, optionally with DG_KEYS_NORMED (DG_QKNORM | DG_KEYS_NORMED:
+ * the keys are normalised too; the softmax then runs without a running
+ * maximum, with the scale folded into the rounded query operand, so y agrees
+ * with dg_attention's within the bf16/fp16 bar rather than bit for bit).
+ * Only the MFMA prefill kernel's shapes are taken (bf16 or
  * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
  * freqs in the data's dtype or fp32): anything else returns DG_EUNSUPPORTED
  * and does nothing, and the caller makes the two calls.

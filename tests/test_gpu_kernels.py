@@ -245,6 +245,55 @@ def test_prefill_rope_random_shapes(dev, dtype, qknorm, shape):
     test_prefill_rope_equals_rope_then_attention(dev, dtype, "f32", qknorm, shape)
 
 
+BOUNDED = [  # (B, H, Tq, Tk, D)
+    (2, 3, 200, 200, 64),   # causal, ragged last query block
+    (1, 2, 130, 330, 128),  # chunked (bottom-right mask), D = 128
+    (2, 2, 16, 16, 64),     # smallest prefill the fused kernel takes
+    (1, 2, 640, 640, 128),  # several query blocks per head
+    (1, 1, 100, 1000, 64),  # chunk far down a long cache
+] + _random_rope_prefills(78, 6)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("fdt", ["f32", "data"])
+@pytest.mark.parametrize("shape", BOUNDED, ids=lambda s: "x".join(map(str, s)))
+def test_prefill_rope_bounded_against_f64(dev, dtype, fdt, shape):
+    """dg_prefill_rope with DG_QKNORM | DG_KEYS_NORMED (keys normalised by
+    dg_rope_qknorm_append, as the model's cache holds them): the softmax runs
+    without a running maximum on scores in log2 units.  y is within the
+    2e-2 * max|ref| bar of float64 attention on the oracle's rotated,
+    normalised q and k, and within the same bar of the running-maximum form."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, Tq, Tk, D = shape
+    wide = _randn((B, Tq, 3 * H * D), 90 + D, dtype, 2.0).to(dev)
+    q = wide[..., H * D : 2 * H * D].view(B, Tq, H, D)
+    k = _randn((B, Tk, H, D), 91 + D, dtype, 3.0).to(dev)
+    v = _randn((B, Tk, H, D), 92 + D, dtype).to(dev)
+    table = precompute_freqs_cis(D, 2 * Tk, 10000)
+    kf = table[:Tk].view(1, Tk, 1, D // 2, 2).to(dev)
+    qf = table[Tk - Tq : Tk].view(1, Tq, 1, D // 2, 2).to(dev)
+    if fdt == "data":
+        kf, qf = kf.to(TDT[dtype]), qf.to(TDT[dtype])
+    k_rot = torch.empty_like(k)
+    _native.rope_qknorm_append_(None, k, None, kf, None, k_rot, None, True)
+    scale = 1.0 / D**0.5
+    y = torch.empty((B, Tq, H, D), dtype=TDT[dtype], device=dev)
+    assert _native.prefill_rope_(q, qf, k_rot, v, y, scale, True, keys_normed=True)
+    y_max = torch.empty_like(y)
+    assert _native.prefill_rope_(q, qf, k_rot, v, y_max, scale, True)
+    torch.cuda.synchronize()
+    exp_q = on.rope_qknorm(q.float().cpu().numpy(), qf.float().cpu().numpy(), dtype)
+    exp_k = on.rope_qknorm(k.float().cpu().numpy(), kf.float().cpu().numpy(), dtype)
+    assert np.array_equal(_bits(k_rot), exp_k.view(np.uint32))
+    ref = on.attention_f64(exp_q, exp_k, v.float().cpu().numpy())
+    got = y.float().cpu().numpy()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= TOL[dtype]
+    two = y_max.float().cpu().numpy()
+    assert np.abs(got - two).max() / np.abs(two).max() <= TOL[dtype]
+
+
 @pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 64), "f32"),
                                          ((1, 2, 8, 8, 64), "bf16")])
 def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
