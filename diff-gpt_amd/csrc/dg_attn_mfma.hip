@@ -230,10 +230,23 @@ __device__ __forceinline__ int piece_swz(int r) {
 }
 
 
+#ifndef DG_PREFILL_BUFFER_DMA
+#define DG_PREFILL_BUFFER_DMA 1
+#endif
+// Third dword of a raw buffer resource on gfx9-family chips (gfx950 included):
+// 32-bit data format, no swizzle, no stride.
+constexpr int kBufferWord3 = 0x00020000;
+
 // 16 bytes per lane from global memory straight into LDS: lane l of the wave
 // writes lds + 16*l (lds wave-uniform), no registers involved
 __device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
   __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+// The same through a buffer resource: 16 bytes per lane from byte offset
+// voff + soff of the resource (zeros past its range) into lds + 16*l.  The
+// address-space cast stays inside this device function.
+__device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 // ds_read_b64_tr_b16: within each 16 lanes, lane t receives element t & 3 of
 // the 8-byte chunks addressed by lanes t/4, 4 + t/4, 8 + t/4, 12 + t/4
@@ -302,8 +315,36 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   // ---- global -> LDS copy of one key tile (no registers involved) -----------
   // Wave wv copies DMA_PER_WAVE blocks of 1 KB of K and of V; lane l of a block
   // fills slot l % PPR of row l / PPR with the piece that the swizzle puts
-  // there.  Rows past Tk re-read the last key (masked, probability 0).
+  // there.
   const int dma_row = lane / PPR, dma_slot = lane % PPR;
+#if DG_PREFILL_BUFFER_DMA
+  // Buffer loads over this head's K and V rows: the per-lane byte offsets of
+  // a tile's pieces are fixed, the tile's start goes into the scalar offset,
+  // so a tile's copies cost no vector arithmetic.  Rows past Tk lie beyond
+  // the resource's range and read as zeros (their keys are masked).
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(kp), 0, (int)(((int64_t)(a.Tk - 1) * a.kt + D) * 2), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(vp), 0, (int)(((int64_t)(a.Tk - 1) * a.vt + D) * 2), kBufferWord3);
+  int kvo[C::DMA_PER_WAVE], vvo[C::DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
+    const int row = (wv * C::DMA_PER_WAVE + i) * C::ROWS_PER_DMA + dma_row;
+    const int piece = dma_slot ^ piece_swz<D>(row);
+    kvo[i] = (row * (int)a.kt + 8 * piece) * 2;
+    vvo[i] = (row * (int)a.vt + 8 * piece) * 2;
+  }
+  auto dma_tile = [&](uint16_t* ks, uint16_t* vs, int kt0) __attribute__((always_inline)) {
+    const int ks0 = kt0 * (int)a.kt * 2, vs0 = kt0 * (int)a.vt * 2;
+#pragma unroll
+    for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
+      const int blk = wv * C::DMA_PER_WAVE + i;
+      lds_copy16_buf(krs, kvo[i], ks0, ks + blk * 512);
+      lds_copy16_buf(vrs, vvo[i], vs0, vs + blk * 512);
+    }
+  };
+#else
+  // Rows past Tk re-read the last key (masked, probability 0).
   auto dma_tile = [&](uint16_t* ks, uint16_t* vs, int kt0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
@@ -315,6 +356,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       lds_copy16(vp + key * (int)a.vt + 8 * piece, vs + blk * 512);
     }
   };
+#endif
   // this wave's copies are in LDS (each wave waits for its own before the
   // barrier that hands the stage to all waves)
   auto stage_ready = [&]() __attribute__((always_inline)) {
@@ -348,14 +390,12 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     dma_tile(ks0, vs0, 0);
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb) {
-      const bool row_live = qw + 32 * qb + r32 < a.Tq;
+      // rows past Tq hold row Tq - 1 (finite, normalised) and are never stored
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        rope_rotate<T, 8>(x[qb][c], cs[qb][c]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[qb][c][i] = row_live ? x[qb][c][i] : 0.f;
-      }
-      if (a.qknorm) {  // lanes l and l^32 hold the same row: both take this branch  // lanes l and l^32 hold the same row: both take this branch
+      for (int c = 0; c < NC; ++c) rope_rotate<T, 8>(x[qb][c], cs[qb][c]);
+      // the bounded form is launched with the norm only; lanes l and l^32 hold
+      // the same row, so both take this branch
+      if (BND || a.qknorm) {
         float s16[NC];
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
@@ -365,19 +405,14 @@ void prefill_mfma_kernel(const PrefillArgs a) {
           s16[c] = half_pair_sum(tree_sum<8>(sq));
         }
         const float mean = tree_sum<NC>(s16) / (float)D;
-        const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+        float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+        // bounded form: the operand is the normalised row times scale*log2(e),
+        // rounded once, so the scores come out of the MFMA in log2 units
+        if constexpr (BND) r = r * a.scale_log2;
 #pragma unroll
         for (int c = 0; c < NC; ++c)
 #pragma unroll
           for (int i = 0; i < 8; ++i) x[qb][c][i] = x[qb][c][i] * r;
-      }
-      if constexpr (BND) {
-        // bounded form: the operand is the normalised row times scale*log2(e),
-        // rounded once, so the scores come out of the MFMA in log2 units
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int i = 0; i < 8; ++i) x[qb][c][i] = x[qb][c][i] * a.scale_log2;
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -722,9 +757,9 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
   if (Tq < 16) return false;  // decode and tiny chunks: vector kernel
   const int64_t nwg = (int64_t)B * H * ((Tq + 127) / 128);
   if (nwg <= 0 || nwg > 0x7fffffffLL) return false;
-  // per-head row offsets are 32-bit inside the kernel
+  // per-head byte offsets (buffer ranges) are 32-bit signed inside the kernel
   const int64_t span = (int64_t)Tk * (k_st->t > v_st->t ? k_st->t : v_st->t);
-  if (span >= (int64_t)1 << 31 || k_st->t < 0 || v_st->t < 0) return false;
+  if (span >= (int64_t)1 << 30 || k_st->t < 0 || v_st->t < 0) return false;
   return aligned16(q) && aligned16(k) && aligned16(v) && aligned16(y) && strides8(q_st) &&
          strides8(k_st) && strides8(v_st) && strides8(y_st);
 }
