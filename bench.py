@@ -71,11 +71,18 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
     cap = PREFIX + NEW
     g = torch.Generator(device=dev).manual_seed(0)
 
-    # KV cache (L,2,B,H,cap,D): per-series prefix broadcast to its 100 rows
-    # (KVCache.prefill), positions >= PREFIX written by the decode job.
-    cache = torch.empty((L, 2, B, H, cap, D), dtype=dt, device=dev)
-    prefix = torch.randn((L, 2, SERIES, 1, H, PREFIX, D), generator=g, device=dev).to(dt)
-    cache.view(L, 2, SERIES, TRAJ, H, cap, D)[..., :PREFIX, :] = prefix
+    # shared: the KVCache.prefill layout -- each series' 96-token prefix once,
+    # as (L,2,SERIES,H,PREFIX,D) pages, and each row's pages holding positions
+    # PREFIX.. only; plain: every row's (L,2,B,H,cap,D) pages hold the whole
+    # prefix (the reference's broadcast copy) and are read as such
+    prefix = torch.randn((L, 2, SERIES, H, PREFIX, D), generator=g, device=dev).to(dt)
+    if shared:
+        own0 = PREFIX
+        cache = torch.empty((L, 2, B, H, NEW, D), dtype=dt, device=dev)
+    else:
+        own0 = 0
+        cache = torch.empty((L, 2, B, H, cap, D), dtype=dt, device=dev)
+        cache.view(L, 2, SERIES, TRAJ, H, cap, D)[..., :PREFIX, :] = prefix.unsqueeze(3)
     table = precompute_freqs_cis(D, 2 * 138, 10000).to(dev).to(dt)
     # synthetic projections for every (step, layer): q, k, v (B,1,H,D)
     qkv = torch.randn((NEW, L, 3, B, 1, H, D), generator=g, device=dev).to(dt)
@@ -94,9 +101,15 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
     P = ctypes.pointer
     S3 = _native._bthd_strides
     packs = []
-    # shared: the 96-token prefix of each series is read from the series'
-    # first row (all 100 rows hold it, KVCache.prefill)
-    prefix_len, group = (PREFIX, TRAJ) if shared else (0, 1)
+    keep = []  # ctypes objects the argument packs point at
+    if shared:
+        pre_arg = [None] * L
+        for layer in range(L):
+            pk, pv = prefix[layer, 0].transpose(1, 2), prefix[layer, 1].transpose(1, 2)
+            pre_arg[layer], _ = _native._prefix_arg(_native.Prefix(PREFIX, TRAJ, pk, pv, PREFIX))
+        keep.append(pre_arg)
+    else:
+        pre_arg = [None] * L
     for s in range(NEW):
         t0 = PREFIX + s
         fc = table[t0:t0 + 1].view(1, 1, 1, D // 2, 2)
@@ -110,13 +123,13 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
                 args = (B, H, D, code, _native._ptr(q), P(S3(q)), _native._ptr(k), P(S3(k)),
                         _native._ptr(v), P(S3(v)), _native._ptr(kc), P(S3(kc)), _native._ptr(vc), P(S3(vc)),
                         _native._ptr(table[t0]), 0, code, t0, None, cap, _native._ptr(y), P(S3(y)),
-                        0.25, prefix_len, group, _native.DG_QKNORM, None, 0, stream)
+                        0.25, pre_arg[layer], _native.DG_QKNORM, None, 0, stream)
                 packs.append((None, args))
                 continue
-            kd = cache[layer, 0, :, :, t0:t0 + 1].transpose(1, 2)
-            vd = cache[layer, 1, :, :, t0:t0 + 1].transpose(1, 2)
-            keys = cache[layer, 0, :, :, :t0 + 1].transpose(1, 2)
-            vals = cache[layer, 1, :, :, :t0 + 1].transpose(1, 2)
+            kd = cache[layer, 0, :, :, t0 - own0:t0 - own0 + 1].transpose(1, 2)
+            vd = cache[layer, 1, :, :, t0 - own0:t0 - own0 + 1].transpose(1, 2)
+            keys = cache[layer, 0, :, :, :t0 + 1 - own0].transpose(1, 2)
+            vals = cache[layer, 1, :, :, :t0 + 1 - own0].transpose(1, 2)
             rope_args = (B, 1, H, D, code,
                          _native._ptr(q), P(S3(q)), _native._ptr(q_rot), P(S3(q_rot)),
                          _native._ptr(k), P(S3(k)), _native._ptr(kd), P(S3(kd)),
@@ -127,7 +140,7 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
             attn_args = (B, H, 1, t0 + 1, D, code,
                          _native._ptr(q_rot), P(S3(q_rot)), _native._ptr(keys), P(S3(keys)),
                          _native._ptr(vals), P(S3(vals)), _native._ptr(y), P(S3(y)),
-                         0.25, prefix_len, group, None, 0, stream)
+                         0.25, pre_arg[layer], None, 0, stream)
             packs.append((rope_args, attn_args))
     rope_fn = lib.dg_rope_qknorm_append
     attn_fn = lib.dg_decode_step if fused else lib.dg_attention_grouped

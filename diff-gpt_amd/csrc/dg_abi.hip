@@ -31,18 +31,18 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D);
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  int prefix_len, int group, const int* pos_dev, void* workspace,
+                  const PrefixRef& pre, const int* pos_dev, void* workspace,
                   size_t workspace_bytes, hipStream_t s);
 // dg_attn_shared.hip
-bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, int prefix_len,
-                                 int group, const void* q, const dg_stride3* q_st, const void* k,
+bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const PrefixRef& pre,
+                                 const void* q, const dg_stride3* q_st, const void* k,
                                  const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
                                  const void* y, const dg_stride3* y_st);
 int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
                      const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
-                     void* y, const dg_stride3* y_st, float scale, int prefix_len, int group,
+                     void* y, const dg_stride3* y_st, float scale, const PrefixRef& pre,
                      const int* pos_dev, hipStream_t s);
-bool shared_step_applicable(int B, int H, int D, int dtype, int prefix_len, int group, int max_pos,
+bool shared_step_applicable(int B, int H, int D, int dtype, const PrefixRef& pre, int max_pos,
                             const void* q, const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                             const void* v, const dg_stride3* v_st, const void* kc, const dg_stride3* kc_st,
                             const void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
@@ -51,8 +51,14 @@ int shared_decode_step(int B, int H, int D, int dtype, const void* q, const dg_s
                        const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
                        const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs,
                        int64_t fpos, int fdtype, int pos, const int* pos_dev, int max_pos, void* y,
-                       const dg_stride3* y_st, float scale, int prefix_len, int group, int qknorm,
+                       const dg_stride3* y_st, float scale, const PrefixRef& pre, int qknorm,
                        hipStream_t s);
+// dg_rope.hip
+int rope_append_at(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, void* q_out,
+                   const dg_stride3* qo_st, const void* k, const dg_stride3* k_st, void* k_cache,
+                   const dg_stride3* kc_st, const void* v, const dg_stride3* v_st, void* v_cache,
+                   const dg_stride3* vc_st, const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
+                   const int32_t* pos, int min_pos, int max_pos, int flags, void* stream);
 // dg_attn_mfma.hip
 bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
@@ -119,6 +125,41 @@ __global__ __launch_bounds__(256) void copy4d_rows_kernel(const CopyArgs a) {
   }
 }
 
+// The dg_prefix of a call as the kernels read it (PrefixRef), after checking
+// it against the cache views: positions t < len of row b come from the
+// group's prefix pages (the group's first row of the cache when prefix->k is
+// NULL); the cache views, which start at position own_start, are shifted so
+// that the kernels index every cache position absolutely.  limit is the
+// number of positions the call covers (Tk, or max_pos).
+int resolve_prefix(const dg_prefix* p, int limit, int dtype, const char* what, const void*& k,
+                   const dg_stride3* k_st, const void*& v, const dg_stride3* v_st, PrefixRef& out) {
+  out = PrefixRef{k, v, 0, 0, 0, 0, 0, 1, 0};
+  if (p == nullptr) return DG_OK;
+  DG_REQUIRE(p->group >= 1, DG_EINVAL, "%s: prefix group must be >= 1 (got %d)", what, p->group);
+  DG_REQUIRE(p->len >= 0 && p->len <= limit, DG_EINVAL, "%s: prefix len %d outside [0, %d]", what, p->len,
+             limit);
+  DG_REQUIRE((p->k == nullptr) == (p->v == nullptr), DG_EINVAL, "%s: prefix k and v must both be given or NULL",
+             what);
+  DG_REQUIRE(p->own_start >= 0 && p->own_start <= p->len, DG_EINVAL,
+             "%s: prefix own_start %d outside [0, len=%d]", what, p->own_start, p->len);
+  DG_REQUIRE(p->k != nullptr || p->own_start == 0, DG_EINVAL,
+             "%s: own_start > 0 needs prefix pages of their own (k, v)", what);
+  if (p->k == nullptr && (p->group == 1 || p->len == 0)) return DG_OK;  // no sharing
+  if (p->k != nullptr) {
+    DG_REQUIRE(p->k_st.t == k_st->t && p->v_st.t == v_st->t, DG_EINVAL,
+               "%s: prefix pages must have the cache's position stride", what);
+    const int64_t es = dtype == DG_F32 ? 4 : 2;
+    k = static_cast<const char*>(k) - (int64_t)p->own_start * k_st->t * es;
+    v = static_cast<const char*>(v) - (int64_t)p->own_start * v_st->t * es;
+    out = PrefixRef{p->k, p->v, p->k_st.b, p->k_st.h, p->v_st.b, p->v_st.h, p->len, p->group, p->own_start};
+  } else {
+    out = PrefixRef{k, v, (int64_t)p->group * k_st->b, k_st->h, (int64_t)p->group * v_st->b, v_st->h,
+                    p->len, p->group, 0};
+  }
+  if (p->len == 0) out.len = 0;
+  return DG_OK;
+}
+
 }  // namespace dg
 
 using namespace dg;
@@ -136,33 +177,34 @@ extern "C" size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int 
 extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                                     const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                                     const void* v, const dg_stride3* v_st, void* y,
-                                    const dg_stride3* y_st, float scale, int prefix_len, int group,
+                                    const dg_stride3* y_st, float scale, const dg_prefix* prefix,
                                     void* workspace, size_t workspace_bytes, void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0 && Tq >= 0 && Tk >= 0, DG_EINVAL, "attention: negative size");
   DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
              "attention: dtype %d unsupported", dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention: head_dim must be even (got %d)", D);
-  DG_REQUIRE(group >= 1, DG_EINVAL, "attention: group must be >= 1 (got %d)", group);
-  DG_REQUIRE(prefix_len >= 0 && prefix_len <= Tk, DG_EINVAL,
-             "attention: prefix_len %d outside [0, Tk=%d]", prefix_len, Tk);
   if ((int64_t)B * H * Tq == 0) return DG_OK;
   DG_REQUIRE(Tk >= Tq, DG_EINVAL, "attention: Tk (%d) < Tq (%d)", Tk, Tq);
   DG_REQUIRE(q && k && v && y && q_st && k_st && v_st && y_st, DG_EINVAL, "attention: NULL argument");
+  const void* kk = k;
+  const void* vv = v;
+  PrefixRef pre;
+  const int rc = resolve_prefix(prefix, Tk, dtype, "attention", kk, k_st, vv, v_st, pre);
+  if (rc != DG_OK) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  // The MFMA prefill kernel reads every row's own keys: equal results, since
-  // the rows of a group hold identical prefixes.
-  if (mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
+  // The MFMA prefill kernel reads every row's own keys: equal results when
+  // the rows hold the prefix themselves (identical within a group).
+  const bool rows_hold_all = prefix == nullptr || prefix->k == nullptr;
+  if (rows_hold_all &&
+      mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale))
     return mfma_prefill(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, s);
-  if (group == 1) prefix_len = 0;
   // Groups of at least 16 rows: the shared prefix as a matrix product (when the
   // vector kernel would not split the keys, so no workspace is involved).
   if (vec_attention_splits(B, H, Tq, Tk, D) == 1 &&
-      shared_attention_applicable(B, H, Tq, Tk, D, dtype, prefix_len, group, q, q_st, k, k_st, v, v_st,
-                                  y, y_st))
-    return shared_attention(B, H, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
-                            group, nullptr, s);
-  return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len,
-                       group, nullptr, workspace, workspace_bytes, s);
+      shared_attention_applicable(B, H, Tq, Tk, D, dtype, pre, q, q_st, kk, k_st, vv, v_st, y, y_st))
+    return shared_attention(B, H, Tk, D, dtype, q, q_st, kk, k_st, vv, v_st, y, y_st, scale, pre, nullptr, s);
+  return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, kk, k_st, vv, v_st, y, y_st, scale, pre, nullptr,
+                       workspace, workspace_bytes, s);
 }
 
 extern "C" int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
@@ -201,7 +243,7 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
                                       const dg_stride3* q_st, const void* k_cache,
                                       const dg_stride3* kc_st, const void* v_cache,
                                       const dg_stride3* vc_st, void* y, const dg_stride3* y_st,
-                                      float scale, int prefix_len, int group, const int32_t* pos,
+                                      float scale, const dg_prefix* prefix, const int32_t* pos,
                                       int max_keys, void* workspace, size_t workspace_bytes,
                                       void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "attention_at: negative size");
@@ -209,23 +251,22 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
              "attention_at: dtype %d unsupported", dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention_at: head_dim must be even (got %d)", D);
   DG_REQUIRE(max_keys >= 1, DG_EINVAL, "attention_at: max_keys must be >= 1 (got %d)", max_keys);
-  DG_REQUIRE(group >= 1, DG_EINVAL, "attention_at: group must be >= 1 (got %d)", group);
-  DG_REQUIRE(prefix_len >= 0 && prefix_len <= max_keys, DG_EINVAL,
-             "attention_at: prefix_len %d outside [0, max_keys=%d]", prefix_len, max_keys);
   if ((int64_t)B * H == 0) return DG_OK;
   DG_REQUIRE(pos && q && k_cache && v_cache && y && q_st && kc_st && vc_st && y_st, DG_EINVAL,
              "attention_at: NULL argument");
-  if (group == 1) prefix_len = 0;
+  const void* kk = k_cache;
+  const void* vv = v_cache;
+  PrefixRef pre;
+  const int rc = resolve_prefix(prefix, max_keys, dtype, "attention_at", kk, kc_st, vv, vc_st, pre);
+  if (rc != DG_OK) return rc;
   // The kernels read at most max_keys keys (Tk = min(*pos + 1, max_keys)); key
   // splits and the workspace are sized for max_keys.
   if (vec_attention_splits(B, H, 1, max_keys, D) == 1 &&
-      shared_attention_applicable(B, H, 1, max_keys, D, dtype, prefix_len, group, q, q_st, k_cache, kc_st,
-                                  v_cache, vc_st, y, y_st))
-    return shared_attention(B, H, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
-                            scale, prefix_len, group, pos, static_cast<hipStream_t>(stream));
-  return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, k_cache, kc_st, v_cache, vc_st, y, y_st,
-                       scale, prefix_len, group, pos, workspace, workspace_bytes,
-                       static_cast<hipStream_t>(stream));
+      shared_attention_applicable(B, H, 1, max_keys, D, dtype, pre, q, q_st, kk, kc_st, vv, vc_st, y, y_st))
+    return shared_attention(B, H, max_keys, D, dtype, q, q_st, kk, kc_st, vv, vc_st, y, y_st, scale, pre, pos,
+                            static_cast<hipStream_t>(stream));
+  return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, kk, kc_st, vv, vc_st, y, y_st, scale, pre, pos,
+                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype) {
@@ -237,7 +278,7 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
                               void* k_cache, const dg_stride3* kc_st, void* v_cache, const dg_stride3* vc_st,
                               const void* freqs, int64_t freqs_pos_stride, int freqs_dtype, int pos,
                               const int32_t* pos_dev, int max_pos, void* y, const dg_stride3* y_st,
-                              float scale, int prefix_len, int group, int flags, void* workspace,
+                              float scale, const dg_prefix* prefix, int flags, void* workspace,
                               size_t workspace_bytes, void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "decode_step: negative size");
   DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
@@ -246,49 +287,65 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
              "decode_step: freqs dtype %d unsupported", freqs_dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "decode_step: head_dim must be even (got %d)", D);
   DG_REQUIRE(max_pos >= 1, DG_EINVAL, "decode_step: max_pos must be >= 1 (got %d)", max_pos);
-  DG_REQUIRE(group >= 1, DG_EINVAL, "decode_step: group must be >= 1 (got %d)", group);
-  DG_REQUIRE(prefix_len >= 0 && prefix_len <= max_pos, DG_EINVAL,
-             "decode_step: prefix_len %d outside [0, max_pos=%d]", prefix_len, max_pos);
   DG_REQUIRE(freqs_pos_stride >= 0, DG_EINVAL, "decode_step: negative freqs_pos_stride");
+  DG_REQUIRE(kc_st && vc_st, DG_EINVAL, "decode_step: NULL cache strides");
+  const void* kk = k_cache;
+  const void* vv = v_cache;
+  PrefixRef pre;
+  int rc = resolve_prefix(prefix, max_pos, dtype, "decode_step", kk, kc_st, vv, vc_st, pre);
+  if (rc != DG_OK) return rc;
+  DG_REQUIRE(pre.own_start < max_pos, DG_EINVAL, "decode_step: the cache pages hold no position (own_start %d, "
+             "max_pos %d)", pre.own_start, max_pos);
   if (pos_dev == nullptr) {
     DG_REQUIRE(pos >= 0 && pos < max_pos, DG_EINVAL, "decode_step: position %d outside [0, max_pos=%d)", pos,
                max_pos);
-    DG_REQUIRE(group == 1 || prefix_len <= pos, DG_EINVAL,
-               "decode_step: position %d inside the shared prefix (prefix_len %d)", pos, prefix_len);
+    DG_REQUIRE(pos >= pre.len, DG_EINVAL, "decode_step: position %d inside the shared prefix (len %d)", pos,
+               pre.len);
   }
   if ((int64_t)B * H == 0) return DG_OK;
-  DG_REQUIRE(q && k && v && k_cache && v_cache && freqs && y && q_st && k_st && v_st && kc_st && vc_st && y_st,
-             DG_EINVAL, "decode_step: NULL argument");
-  if (group == 1) prefix_len = 0;
+  DG_REQUIRE(q && k && v && k_cache && v_cache && freqs && y && q_st && k_st && v_st && y_st, DG_EINVAL,
+             "decode_step: NULL argument");
+  void* kw = const_cast<void*>(kk);
+  void* vw = const_cast<void*>(vv);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int qknorm = (flags & DG_QKNORM) ? 1 : 0;
   if (vec_attention_splits(B, H, 1, max_pos, D) == 1 &&
-      shared_step_applicable(B, H, D, dtype, prefix_len, group, max_pos, q, q_st, k, k_st, v, v_st, k_cache,
-                             kc_st, v_cache, vc_st, freqs, freqs_pos_stride, freqs_dtype, y, y_st))
-    return shared_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, k_cache, kc_st, v_cache, vc_st, freqs,
-                              freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, prefix_len,
-                              group, qknorm, s);
+      shared_step_applicable(B, H, D, dtype, pre, max_pos, q, q_st, k, k_st, v, v_st, kw, kc_st, vw, vc_st,
+                             freqs, freqs_pos_stride, freqs_dtype, y, y_st))
+    return shared_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, kw, kc_st, vw, vc_st, freqs,
+                              freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, pre, qknorm,
+                              s);
   // Two launches: RoPE/QK-norm/append with the rotated q staged in y, then the
   // attention reading q from y (every attention kernel reads a query row
-  // before it writes the output row at the same place).
-  int rc;
+  // before it writes the output row at the same place).  Both index the
+  // shifted cache pointers absolutely.
   if (pos_dev != nullptr) {
-    rc = dg_rope_qknorm_append_at(B, H, D, dtype, q, q_st, y, y_st, k, k_st, k_cache, kc_st, v, v_st, v_cache,
-                                  vc_st, freqs, freqs_pos_stride, freqs_dtype, pos_dev, max_pos, flags, stream);
+    rc = rope_append_at(B, H, D, dtype, q, q_st, y, y_st, k, k_st, kw, kc_st, v, v_st, vw, vc_st, freqs,
+                        freqs_pos_stride, freqs_dtype, pos_dev, pre.own_start, max_pos, flags, stream);
     if (rc != DG_OK) return rc;
-    return dg_decode_attention_at(B, H, D, dtype, y, y_st, k_cache, kc_st, v_cache, vc_st, y, y_st, scale,
-                                  prefix_len, group, pos_dev, max_pos, workspace, workspace_bytes, stream);
+    return vec_attention_splits(B, H, 1, max_pos, D) == 1 &&
+                   shared_attention_applicable(B, H, 1, max_pos, D, dtype, pre, y, y_st, kw, kc_st, vw, vc_st, y,
+                                               y_st)
+               ? shared_attention(B, H, max_pos, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
+                                  pos_dev, s)
+               : vec_attention(B, H, 1, max_pos, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
+                               pos_dev, workspace, workspace_bytes, s);
   }
   const int64_t es = dtype == DG_F32 ? 4 : 2, fes = freqs_dtype == DG_F32 ? 4 : 2;
   const dg_stride3 f_st = {0, 0, 0};
   rc = dg_rope_qknorm_append(B, 1, H, D, dtype, q, q_st, y, y_st, k, k_st,
-                             static_cast<char*>(k_cache) + (int64_t)pos * kc_st->t * es, kc_st, v, v_st,
-                             static_cast<char*>(v_cache) + (int64_t)pos * vc_st->t * es, vc_st,
+                             static_cast<char*>(kw) + (int64_t)pos * kc_st->t * es, kc_st, v, v_st,
+                             static_cast<char*>(vw) + (int64_t)pos * vc_st->t * es, vc_st,
                              static_cast<const char*>(freqs) + (int64_t)pos * freqs_pos_stride * fes, &f_st,
                              freqs_dtype, flags, stream);
   if (rc != DG_OK) return rc;
-  return dg_attention_grouped(B, H, 1, pos + 1, D, dtype, y, y_st, k_cache, kc_st, v_cache, vc_st, y, y_st, scale,
-                              prefix_len, group, workspace, workspace_bytes, stream);
+  return vec_attention_splits(B, H, 1, pos + 1, D) == 1 &&
+                 shared_attention_applicable(B, H, 1, pos + 1, D, dtype, pre, y, y_st, kw, kc_st, vw, vc_st, y,
+                                             y_st)
+             ? shared_attention(B, H, pos + 1, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
+                                nullptr, s)
+             : vec_attention(B, H, 1, pos + 1, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
+                             nullptr, workspace, workspace_bytes, s);
 }
 
 extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
@@ -296,7 +353,7 @@ extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, cons
                             const void* v, const dg_stride3* v_st, void* y,
                             const dg_stride3* y_st, float scale, void* workspace,
                             size_t workspace_bytes, void* stream) {
-  return dg_attention_grouped(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, 0, 1,
+  return dg_attention_grouped(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, nullptr,
                               workspace, workspace_bytes, stream);
 }
 

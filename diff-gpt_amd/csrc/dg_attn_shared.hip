@@ -2,14 +2,15 @@
 // groups sharing a cache prefix, with the prefix on the matrix cores.
 //
 // After KVCache.prefill from a batch-1 cache (kv_cache.py:77-79) the `group`
-// consecutive rows of each group hold identical keys and values at positions
-// 0 .. prefix_len-1.  For one decode step the scores of a group's rows against
-// that prefix form a real matrix product, S = Q_rows K_prefix^T, and so does
-// P V_prefix: this kernel runs both on MFMA, reading the prefix (L2-resident,
-// shared by the tiles of a group) once per 16-row tile.  The rows' own keys,
-// positions prefix_len .. Tk-1, differ from row to row and go through the
-// vector ALUs.  The two parts run at the same time on two wavefronts and merge
-// at the end.
+// consecutive rows of each group share the keys and values at positions
+// 0 .. len-1 (dg_prefix: stored once per group, or in each group's first row
+// of a broadcast cache).  For one decode step the scores of a group's rows
+// against that prefix form a real matrix product, S = Q_rows K_prefix^T, and
+// so does P V_prefix: this kernel runs both on MFMA, reading the prefix
+// (L2-resident, shared by the tiles of a group) once per 16-row tile.  The
+// rows' own keys, positions len .. Tk-1, differ from row to row and go through
+// the vector ALUs.  The two parts run at the same time on two wavefronts and
+// merge at the end.
 //
 // Work unit = one block of two wavefronts = (group, tile of 16 rows of the
 // group, head).  Wave 0 takes the prefix, wave 1 the own keys.
@@ -57,7 +58,8 @@ struct SharedArgs {
   int64_t vb, vt, vh;
   int64_t yb, yh;
   int64_t units;  // ceil(B / group) * tiles * H
-  int B, H, D, Tk, prefix_len, group, tiles;
+  int B, H, D, Tk, tiles;
+  PrefixRef pre;  // the groups' prefix pages (pre.group rows per group)
   float scale_log2;  // scale * log2(e)
   float lazy_raw;    // kSharedLazyLog2 / scale_log2
   // graph-replayable form: keys are positions 0 .. *pos_dev, at most Tk
@@ -176,12 +178,12 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   const int tile = rest % a.tiles;
   const int grp = rest / a.tiles;
 
-  const int64_t b0 = (int64_t)grp * a.group;  // the group's first row holds the prefix
+  const int64_t b0 = (int64_t)grp * a.pre.group;  // the group's first row
   // tile row r of the unit -> batch row (rows past the group compute on b0
   // and store nothing)
   auto row_of = [&](int r, bool& ok) __attribute__((always_inline)) {
     const int rin = tile * 16 + r;
-    ok = rin < a.group && b0 + rin < a.B;
+    ok = rin < a.pre.group && b0 + rin < a.B;
     return ok ? b0 + rin : b0;
   };
 
@@ -190,7 +192,8 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   int Tk, Tc;
   if constexpr (FUSED) {
     const int pos = a.pos_dev != nullptr ? *a.pos_dev : a.pos;
-    if (pos < 0 || pos >= a.max_pos) return;  // uniform over the grid
+    // uniform over the grid; the append goes to the rows' own pages
+    if (pos < a.pre.own_start || pos >= a.max_pos) return;
     Tk = pos + 1;
     Tc = pos;
   } else {
@@ -199,7 +202,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     Tc = Tk;
   }
   (void)Tk;
-  const int P = min(a.prefix_len, Tc);
+  const int P = min(a.pre.len, Tc);
   const float cl = a.scale_log2;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
   const T* kbase = static_cast<const T*>(a.k) + (int64_t)h * a.kh;
@@ -234,8 +237,8 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   // wait for them.
   if (role == 0) {
     // --- prefix on MFMA: lane (c, g) -------------------------------------------
-    const T* kpre = kbase + b0 * a.kb;
-    const T* vpre = vbase + b0 * a.vb;
+    const T* kpre = static_cast<const T*>(a.pre.k) + grp * a.pre.kb + (int64_t)h * a.pre.kh;
+    const T* vpre = static_cast<const T*>(a.pre.v) + grp * a.pre.vb + (int64_t)h * a.pre.vh;
     Op kopA[NT], kopB[D == 16 ? NT : 1];
     T vvA[NT][4][DT], vvB[D == 16 ? NT : 1][4][DT];
     // the first 128 prefix keys (64 at D = 32)
@@ -377,9 +380,11 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
         load_row<T, EPL>(vr[u], vown + j * vt);
       }
     };
-    // the first two sets
+    // the first two sets (only when there are own keys: the own pages may
+    // start at P, so no position below it is read from them)
     auto first_sets = [&]() __attribute__((always_inline)) {
-      const int last = max(Tc - 1, 0);
+      if (Tc <= P) return;  // wave-uniform
+      const int last = Tc - 1;
 #pragma unroll
       for (int u = 0; u < 2 * UO; ++u) {
         const int j = min(P + KPQ * u + kk, last);
@@ -524,13 +529,14 @@ int launch_shared_d(const SharedArgs& a, hipStream_t s) {
 
 void fill_common(SharedArgs& a, int B, int H, int D, int Tk, const void* q, const dg_stride3* q_st,
                  const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
-                 const dg_stride3* y_st, float scale, int prefix_len, int group, const int* pos_dev) {
+                 const dg_stride3* y_st, float scale, const PrefixRef& pre, const int* pos_dev) {
+  const int group = pre.group;
   a.q = q; a.k = k; a.v = v; a.y = y;
   a.qb = q_st->b; a.qh = q_st->h;
   a.kb = k_st->b; a.kt = k_st->t; a.kh = k_st->h;
   a.vb = v_st->b; a.vt = v_st->t; a.vh = v_st->h;
   a.yb = y_st->b; a.yh = y_st->h;
-  a.B = B; a.H = H; a.D = D; a.Tk = Tk; a.prefix_len = prefix_len; a.group = group;
+  a.B = B; a.H = H; a.D = D; a.Tk = Tk; a.pre = pre;
   a.tiles = (group + 15) / 16;
   a.units = (((int64_t)B + group - 1) / group) * a.tiles * H;
   a.scale_log2 = scale * 1.44269504088896340736f;
@@ -543,11 +549,12 @@ void fill_common(SharedArgs& a, int B, int H, int D, int Tk, const void* q, cons
 // The matrix-core path takes single-token decode over groups of at least 16
 // rows, head_dim 16 or 32, 16-byte aligned rows; everything else stays on the
 // vector kernel.
-bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, int prefix_len,
-                                 int group, const void* q, const dg_stride3* q_st, const void* k,
+bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const PrefixRef& pre,
+                                 const void* q, const dg_stride3* q_st, const void* k,
                                  const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
                                  const void* y, const dg_stride3* y_st) {
-  if (Tq != 1 || group < kSharedMinGroup || prefix_len < 1 || prefix_len > Tk) return false;
+  const int group = pre.group;
+  if (Tq != 1 || group < kSharedMinGroup || pre.len < 1 || pre.len > Tk) return false;
   if (D != 16 && D != 32) return false;
   if (dtype != DG_F32 && dtype != DG_BF16 && dtype != DG_F16) return false;
   const int64_t es = dtype == DG_F32 ? 4 : 2;
@@ -556,6 +563,8 @@ bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype,
   if (!st16(q_st->b) || !st16(q_st->h) || !st16(y_st->b) || !st16(y_st->h)) return false;
   if (!st16(k_st->b) || !st16(k_st->t) || !st16(k_st->h)) return false;
   if (!st16(v_st->b) || !st16(v_st->t) || !st16(v_st->h)) return false;
+  if (!al16(pre.k) || !al16(pre.v) || !st16(pre.kb) || !st16(pre.kh) || !st16(pre.vb) || !st16(pre.vh))
+    return false;
   if (k_st->t < 0 || v_st->t < 0) return false;
   if ((int64_t)Tk * k_st->t >= ((int64_t)1 << 31) || (int64_t)Tk * v_st->t >= ((int64_t)1 << 31)) return false;
   const int64_t groups = ((int64_t)B + group - 1) / group;
@@ -566,11 +575,11 @@ bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype,
 
 int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
                      const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st,
-                     void* y, const dg_stride3* y_st, float scale, int prefix_len, int group,
+                     void* y, const dg_stride3* y_st, float scale, const PrefixRef& pre,
                      const int* pos_dev, hipStream_t s) {
   DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
   SharedArgs a{};
-  fill_common(a, B, H, D, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale, prefix_len, group, pos_dev);
+  fill_common(a, B, H, D, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale, pre, pos_dev);
   if (dtype == DG_F32) return launch_shared_d<float, false, float>(a, s);
   if (dtype == DG_BF16) return launch_shared_d<bf16_t, false, bf16_t>(a, s);
   return launch_shared_d<f16_t, false, f16_t>(a, s);
@@ -579,12 +588,12 @@ int shared_attention(int B, int H, int Tk, int D, int dtype, const void* q, cons
 // The fused decode step takes what shared_attention takes, with the cache as
 // (B, max_pos, H, D) pages, plus 16-byte aligned projection rows and RoPE
 // table rows (table dtype: the data's or fp32).
-bool shared_step_applicable(int B, int H, int D, int dtype, int prefix_len, int group, int max_pos,
+bool shared_step_applicable(int B, int H, int D, int dtype, const PrefixRef& pre, int max_pos,
                             const void* q, const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                             const void* v, const dg_stride3* v_st, const void* kc, const dg_stride3* kc_st,
                             const void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
                             int fdtype, const void* y, const dg_stride3* y_st) {
-  if (!shared_attention_applicable(B, H, 1, max_pos, D, dtype, prefix_len, group, q, q_st, kc, kc_st, vc,
+  if (!shared_attention_applicable(B, H, 1, max_pos, D, dtype, pre, q, q_st, kc, kc_st, vc,
                                    vc_st, y, y_st))
     return false;
   const int64_t es = dtype == DG_F32 ? 4 : 2;
@@ -600,11 +609,11 @@ int shared_decode_step(int B, int H, int D, int dtype, const void* q, const dg_s
                        const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
                        const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs,
                        int64_t fpos, int fdtype, int pos, const int* pos_dev, int max_pos, void* y,
-                       const dg_stride3* y_st, float scale, int prefix_len, int group, int qknorm,
+                       const dg_stride3* y_st, float scale, const PrefixRef& pre, int qknorm,
                        hipStream_t s) {
   DG_REQUIRE(scale > 0.f, DG_EINVAL, "decode_step: scale must be positive (got %g)", (double)scale);
   SharedArgs a{};
-  fill_common(a, B, H, D, max_pos, q, q_st, kc, kc_st, vc, vc_st, y, y_st, scale, prefix_len, group, pos_dev);
+  fill_common(a, B, H, D, max_pos, q, q_st, kc, kc_st, vc, vc_st, y, y_st, scale, pre, pos_dev);
   a.kp = k; a.vp = v;
   a.kpb = k_st->b; a.kph = k_st->h; a.vpb = v_st->b; a.vph = v_st->h;
   a.freqs = freqs; a.fpos = fpos;

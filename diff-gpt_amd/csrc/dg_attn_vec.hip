@@ -42,8 +42,7 @@ struct AttnArgs {
   int H, Tq, Tk, D;
   int q_offset;  // Tk - Tq: query i sees keys j <= i + q_offset
   int nsplit, split_len;
-  int prefix_len;    // keys j < prefix_len of row b are read from row (b / group) * group
-  int group;
+  PrefixRef pre;     // keys j < pre.len of row b come from its group's prefix pages
   float scale_log2;  // scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2
   // Decode-step form (graph-replayable, Tq == 1): when pos_dev is set, the
@@ -105,11 +104,12 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   // wave-uniform page bases; per-lane offsets of slot u inside a trip
   const T* kbase = static_cast<const T*>(a.k) + b * a.kb + (int64_t)h * a.kh;
   const T* vbase = static_cast<const T*>(a.v) + b * a.vb + (int64_t)h * a.vh;
-  // shared prefix: keys below prefix_len come from the group's first row
-  const int64_t b0 = (b / a.group) * a.group;
-  const T* kpre = static_cast<const T*>(a.k) + b0 * a.kb + (int64_t)h * a.kh;
-  const T* vpre = static_cast<const T*>(a.v) + b0 * a.vb + (int64_t)h * a.vh;
-  const int P = a.prefix_len;
+  // shared prefix: keys below pre.len come from the group's prefix pages
+  // (same t stride as the cache); own keys are at or past it
+  const int64_t grp_of = b / a.pre.group;
+  const T* kpre = static_cast<const T*>(a.pre.k) + grp_of * a.pre.kb + (int64_t)h * a.pre.kh;
+  const T* vpre = static_cast<const T*>(a.pre.v) + grp_of * a.pre.vb + (int64_t)h * a.pre.vh;
+  const int P = a.pre.len;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
   int koff[U], voff[U];
 #pragma unroll
@@ -423,7 +423,7 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
 int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  int prefix_len, int group, const int* pos_dev, void* workspace,
+                  const PrefixRef& pre, const int* pos_dev, void* workspace,
                   size_t workspace_bytes, hipStream_t s) {
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
@@ -440,9 +440,11 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
     if (epl != 2 && dpad != D) return false;
     if (dpad / epl > 64) return false;
     const int64_t bytes = (int64_t)epl * es;
+    const bool pre_ok = pre.len == 0 || (aligned(pre.k, bytes) && aligned(pre.v, bytes) && pre.kb % epl == 0 &&
+                                         pre.kh % epl == 0 && pre.vb % epl == 0 && pre.vh % epl == 0);
     return aligned(q, bytes) && aligned(k, bytes) && aligned(v, bytes) && aligned(y, bytes) &&
            strides_multiple(q_st, epl) && strides_multiple(k_st, epl) &&
-           strides_multiple(v_st, epl) && strides_multiple(y_st, epl);
+           strides_multiple(v_st, epl) && strides_multiple(y_st, epl) && pre_ok;
   };
   int epl = 0;
   if (fits(pref)) epl = pref;
@@ -460,8 +462,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.q_offset = Tk - Tq;
   a.scale_log2 = scale * 1.44269504088896340736f;
   a.lazy_raw = kVecLazyLog2 / a.scale_log2;
-  a.prefix_len = prefix_len;
-  a.group = group;
+  a.pre = pre;
   a.pos_dev = pos_dev;
 
   int ns = vec_attention_splits(B, H, Tq, Tk, D);

@@ -368,6 +368,18 @@ __device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowR
 namespace dg {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+
+// A shared prefix (dg_prefix) as the kernels read it: keys t < len of row b
+// at k + (b / group) * kb + t * (the cache's t stride) + h * kh (likewise v).
+// The cache pointers the kernels receive are shifted so that position t >=
+// own_start of row b is at cache + b*kb_cache + t*kt + h*kh_cache; they never
+// read the cache below own_start, nor write it.  len = 0: no prefix.
+struct PrefixRef {
+  const void* k;
+  const void* v;
+  int64_t kb, kh, vb, vh;
+  int len, group, own_start;
+};
 }  // namespace dg
 
 #define DG_REQUIRE(cond, code, ...) \

@@ -62,8 +62,8 @@ extern "C" int dg_decode_step_noalloc(int B, int H, int D, int dtype, const void
                                       const dg_stride3* v_st, void* k_cache, const dg_stride3* kc_st,
                                       void* v_cache, const dg_stride3* vc_st, const void* freqs,
                                       int64_t freqs_pos_stride, int freqs_dtype, int pos, const int32_t* pos_dev,
-                                      int max_pos, void* y, const dg_stride3* y_st, float scale, int prefix_len,
-                                      int group, int flags, void* stream) {
+                                      int max_pos, void* y, const dg_stride3* y_st, float scale,
+                                      const dg_prefix* prefix, int flags, void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0 && D >= 2 && max_pos >= 1, DG_EINVAL,
              "decode_step_noalloc: bad sizes (B=%d H=%d D=%d max_pos=%d)", B, H, D, max_pos);
   const size_t need = dg_decode_step_workspace_size(B, H, max_pos, D, dtype);
@@ -89,6 +89,6 @@ extern "C" int dg_decode_step_noalloc(int B, int H, int D, int dtype, const void
   const int rc = device_scratch(dev, &ws);
   if (rc != DG_OK) return rc;
   return dg_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, k_cache, kc_st, v_cache, vc_st, freqs,
-                        freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, prefix_len, group,
-                        flags, ws, kStaticScratchBytes, stream);
+                        freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, prefix, flags, ws,
+                        kStaticScratchBytes, stream);
 }

@@ -34,9 +34,9 @@ struct RopeArgs {
   // Decode-step form (graph-replayable): when pos_dev is set, the number of
   // positions already cached is read on the device; destinations advance by
   // pstep[w] and the table by fpos elements per position.  Positions outside
-  // [0, max_pos) write nothing.
+  // [min_pos, max_pos) write nothing.
   const int* pos_dev;
-  int max_pos;
+  int min_pos, max_pos;
   int64_t pstep[3];
   int64_t fpos;
 };
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
   int64_t pos = 0;
   if (a.pos_dev != nullptr) {  // uniform over the grid
     pos = *a.pos_dev;
-    if (pos < 0 || pos >= a.max_pos) return;
+    if (pos < a.min_pos || pos >= a.max_pos) return;
   }
 
   // the host keeps B*T*H below 2^31: 32-bit division
@@ -270,7 +270,7 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
                void* q_out, const dg_stride3* qo_st, const void* k, const dg_stride3* k_st,
                void* k_out, const dg_stride3* ko_st, const void* v, const dg_stride3* v_st,
                void* v_out, const dg_stride3* vo_st, const void* freqs, const dg_stride3* f_st,
-               int freqs_dtype, int flags, const int32_t* pos_dev, int max_pos,
+               int freqs_dtype, int flags, const int32_t* pos_dev, int min_pos, int max_pos,
                const int64_t (&pstep)[3], int64_t fpos, void* stream) {
   DG_REQUIRE(B >= 0 && T >= 0 && H >= 0, DG_EINVAL, "rope: negative size");
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "rope: head_dim must be even and >= 2 (got %d)", D);
@@ -344,6 +344,7 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
   a.D = D;
   a.qknorm = (flags & DG_QKNORM) ? 1 : 0;
   a.pos_dev = pos_dev;
+  a.min_pos = min_pos;
   a.max_pos = max_pos;
   for (int w = 0; w < 3; ++w) a.pstep[w] = pstep[w];
   a.fpos = fpos;
@@ -371,8 +372,29 @@ extern "C" int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype, cons
                                      void* stream) {
   const int64_t none[3] = {0, 0, 0};
   return rope_entry(B, T, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_out, ko_st, v, v_st, v_out,
-                    vo_st, freqs, f_st, freqs_dtype, flags, nullptr, 0, none, 0, stream);
+                    vo_st, freqs, f_st, freqs_dtype, flags, nullptr, 0, 0, none, 0, stream);
 }
+
+namespace dg {
+// dg_rope_qknorm_append_at with a lower bound on the position: nothing is
+// written when *pos is outside [min_pos, max_pos) (the decode step's cache
+// pages may start at a shared prefix's end).
+int rope_append_at(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, void* q_out,
+                   const dg_stride3* qo_st, const void* k, const dg_stride3* k_st, void* k_cache,
+                   const dg_stride3* kc_st, const void* v, const dg_stride3* v_st, void* v_cache,
+                   const dg_stride3* vc_st, const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
+                   const int32_t* pos, int min_pos, int max_pos, int flags, void* stream) {
+  DG_REQUIRE(pos != nullptr, DG_EINVAL, "rope_at: NULL position pointer");
+  DG_REQUIRE(max_pos >= 1 && min_pos >= 0, DG_EINVAL, "rope_at: bad position range [%d, %d)", min_pos, max_pos);
+  DG_REQUIRE((k == nullptr || kc_st != nullptr) && (v == nullptr || vc_st != nullptr), DG_EINVAL,
+             "rope_at: missing cache strides");
+  const int64_t pstep[3] = {0, k ? kc_st->t : 0, v ? vc_st->t : 0};
+  const dg_stride3 fst = {0, 0, 0};  // one position per call, broadcast over rows and heads
+  return rope_entry(B, 1, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_cache, kc_st, v, v_st,
+                    v_cache, vc_st, freqs, &fst, freqs_dtype, flags, pos, min_pos, max_pos, pstep,
+                    freqs_pos_stride, stream);
+}
+}  // namespace dg
 
 extern "C" int dg_rope_qknorm_append_at(int B, int H, int D, int dtype, const void* q,
                                         const dg_stride3* q_st, void* q_out,
@@ -383,15 +405,8 @@ extern "C" int dg_rope_qknorm_append_at(int B, int H, int D, int dtype, const vo
                                         const dg_stride3* vc_st, const void* freqs,
                                         int64_t freqs_pos_stride, int freqs_dtype,
                                         const int32_t* pos, int max_pos, int flags, void* stream) {
-  DG_REQUIRE(pos != nullptr, DG_EINVAL, "rope_at: NULL position pointer");
-  DG_REQUIRE(max_pos >= 1, DG_EINVAL, "rope_at: max_pos must be >= 1 (got %d)", max_pos);
-  DG_REQUIRE((k == nullptr || kc_st != nullptr) && (v == nullptr || vc_st != nullptr), DG_EINVAL,
-             "rope_at: missing cache strides");
-  const int64_t pstep[3] = {0, k ? kc_st->t : 0, v ? vc_st->t : 0};
-  const dg_stride3 fst = {0, 0, 0};  // one position per call, broadcast over rows and heads
-  return rope_entry(B, 1, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_cache, kc_st, v, v_st,
-                    v_cache, vc_st, freqs, &fst, freqs_dtype, flags, pos, max_pos, pstep,
-                    freqs_pos_stride, stream);
+  return rope_append_at(B, H, D, dtype, q, q_st, q_out, qo_st, k, k_st, k_cache, kc_st, v, v_st, v_cache, vc_st,
+                        freqs, freqs_pos_stride, freqs_dtype, pos, 0, max_pos, flags, stream);
 }
 
 extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,

@@ -17,6 +17,7 @@ import ctypes
 import math
 import os
 from pathlib import Path
+from typing import NamedTuple
 
 import torch
 
@@ -37,6 +38,38 @@ class Stride3(ctypes.Structure):
     """``dg_stride3``: element strides of a (B,T,H,D) view."""
 
     _fields_ = [("b", ctypes.c_int64), ("t", ctypes.c_int64), ("h", ctypes.c_int64)]
+
+
+class DgPrefix(ctypes.Structure):
+    """``dg_prefix``: a prefix shared by groups of rows (see include/dgattn.h)."""
+
+    _fields_ = [("len", ctypes.c_int), ("group", ctypes.c_int), ("k", ctypes.c_void_p),
+                ("v", ctypes.c_void_p), ("k_st", Stride3), ("v_st", Stride3), ("own_start", ctypes.c_int)]
+
+
+class Prefix(NamedTuple):
+    """A prefix shared by groups of ``group`` consecutive rows: positions
+    0 .. length-1 of every row of a group are the group's.  k, v: the prefix
+    pages, (G, length, H, D) views (one entry per group); None when each
+    group's first row of the cache holds them.  own_start: the first position
+    the per-row cache views hold (length when the prefix lives only in k, v)."""
+
+    length: int
+    group: int
+    k: torch.Tensor | None = None
+    v: torch.Tensor | None = None
+    own_start: int = 0
+
+
+def _prefix_arg(prefix: "Prefix | None"):
+    if prefix is None or (prefix.k is None and (prefix.group <= 1 or prefix.length <= 0)):
+        return None, 0
+    p = DgPrefix()
+    p.len, p.group, p.own_start = int(prefix.length), int(prefix.group), int(prefix.own_start)
+    if prefix.k is not None:
+        p.k, p.v = prefix.k.data_ptr(), prefix.v.data_ptr()
+        p.k_st, p.v_st = _bthd_strides(prefix.k), _bthd_strides(prefix.v)
+    return ctypes.pointer(p), p.own_start
 
 
 _lib: ctypes.CDLL | None = None
@@ -61,8 +94,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int] * 6
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4
-        + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
-           ctypes.c_void_p],
+        + [ctypes.c_float, ctypes.POINTER(DgPrefix), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
     "dg_lm_head": (
         ctypes.c_int,
@@ -90,7 +122,7 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int] * 4
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 4  # q, k_cache, v_cache, y
-        + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+        + [ctypes.c_float, ctypes.POINTER(DgPrefix), ctypes.c_void_p, ctypes.c_int,
            ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
     "dg_decode_step_workspace_size": (ctypes.c_size_t, [ctypes.c_int] * 5),
@@ -99,7 +131,7 @@ _SIGNATURES = {
         [ctypes.c_int] * 4
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 5  # q, k, v, k_cache, v_cache
         + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
-        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.c_int, ctypes.c_int,
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.POINTER(DgPrefix),
            ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p],
     ),
     "dg_decode_step_noalloc_scratch_bytes": (ctypes.c_size_t, []),
@@ -108,7 +140,7 @@ _SIGNATURES = {
         [ctypes.c_int] * 4
         + [ctypes.c_void_p, ctypes.POINTER(Stride3)] * 5  # q, k, v, k_cache, v_cache
         + [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int]
-        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.c_int, ctypes.c_int,
+        + [ctypes.c_void_p, ctypes.POINTER(Stride3), ctypes.c_float, ctypes.POINTER(DgPrefix),
            ctypes.c_int, ctypes.c_void_p],
     ),
     "dg_rms_norm": (
@@ -145,7 +177,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def lib() -> ctypes.CDLL:
@@ -289,13 +321,18 @@ def rope_qknorm_append_(
 
 
 def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tensor,
-               scale: float, prefix_len: int = 0, group: int = 1) -> None:
-    """dg_attention_grouped: q,y (B,Tq,H,D) views; k,v (B,Tk,H,D) views.  With
-    group > 1 the first prefix_len keys of row b are read from row
-    (b // group) * group (rows of a group must hold identical prefixes)."""
+               scale: float, prefix_len: int = 0, group: int = 1, prefix: Prefix | None = None) -> None:
+    """dg_attention_grouped: q,y (B,Tq,H,D) views; k,v (B,Tk - own_start,H,D)
+    views of the rows' keys from position own_start on.  With group > 1 the
+    first prefix_len keys of row b are read from row (b // group) * group (rows
+    of a group must hold identical prefixes); ``prefix`` (a Prefix) names
+    separate prefix pages instead."""
+    if prefix is None:
+        prefix = Prefix(prefix_len, group)
+    parg, own_start = _prefix_arg(prefix)
     B, Tq, H, D = q.shape
-    Tk = k.size(1)
-    if k.shape != (B, Tk, H, D) or v.shape != (B, Tk, H, D) or y.shape != q.shape:
+    Tk = k.size(1) + own_start
+    if k.shape != (B, Tk - own_start, H, D) or v.shape != k.shape or y.shape != q.shape:
         raise ValueError("attention: inconsistent q/k/v/y shapes")
     if not (q.dtype == k.dtype == v.dtype == y.dtype):
         raise TypeError("attention: q/k/v/y must share one dtype")
@@ -309,7 +346,7 @@ def attention_(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, y: torch.Tenso
         _ptr(k), ctypes.pointer(_bthd_strides(k)),
         _ptr(v), ctypes.pointer(_bthd_strides(v)),
         _ptr(y), ctypes.pointer(_bthd_strides(y)),
-        float(scale), int(prefix_len), int(group), _ptr(ws), ws_bytes, _stream(q),
+        float(scale), parg, _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "attention")
 
@@ -421,9 +458,13 @@ def decode_attention_at_(
     pos: torch.Tensor,
     prefix_len: int = 0,
     group: int = 1,
+    prefix: Prefix | None = None,
 ) -> None:
     """dg_decode_attention_at: q, y (B,1,H,D); k_cache / v_cache (B,Tcap,H,D)
-    views; attends over positions 0 .. pos[0]."""
+    views from position own_start; attends over positions 0 .. pos[0]."""
+    if prefix is None:
+        prefix = Prefix(prefix_len, group)
+    parg, own_start = _prefix_arg(prefix)
     B, T, H, D = q.shape
     if T != 1 or y.shape != q.shape:
         raise ValueError("decode_attention_at: q and y must be (B, 1, H, D)")
@@ -433,13 +474,13 @@ def decode_attention_at_(
         raise TypeError("decode_attention_at: pos must be a one-element int32 tensor on q's device")
     code = _dtype_code(q)
     L = lib()
-    max_keys = k_cache.size(1)
+    max_keys = k_cache.size(1) + own_start
     ws_bytes = L.dg_decode_attention_at_workspace_size(B, H, max_keys, D, code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device) if ws_bytes else None
     st = lambda t: ctypes.pointer(_bthd_strides(t))  # noqa: E731
     rc = L.dg_decode_attention_at(
         B, H, D, code, _ptr(q), st(q), _ptr(k_cache), st(k_cache), _ptr(v_cache), st(v_cache),
-        _ptr(y), st(y), float(scale), int(prefix_len), int(group), _ptr(pos), max_keys,
+        _ptr(y), st(y), float(scale), parg, _ptr(pos), max_keys,
         _ptr(ws), ws_bytes, _stream(q),
     )
     _check(rc, "decode_attention_at")
@@ -459,6 +500,7 @@ def decode_step_(
     group: int = 1,
     qknorm: bool = True,
     noalloc: bool = False,
+    prefix: Prefix | None = None,
 ) -> None:
     """dg_decode_step: RoPE + QK-norm of the step's q, k (B,1,H,D), the K/V
     append at position p of the (B,Tcap,H,D) cache views (at position 0), and
@@ -467,13 +509,17 @@ def decode_step_(
     one-element int32 device tensor holding p, with freqs the whole contiguous
     (Tmax, D/2, 2) table.  noalloc=True calls dg_decode_step_noalloc, whose
     key-split partials live in the library's static device scratch instead of
-    a workspace allocated here."""
+    a workspace allocated here.  ``prefix`` (a Prefix) replaces prefix_len /
+    group; with own_start > 0 the cache views hold positions own_start on."""
+    if prefix is None:
+        prefix = Prefix(prefix_len, group)
+    parg, own_start = _prefix_arg(prefix)
     B, T, H, D = q.shape
     if T != 1 or k.shape != q.shape or v.shape != q.shape or y.shape != q.shape:
         raise ValueError("decode_step: q, k, v, y must be (B, 1, H, D)")
     if k_cache.dim() != 4 or k_cache.shape[0] != B or k_cache.shape[2:] != (H, D) or v_cache.shape != k_cache.shape:
         raise ValueError("decode_step: cache views must be (B, Tcap, H, D)")
-    max_pos = k_cache.size(1)
+    max_pos = k_cache.size(1) + own_start
     if isinstance(pos, torch.Tensor):
         if pos.dtype != torch.int32 or pos.numel() != 1 or pos.device != q.device:
             raise TypeError("decode_step: a device position must be a one-element int32 tensor on q's device")
@@ -492,7 +538,7 @@ def decode_step_(
         B, H, D, code, _ptr(q), st(q), _ptr(k), st(k), _ptr(v), st(v),
         _ptr(k_cache), st(k_cache), _ptr(v_cache), st(v_cache),
         _ptr(freqs), fstride, _dtype_code(freqs), pos_host, pos_ptr, max_pos,
-        _ptr(y), st(y), float(scale), int(prefix_len), int(group), DG_QKNORM if qknorm else 0,
+        _ptr(y), st(y), float(scale), parg, DG_QKNORM if qknorm else 0,
     )
     if noalloc:
         _check(L.dg_decode_step_noalloc(*args, _stream(q)), "decode_step_noalloc")

@@ -228,7 +228,7 @@ class Engine:
                     logits = logits[:, -1, :]
         finally:
             if decode is not None:
-                if cache.kv_cache.numel() * cache.kv_cache.element_size() <= _KEEP_GRAPH_BYTES:
+                if cache.nbytes() <= _KEEP_GRAPH_BYTES:
                     self._kept = (key, cache, decode)
                 else:
                     decode.close()

@@ -188,21 +188,20 @@ class MultiHeadAttention(nn.Module):
         model's whole (Tmax, D/2, 2) table; otherwise freqs is the row of the
         current position."""
         B, T, H, D = q.shape
+        cap = kv_cache.kv_shape[4]
         t0, t1 = kv_cache.ensure_window(1, k.dtype, k.device)
-        cache = kv_cache.kv_cache
-        if cache.dtype != k.dtype:
-            raise TypeError(f"KV cache holds {cache.dtype} but the layer computes in {k.dtype}")
+        # the rows' pages (B, positions, H, D) from position own_start, and the
+        # broadcast prefix (KVCache.prefill), read once per row group
+        k_cache, v_cache, prefix = kv_cache.decode_views(self.layer_idx)
+        if k_cache.dtype != k.dtype:
+            raise TypeError(f"KV cache holds {k_cache.dtype} but the layer computes in {k.dtype}")
         if kv_cache.pos_dev is not None:
-            assert cache.size(4) >= t1, "the cache must not grow inside a captured decode step"
+            assert cap >= t1, "the cache must not grow inside a captured decode step"
             pos = kv_cache.pos_dev
         else:
             pos = t0
-        k_cache = cache[self.layer_idx, 0].transpose(1, 2)  # (B, Tcap, H, D) at position 0
-        v_cache = cache[self.layer_idx, 1].transpose(1, 2)
-        # a broadcast prefix (KVCache.prefill) is read once per row group
-        prefix_len, group = (0, 1) if kv_cache.shared_prefix is None else kv_cache.shared_prefix
         y = torch.empty_like(q)
-        _native.decode_step_(q, k, v, freqs, k_cache, v_cache, y, 1.0 / math.sqrt(D), pos, prefix_len, group)
+        _native.decode_step_(q, k, v, freqs, k_cache, v_cache, y, 1.0 / math.sqrt(D), pos, prefix=prefix)
         kv_cache.advance(self.layer_idx, t1)
         y = y.view(B, T, H * D)
         _native.ops().gate_(y, g)  # y * sigmoid(g)

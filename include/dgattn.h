@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DG_ABI_VERSION 1
+#define DG_ABI_VERSION 2
 
 #if defined(__GNUC__)
 #define DG_API __attribute__((visibility("default")))
@@ -150,27 +150,55 @@ DG_API int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype,
                            void* y, const dg_stride3* y_st, float scale, void* stream);
 
 /*
- * dg_attention over a batch whose rows come in groups sharing a prefix: for
- * row b, keys j < prefix_len are read from row (b / group) * group of k and v
- * instead of row b; keys j >= prefix_len from row b itself.  This is the
- * decode attention of mha.py:65-68 over the cache that KVCache.prefill's
- * batch broadcast (kv_cache.py:77-79) leaves behind: every row of a group
- * holds the same first prefix_len positions, so the result is
- * dg_attention's, while the prefix is fetched from HBM about once per group
- * (rows of one group run on one XCD and hit its L2).  The caller guarantees
- * the identical prefixes.  group = 1 (or prefix_len = 0) is dg_attention.
+ * A prefix shared by groups of rows: KVCache.prefill's batch broadcast
+ * (kv_cache.py:77-79) gives the `group` consecutive rows of each group the
+ * same positions 0 .. len-1.  Row b belongs to group b / group.
+ *   k, v      -- the prefix's keys and values, one page set per group:
+ *                position t, head h of group g at k + g*k_st.b + t*k_st.t
+ *                + h*k_st.h (likewise v).  Their t strides must equal the
+ *                cache view's.  NULL (both): each group's first row of the
+ *                cache view holds the prefix (the broadcast cache itself).
+ *   own_start -- the first position the per-row cache view holds: with
+ *                own_start = s, position t >= s of row b is at
+ *                cache + b*st.b + (t - s)*st.t + h*st.h.  0 for a cache that
+ *                holds every position; len when the prefix is stored only in
+ *                k / v and the rows' pages start after it.  Must be 0 with
+ *                k = NULL, and at most len.
+ * A NULL dg_prefix*, len = 0, or group = 1 with k = NULL means no shared
+ * prefix.
+ */
+typedef struct dg_prefix {
+  int len;
+  int group;
+  const void* k;
+  const void* v;
+  dg_stride3 k_st;
+  dg_stride3 v_st;
+  int own_start;
+} dg_prefix;
+
+/*
+ * dg_attention over a batch whose rows come in groups sharing a prefix
+ * (dg_prefix): for row b, keys j < prefix->len come from its group's prefix
+ * pages, keys j >= len from row b's own cache pages.  This is the decode
+ * attention of mha.py:65-68 over the cache that KVCache.prefill's batch
+ * broadcast (kv_cache.py:77-79) leaves behind, with the prefix fetched from
+ * HBM about once per group (rows of one group run on one XCD and hit its L2)
+ * and, with separate prefix pages, stored once per group.  The caller
+ * guarantees that the prefix pages hold what every row of the group would.
  * Single-token decode with group >= 16, head_dim 16 or 32 and no key splits
  * runs the prefix part as a matrix product on MFMA (fp32 products for fp32
  * inputs): equal to dg_attention within the fp32 rounding of a different
  * summation order.  Other shapes give dg_attention's bits exactly.  Prefill
- * launches that take the MFMA kernel read every row's own keys.
+ * launches the MFMA kernel takes (prefix in the cache rows themselves) read
+ * every row's own keys.
  */
 DG_API int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype,
                                 const void* q, const dg_stride3* q_st,
                                 const void* k, const dg_stride3* k_st,
                                 const void* v, const dg_stride3* v_st,
                                 void* y, const dg_stride3* y_st, float scale,
-                                int prefix_len, int group,
+                                const dg_prefix* prefix,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -187,9 +215,10 @@ DG_API int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dtype,
  * the device).  Nothing is written when *pos is outside [0, max_pos).
  *
  * dg_decode_attention_at: dg_attention_grouped with Tq = 1 over the keys
- * 0 .. *pos of the cache pages (mha.py:65-68), at most max_keys of them.  Key
- * splits and the workspace (dg_decode_attention_at_workspace_size) are sized
- * for max_keys.
+ * 0 .. *pos of the cache pages (mha.py:65-68), at most max_keys of them (an
+ * absolute position bound; with prefix->own_start = s the cache views hold
+ * positions s .. max_keys-1).  Key splits and the workspace
+ * (dg_decode_attention_at_workspace_size) are sized for max_keys.
  */
 DG_API int dg_rope_qknorm_append_at(int B, int H, int D, int dtype,
                                     const void* q, const dg_stride3* q_st,
@@ -208,7 +237,7 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
                                   const void* k_cache, const dg_stride3* kc_st,
                                   const void* v_cache, const dg_stride3* vc_st,
                                   void* y, const dg_stride3* y_st, float scale,
-                                  int prefix_len, int group, const int32_t* pos, int max_keys,
+                                  const dg_prefix* prefix, const int32_t* pos, int max_keys,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -216,12 +245,13 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
  * position p (mha.py:44-56, kv_cache.py:108-109) followed by
  * dg_attention_grouped with Tq = 1 over positions 0 .. p (mha.py:65-68).
  * q, k, v are the step's projections (B,1,H,D); k_cache / v_cache the cache
- * pages at position 0 viewed as (B,max_pos,H,D); freqs the (cos, sin) row of
+ * pages viewed as (B,positions,H,D) from position prefix->own_start (0
+ * without a prefix) up to max_pos (absolute); freqs the (cos, sin) row of
  * position 0 with freqs_pos_stride elements per position (0: freqs already
  * points at position p's row); y (B,1,H,D) receives the attention output.
  * p = *pos_dev when pos_dev != NULL (graph-replayable: nothing is written when
- * *pos_dev is outside [0, max_pos)), else p = pos, which must lie in
- * [0, max_pos) and at or past prefix_len when group > 1.
+ * *pos_dev is outside [own_start, max_pos)), else p = pos, which must lie in
+ * [own_start, max_pos) and at or past the prefix's length.
  *
  * With a shared prefix (group >= 16, D 16 or 32) this is one launch: the new
  * key and value are appended and also used from registers.  The cache
@@ -242,7 +272,7 @@ DG_API int dg_decode_step(int B, int H, int D, int dtype,
                           const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
                           int pos, const int32_t* pos_dev, int max_pos,
                           void* y, const dg_stride3* y_st, float scale,
-                          int prefix_len, int group, int flags,
+                          const dg_prefix* prefix, int flags,
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
@@ -270,7 +300,7 @@ DG_API int dg_decode_step_noalloc(int B, int H, int D, int dtype,
                                   const void* freqs, int64_t freqs_pos_stride, int freqs_dtype,
                                   int pos, const int32_t* pos_dev, int max_pos,
                                   void* y, const dg_stride3* y_st, float scale,
-                                  int prefix_len, int group, int flags, void* stream);
+                                  const dg_prefix* prefix, int flags, void* stream);
 
 /*
  * Parameter-free RMSNorm over the last dim (rms_norm.py:5-7 == F.rms_norm with

@@ -58,23 +58,42 @@ def test_argument_errors_return_status_and_message():
     # rms_norm row too long
     rc = lib.dg_rms_norm(1, 10000, 0, fake, 10000, fake, 10000, nul)
     assert rc == -2
-    # grouped attention: group < 1 and a prefix longer than the keys
+    # grouped attention: group < 1, a prefix longer than the keys, own pages
+    # without prefix pages, prefix pages with another position stride
     rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake,
-                                  _s3(), 1.0, 4, 0, nul, 0, nul)
+                                  _s3(), 1.0, _prefix(4, 0), nul, 0, nul)
     assert rc == -1 and b"group" in lib.dg_last_error()
     rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake,
-                                  _s3(), 1.0, 9, 2, nul, 0, nul)
-    assert rc == -1 and b"prefix_len" in lib.dg_last_error()
+                                  _s3(), 1.0, _prefix(9, 2), nul, 0, nul)
+    assert rc == -1 and b"prefix len" in lib.dg_last_error()
+    rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(), fake, _s3(), fake, _s3(), fake,
+                                  _s3(), 1.0, _prefix(4, 2, own_start=4), nul, 0, nul)
+    assert rc == -1 and b"own_start" in lib.dg_last_error()
+    rc = lib.dg_attention_grouped(1, 1, 1, 8, 16, 0, fake, _s3(0, 16, 0), fake, _s3(0, 16, 0), fake, _s3(), fake,
+                                  _s3(), 1.0, _prefix(4, 2, pages=True, t=32), nul, 0, nul)
+    assert rc == -1 and b"position stride" in lib.dg_last_error()
     # empty work is a no-op success
     assert lib.dg_attention(0, 1, 1, 1, 16, 0, nul, _s3(), nul, _s3(), nul, _s3(), nul, _s3(),
                             1.0, nul, 0, nul) == 0
+
+
+def _prefix(length, group, own_start=0, pages=False, t=0):
+    from diff_gpt._native import DgPrefix, Stride3
+
+    p = DgPrefix()
+    p.len, p.group, p.own_start = length, group, own_start
+    if pages:
+        p.k = p.v = 0x2000
+        p.k_st = p.v_st = Stride3(0, t, 0)
+    return ctypes.pointer(p)
 
 
 def _decode_step(lib, pos, max_pos=8, prefix_len=0, group=1, dtype=0, D=16, B=1):
     fake = ctypes.c_void_p(0x1000)
     nul = ctypes.c_void_p(0)
     return lib.dg_decode_step(B, 1, D, dtype, fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(), fake, _s3(),
-                              fake, 0, 0, pos, nul, max_pos, fake, _s3(), 0.25, prefix_len, group, 1, nul, 0, nul)
+                              fake, 0, 0, pos, nul, max_pos, fake, _s3(), 0.25, _prefix(prefix_len, group), 1,
+                              nul, 0, nul)
 
 
 def test_decode_step_argument_errors():
@@ -86,7 +105,7 @@ def test_decode_step_argument_errors():
     assert _decode_step(lib, pos=8) == -1 and b"position" in lib.dg_last_error()
     assert _decode_step(lib, pos=-1) == -1 and b"position" in lib.dg_last_error()
     assert _decode_step(lib, pos=3, prefix_len=5, group=4) == -1 and b"prefix" in lib.dg_last_error()
-    assert _decode_step(lib, pos=3, prefix_len=9, group=4) == -1 and b"prefix_len" in lib.dg_last_error()
+    assert _decode_step(lib, pos=3, prefix_len=9, group=4) == -1 and b"prefix len" in lib.dg_last_error()
     assert _decode_step(lib, pos=3, dtype=7) == -2 and b"dtype" in lib.dg_last_error()
     assert _decode_step(lib, pos=3, D=15) == -1 and b"even" in lib.dg_last_error()
     assert _decode_step(lib, pos=3, max_pos=0) == -1 and b"max_pos" in lib.dg_last_error()

@@ -637,3 +637,81 @@ def test_grouped_prefix_random_shapes(dev, dtype, shape):
     ref = on.attention_f64(q.float().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy())
     err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err <= TOL[dtype], err
+
+
+# ------------------------------------------------------------------ shared prefix stored once
+
+PREFIX_PAGES = [  # (B, group, H, P, pos, D, dtype)
+    (32, 16, 4, 96, 120, 16, "f32"),    # shared kernel (MFMA prefix), configs[1] geometry
+    (48, 16, 2, 40, 40, 32, "bf16"),    # shared kernel, first decode step (no own key yet)
+    (8, 4, 2, 50, 70, 64, "bf16"),      # vector kernel with a prefix
+    (3, 1, 2, 40, 45, 32, "f32"),       # one row per group: each row's own prefix page
+    (4, 2, 8, 2000, 2100, 128, "bf16"), # vector kernel with key splits
+]
+
+
+def _split_case(dev, B, group, H, P, pos, D, dtype, seed):
+    """A broadcast cache (every row of a group holds its group's prefix) and
+    the same contents as prefix pages + own pages (positions P.. only)."""
+    cap = pos + 8
+    G = B // group
+    dense = _randn((2, B, H, cap, D), seed, dtype).to(dev)
+    dense.view(2, G, group, H, cap, D)[..., :P, :] = dense.view(2, G, group, H, cap, D)[:, :, :1, :, :P, :]
+    pages = dense.view(2, G, group, H, cap, D)[:, :, 0, :, :P, :].contiguous()  # (2, G, H, P, D)
+    own = dense[..., P:, :].contiguous()  # (2, B, H, cap - P, D)
+    return dense, pages, own
+
+
+@pytest.mark.parametrize("shape", PREFIX_PAGES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("device_pos", [False, True], ids=["host_pos", "device_pos"])
+def test_decode_step_prefix_pages_equal_broadcast_rows(dev, shape, device_pos):
+    """dg_decode_step with the prefix in pages of its own (dg_prefix k/v,
+    own_start = P) computes and writes exactly what it does on the broadcast
+    cache that holds the prefix in every row: same y bits, same appended
+    key/value, nothing written below own_start."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, group, H, P, pos, D, dtype = shape
+    dense, pages, own = _split_case(dev, B, group, H, P, pos, D, dtype, 7 + D)
+    g = torch.Generator().manual_seed(8)
+    q, k, v = (torch.randn(B, 1, H, D, generator=g).to(TDT[dtype]).to(dev) for _ in range(3))
+    table = precompute_freqs_cis(D, 2 * (pos + 8), 10000).to(dev).to(TDT[dtype])
+    if device_pos:
+        p, freqs = torch.tensor([pos], dtype=torch.int32, device=dev), table
+    else:
+        p, freqs = pos, table[pos]
+    scale = D ** -0.5
+    y0 = torch.empty_like(q)
+    _native.decode_step_(q, k, v, freqs, dense[0].transpose(1, 2), dense[1].transpose(1, 2), y0, scale, p, P, group)
+    y1 = torch.empty_like(q)
+    pre = _native.Prefix(P, group, pages[0].transpose(1, 2), pages[1].transpose(1, 2), P)
+    pages_before = pages.clone()
+    _native.decode_step_(q, k, v, freqs, own[0].transpose(1, 2), own[1].transpose(1, 2), y1, scale, p, prefix=pre)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    assert torch.equal(own, dense[..., P:, :])
+    assert torch.equal(pages, pages_before)
+
+
+@pytest.mark.parametrize("shape", PREFIX_PAGES, ids=lambda s: "x".join(map(str, s)))
+@pytest.mark.parametrize("Tq", [1, 5])
+def test_attention_prefix_pages_equal_broadcast_rows(dev, shape, Tq):
+    """dg_attention_grouped over prefix pages + own pages: the decode (Tq = 1)
+    and a 5-query chunk give the bits of the broadcast cache."""
+    from diff_gpt import _native
+
+    B, group, H, P, pos, D, dtype = shape
+    dense, pages, own = _split_case(dev, B, group, H, P, pos, D, dtype, 11 + D)
+    Tk = pos + 1
+    q = _randn((B, Tq, H, D), 12, dtype).to(dev)
+    scale = D ** -0.5
+    y0 = torch.empty_like(q)
+    _native.attention_(q, dense[0, :, :, :Tk].transpose(1, 2), dense[1, :, :, :Tk].transpose(1, 2), y0, scale,
+                       P, group)
+    y1 = torch.empty_like(q)
+    pre = _native.Prefix(P, group, pages[0].transpose(1, 2), pages[1].transpose(1, 2), P)
+    _native.attention_(q, own[0, :, :, :Tk - P].transpose(1, 2), own[1, :, :, :Tk - P].transpose(1, 2), y1, scale,
+                       prefix=pre)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)

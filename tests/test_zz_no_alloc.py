@@ -91,5 +91,5 @@ def test_noalloc_rejects_sizes_beyond_the_scratch():
     fake, nul = ctypes.c_void_p(0x1000), ctypes.c_void_p(0)
     s3 = lambda: ctypes.pointer(Stride3(0, 0, 0))  # noqa: E731
     rc = lib.dg_decode_step_noalloc(8191, 1, 256, 1, fake, s3(), fake, s3(), fake, s3(), fake, s3(), fake, s3(),
-                                    fake, 0, 1, 10, nul, 300, fake, s3(), 0.0625, 0, 1, 1, nul)
+                                    fake, 0, 1, 10, nul, 300, fake, s3(), 0.0625, None, 1, nul)
     assert rc == -4 and b"scratch" in lib.dg_last_error()
