@@ -147,17 +147,8 @@ class DiffGPT:
             use_decimal=self.use_decimal,
         )
 
-    def _generate_future_samples(
-        self,
-        df: pd.DataFrame,
-        max_new_points: int,
-        sampler: Sampler | None,
-        num_samples: int,
-    ) -> np.ndarray:
-        """(num_samples, max_new_points, n_features) future rows
-        (diff_gpt.py:179-253): one prompt prefill, all trajectories decoded
-        together by Engine.generate_batch, each decoded on the host."""
-        assert num_samples >= 1
+    def _check_budget(self, df: pd.DataFrame, max_new_points: int) -> int:
+        """The context checks of diff_gpt.py:209-214; returns the max order."""
         columns = df.shape[1]
         max_order = _max_order(self.order_of_derivative, columns, "columns")
         assert max_order <= df.shape[0], (
@@ -170,6 +161,21 @@ class DiffGPT:
             f"{columns} columns (max_order={max_order}) require {total_positions} "
             f"context positions, but block_size is {self.model.block_size}"
         )
+        return max_order
+
+    def _generate_future_samples(
+        self,
+        df: pd.DataFrame,
+        max_new_points: int,
+        sampler: Sampler | None,
+        num_samples: int,
+    ) -> np.ndarray:
+        """(num_samples, max_new_points, n_features) future rows
+        (diff_gpt.py:179-253): one prompt prefill, all trajectories decoded
+        together by Engine.generate_batch, each decoded on the host."""
+        assert num_samples >= 1
+        columns = df.shape[1]
+        self._check_budget(df, max_new_points)
         start, scale, encoded = self._encode_frame(df)
         prompt = encoded.reshape(-1).astype(np.int64).tolist()
         results, _ = Engine(model=self.model).generate_batch(
@@ -198,6 +204,72 @@ class DiffGPT:
         return self._generate_future_samples(
             df=df, max_new_points=max_new_points, sampler=sampler, num_samples=num_samples
         )
+
+    @torch.inference_mode()
+    def predict_samples_batch(
+        self,
+        dfs: "list[pd.DataFrame]",
+        max_new_points: int,
+        num_samples: int,
+        sampler: Sampler | None = None,
+        seed: int = 42,
+    ) -> np.ndarray:
+        """predict_samples for several series at once: (len(dfs),
+        num_samples, max_new_points, n_features).  The frames must share their
+        shape (the encoded prompts then share their length); their prompts are
+        prefilled together and every trajectory of every series is decoded in
+        one loop (Engine.generate_multi_batch), each series' prompt cache
+        stored once and read once per step by its trajectories.  With a greedy
+        sampler each series gets what predict_samples gives it; sampled
+        trajectories draw from one generator for all series."""
+        assert len(dfs) > 0, "dfs must be a non-empty list of frames"
+        assert len({df.shape for df in dfs}) == 1, "all frames must have the same shape"
+        columns = dfs[0].shape[1]
+        self._check_budget(dfs[0], max_new_points)
+        encoded = [self._encode_frame(df) for df in dfs]
+        prompts = [e[2].reshape(-1).astype(np.int64).tolist() for e in encoded]
+        results, _ = Engine(model=self.model).generate_multi_batch(
+            prompts, num_samples=num_samples, max_tokens=max_new_points * columns, sampler=sampler, seed=seed,
+        )
+        out = np.empty((len(dfs), num_samples, max_new_points, columns), dtype=np.float64)
+        lo, hi = dfs[0].shape[0], dfs[0].shape[0] + max_new_points
+        for r, row in enumerate(results):
+            start, scale, _ = encoded[r // num_samples]
+            values = self._decode_tokens(start, scale, np.asarray(row, dtype=np.int64).reshape(-1, columns))
+            out[r // num_samples, r % num_samples] = np.asarray(values[lo:hi], dtype=np.float64)
+        return out
+
+    @torch.inference_mode()
+    def predict_batch(
+        self,
+        dfs: "list[pd.DataFrame]",
+        future_covariates_dfs: "list[pd.DataFrame]",
+        target_columns: "list[str] | list[int]",
+        sampler: Sampler | None = None,
+    ) -> "list[pd.DataFrame]":
+        """The teacher-forced predict (diff_gpt.py:396-498) for several series
+        at once: each series' covariate columns are forced from its own known
+        future, so every series has a schedule of its own; all series decode
+        in one loop (Engine.generate_multi_batch with per-prompt schedules).
+        The frames and futures must share their shapes."""
+        assert len(dfs) == len(future_covariates_dfs) and len(dfs) > 0, (
+            "dfs and future_covariates_dfs must be non-empty lists of the same length"
+        )
+        assert len({df.shape for df in dfs}) == 1 and len({f.shape for f in future_covariates_dfs}) == 1, (
+            "all frames (and all futures) must have the same shape"
+        )
+        plans = [self._forced_plan(df, fut, target_columns) for df, fut in zip(dfs, future_covariates_dfs)]
+        n_prompt, total = plans[0][3], plans[0][4]
+        results, _ = Engine(model=self.model).generate_multi_batch(
+            [p[2][:n_prompt].tolist() for p in plans], num_samples=1, max_tokens=total - n_prompt,
+            sampler=sampler, force_schedule=[p[5] for p in plans],
+        )
+        out = []
+        for (start, scale, _, _, _, _, columns_list), row in zip(plans, results):
+            n_features = len(columns_list)
+            tokens = np.asarray(row, dtype=np.int64).reshape(-1, n_features)
+            out.append(pd.DataFrame(self._decode_tokens(start, scale, tokens), columns=columns_list))
+        return out
 
     @torch.inference_mode()
     def predict_quantiles(
@@ -251,17 +323,14 @@ class DiffGPT:
         out[max_order:] = flat.reshape(encoded.shape[0], columns)
         return pd.DataFrame(out, columns=df.columns, index=df.index)
 
-    def _predict_teacher_forced(
+    def _forced_plan(
         self,
         context_df: pd.DataFrame,
         future_covariates_df: pd.DataFrame,
         target_columns: "list[str] | list[int]",
-        sampler: Sampler | None,
-    ) -> pd.DataFrame:
-        """Sample the target columns of the future rows, force the covariate
-        columns from their known values (diff_gpt.py:396-498): the encoded
-        context is the prompt and a force_schedule holds the covariate token
-        of every future position that is not a target column."""
+    ):
+        """Encoding and force schedule of one teacher-forced forecast: (start,
+        scale, tokens, n_prompt, total_tokens, schedule, columns)."""
         columns_list = list(context_df.columns)
         assert list(future_covariates_df.columns) == columns_list, (
             "context and future must have the same columns"
@@ -300,6 +369,22 @@ class DiffGPT:
             None if (p % n_features) in targets else int(flat[p])
             for p in range(n_prompt, total_tokens)
         ]
+        return start, scale, flat, n_prompt, total_tokens, schedule, columns_list
+
+    def _predict_teacher_forced(
+        self,
+        context_df: pd.DataFrame,
+        future_covariates_df: pd.DataFrame,
+        target_columns: "list[str] | list[int]",
+        sampler: Sampler | None,
+    ) -> pd.DataFrame:
+        """Sample the target columns of the future rows, force the covariate
+        columns from their known values (diff_gpt.py:396-498): the encoded
+        context is the prompt and a force_schedule holds the covariate token
+        of every future position that is not a target column."""
+        start, scale, flat, n_prompt, total_tokens, schedule, columns_list = self._forced_plan(
+            context_df, future_covariates_df, target_columns
+        )
         results, _ = Engine(model=self.model).generate_batch(
             tokens=flat[:n_prompt].tolist(),
             num_samples=1,
@@ -307,7 +392,7 @@ class DiffGPT:
             sampler=sampler,
             force_schedule=schedule,
         )
-        tokens = np.asarray(results[0], dtype=np.int64).reshape(-1, n_features)
+        tokens = np.asarray(results[0], dtype=np.int64).reshape(-1, len(columns_list))
         return pd.DataFrame(self._decode_tokens(start, scale, tokens), columns=columns_list)
 
     # ------------------------------------------------------------------ persistence

@@ -98,3 +98,24 @@ def test_argument_checks_and_no_training(setup):
         dg.predict(df, max_new_points=100, sampler=greedy)
     with pytest.raises(NotImplementedError):
         dg.train(None)
+
+
+def test_many_series_in_one_decode_loop(setup):
+    """predict_samples_batch and predict_batch decode three series together
+    (one prefill, one decode loop, a schedule per series for the forced
+    form); greedy, so each series gets exactly what predict_samples /
+    predict give it alone -- which the tests above pin to the reference."""
+    dg, df, _, greedy, _ = setup
+    frames = [df] + [pd.DataFrame(_series(s, GOLDEN["rows"], GOLDEN["cols"]), columns=df.columns) for s in (5, 6)]
+    many = dg.predict_samples_batch(frames, max_new_points=4, num_samples=3, sampler=greedy)
+    assert many.shape == (3, 3, 4, 3)
+    assert np.array_equal(many[0], np.asarray(GOLDEN["samples"]))
+    for i, frame in enumerate(frames):
+        assert np.array_equal(many[i], dg.predict_samples(frame, max_new_points=4, num_samples=3, sampler=greedy))
+    ctxs = [f.iloc[:25].reset_index(drop=True) for f in frames]
+    futs = [f.iloc[25:].reset_index(drop=True) for f in frames]
+    forced = dg.predict_batch(ctxs, futs, target_columns=["a"], sampler=greedy)
+    assert np.array_equal(forced[0].to_numpy(), np.asarray(GOLDEN["predict_forced"]))
+    for c, f, got in zip(ctxs, futs, forced):
+        one = dg.predict(c, future_covariates_df=f, target_columns=["a"], sampler=greedy)
+        assert np.array_equal(got.to_numpy(), one.to_numpy())
