@@ -22,11 +22,16 @@ k/v projections read and appended; in shared mode the prefix rows count once
 per series.  The decode_unfused leg runs the same job as two launches per
 layer-step (RoPE/append, then attention) and reports the attention kernel
 alone (es*(2*L_kv*D + 2*D) per (row, head)).  The prefill leg (configs[2]:
-B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s with
-FLOP = 2*B*H*D*T*(T+1).  The shapes leg times decode and prefill attention
-alone at configs[3] / configs[4] shapes.  cpu_baseline = the oracle's
-torch-CPU restatement of the reference decode path on a bounded sample, on
-this host's cores.
+B=256, H=8, T=1024, D=64, bf16, RoPE + QK-norm, causal) reports TFLOP/s of
+the model's prefill kernel with FLOP = 2*B*H*D*T*(T+1).  The shapes leg times
+decode and prefill attention alone at configs[3] / configs[4] shapes; the
+jobs leg runs configs[3]'s and configs[4]'s whole decode jobs through the
+captured decode step, and both configurations end to end through
+Engine.generate_multi_batch; the engine leg runs configs[1] end to end as one
+call and as the reference's 64 per-series calls.  cpu_baseline = the
+oracle's torch-CPU restatement of the reference decode path on sampled steps
+of the job (warm-up, median of 5), on this host's cores; the prefill and
+engine legs carry baselines of their own.
 """
 
 from __future__ import annotations
@@ -145,22 +150,24 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
     rope_fn = lib.dg_rope_qknorm_append
     attn_fn = lib.dg_decode_step if fused else lib.dg_attention_grouped
 
-    def run(with_rope: bool):
-        for rope_args, attn_args in packs:
+    def run(with_rope: bool, upto: int | None = None):
+        for rope_args, attn_args in packs[:upto]:
             if with_rope and rope_args is not None and rope_fn(*rope_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
             if attn_fn(*attn_args) != 0:
                 raise RuntimeError(lib.dg_last_error().decode())
 
     with torch.cuda.stream(side):
-        for _ in range(max(1, warmup)):  # eager: loads the code objects before capture
-            run(True)
+        run(True, upto=1)  # one eager layer-step loads the code objects before capture
     torch.cuda.synchronize()
     job, attn_only = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.graph(job, stream=side):
         run(True)
     with torch.cuda.graph(attn_only, stream=side):
         run(False)
+    with torch.cuda.stream(side):
+        for _ in range(warmup):  # untimed warm-up jobs: graph replays, as the timed ones
+            job.replay()
     torch.cuda.synchronize()
     log(f"decode {dtype_name}: warmup done, timing {steps} jobs")
     with torch.cuda.stream(side):
@@ -209,13 +216,16 @@ def decode_job(dtype_name: str, steps: int, warmup: int, shared: bool = False, f
 
 def prefill_leg(reps: int = 10, traffic_json: str | None = None):
     """B=256, T=1024, H=8, D=64 bf16, q/k/v in (B,T,H,D) projection
-    layout, RoPE base 1e4 + QK-norm.  The model's step: RoPE + QK-norm of k in
-    a first launch, then dg_prefill_rope (causal attention that rotates and
-    normalises q as it loads it).  attn_ms: mean over `reps` back-to-back
-    dg_attention launches on the rotated q (one graph replay, HIP events on its
-    stream); with_rope_ms: the same for the model's two-launch step;
-    with_rope_unfused_ms: RoPE on q and k in the first launch, dg_attention in
-    the second."""
+    layout, RoPE base 1e4 + QK-norm, causal.  The model's prefill step is two
+    launches: RoPE + QK-norm of k (dg_rope_qknorm_append), then
+    dg_prefill_rope, which rotates and normalises q as it loads it and -- the
+    keys being normalised -- runs its softmax without a running maximum.
+    fused_ms: that attention kernel alone (the headline TFLOP/s and
+    roofline); with_rope_ms: the two-launch step; attn_ms: dg_attention on an
+    already rotated q (general kernel, running maximum); with_rope_unfused_ms:
+    RoPE on q and k in the first launch, dg_attention in the second.  Each is
+    a graph of `reps` back-to-back launches timed with HIP events on its
+    stream, median of 3 replays."""
     import torch
 
     from diff_gpt import _native
@@ -229,49 +239,48 @@ def prefill_leg(reps: int = 10, traffic_json: str | None = None):
     q_rot, k_rot, y = (torch.empty_like(q) for _ in range(3))
     ops = _native.ops()
     flop = 2.0 * B * H * D * T * (T + 1)
+    scale = 1.0 / D**0.5
 
-    def step(with_rope):
-        if with_rope == "fused":
-            ops.rope_qknorm_append(None, k, None, fc, None, k_rot, None, True)
-            if not _native.prefill_rope_(q, fc, k_rot, v, y, 1.0 / D**0.5, True):
-                raise RuntimeError("configs[2] prefill is not taken by dg_prefill_rope")
-            return
-        if with_rope:
-            ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
-        _native.attention_(q_rot, k_rot, v, y, 1.0 / D**0.5)
+    def fused_kernel():
+        if not _native.prefill_rope_(q, fc, k_rot, v, y, scale, True, keys_normed=True):
+            raise RuntimeError("configs[2] prefill is not taken by dg_prefill_rope")
 
-    # reps back-to-back steps captured in a graph (as the decode job), and the
-    # attention launches alone; each timed over 3 replays with events
+    def model_step():
+        ops.rope_qknorm_append(None, k, None, fc, None, k_rot, None, True)
+        fused_kernel()
+
+    def unfused_step():
+        ops.rope_qknorm_append(q, k, None, fc, q_rot, k_rot, None, True)
+        _native.attention_(q_rot, k_rot, v, y, scale)
+
+    def attn_alone():
+        _native.attention_(q_rot, k_rot, v, y, scale)
+
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        step(True)
-        step("fused")
+        unfused_step()
+        model_step()
     torch.cuda.synchronize()
-    full, attn_only, fused = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
-    with torch.cuda.graph(full, stream=side):
-        for _ in range(reps):
-            step(True)
-    with torch.cuda.graph(attn_only, stream=side):
-        for _ in range(reps):
-            step(False)
-    with torch.cuda.graph(fused, stream=side):
-        for _ in range(reps):
-            step("fused")
-    times, attn, fused_t = [], [], []
+    legs = {"fused": fused_kernel, "model": model_step, "unfused": unfused_step, "attn": attn_alone}
+    graphs = {}
+    for name, fn in legs.items():
+        graphs[name] = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graphs[name], stream=side):
+            for _ in range(reps):
+                fn()
+    times = {name: [] for name in legs}
     with torch.cuda.stream(side):
         for _ in range(3):
-            for graph, out in ((full, times), (attn_only, attn), (fused, fused_t)):
+            for name, graph in graphs.items():
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record(side)
                 graph.replay()
                 b.record(side)
                 torch.cuda.synchronize()
-                out.append(a.elapsed_time(b) / 1e3 / reps)
-    t_attn = sorted(attn)[len(attn) // 2]
-    t_all = sorted(times)[len(times) // 2]
-    t_fused = sorted(fused_t)[len(fused_t) // 2]
-    tf = flop / t_attn / 1e12
+                times[name].append(a.elapsed_time(b) / 1e3 / reps)
+    t = {name: sorted(v)[1] for name, v in times.items()}
+    tf = flop / t["fused"] / 1e12
     # HBM bytes per attention launch, from the committed rocprofv3 counter runs
     traffic = None
     if traffic_json and Path(traffic_json).exists():
@@ -279,13 +288,68 @@ def prefill_leg(reps: int = 10, traffic_json: str | None = None):
     return {
         "workload": "configs[2] causal prefill B=256 H=8 T=1024 D=64 bf16, RoPE+QK-norm",
         "tflops": tf,
-        "attn_ms": t_attn * 1e3,
-        "with_rope_ms": t_fused * 1e3,
-        "tflops_with_rope": flop / t_fused / 1e12,
-        "with_rope_unfused_ms": t_all * 1e3,
+        "fused_ms": t["fused"] * 1e3,
+        "with_rope_ms": t["model"] * 1e3,
+        "tflops_with_rope": flop / t["model"] / 1e12,
+        "attn_ms": t["attn"] * 1e3,
+        "attn_tflops": flop / t["attn"] / 1e12,
+        "with_rope_unfused_ms": t["unfused"] * 1e3,
         "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS, "traffic": traffic},
     }
+
+
+def prefill_cpu_baseline(batch: int = 8, runs: int = 5):
+    """configs[2] on the host cores: the reference's prefill attention path
+    (rope.py, rms_norm.py at mha.py:48, SDPA with is_causal, mha.py:44-64) in
+    torch on the CPU, bf16, at B = `batch` of the 256 sequences; one warm-up,
+    then the median of `runs`; TFLOP/s over the same FLOP count, time
+    extrapolated linearly to B = 256 (rows are independent)."""
+    import torch
+
+    from oracle import torch_ref as tr
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    T, H, D = 1024, 8, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn((batch, T, H, D), generator=g).to(torch.bfloat16) for _ in range(3))
+    fc = tr.freqs_table(D, 2 * T, 10000).to(torch.bfloat16)[:T].view(1, T, 1, D // 2, 2)
+
+    def run():
+        qq, kk = tr.rms(tr.rope(q, fc)), tr.rms(tr.rope(k, fc))
+        return tr.sdpa(qq.transpose(1, 2), kk.transpose(1, 2), v.transpose(1, 2))
+
+    with torch.no_grad():
+        run()
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            run()
+            ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
+    flop = 2.0 * batch * H * D * T * (T + 1)
+    return {
+        "value": flop / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "cpu": cpu_model(),
+        "kind": "port",
+        "sample": f"configs[2] prefill (RoPE + QK-norm + causal SDPA, bf16) at B={batch} of 256, "
+                  f"median of {runs} after a warm-up; {med * 1e3:.1f} ms, extrapolated to "
+                  f"{med * 256 / batch * 1e3:.0f} ms for B=256 (linear in B)",
+    }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def shapes_leg(reps: int = 20):
@@ -344,15 +408,27 @@ def shapes_leg(reps: int = 20):
                         "frac": nbytes / t / 1e9 / HBM_PEAK_GBS})
             log(f"shapes: {out[-1]}")
         del cache, q, y
+    from diff_gpt.model.rope import precompute_freqs_cis
+
     for name, B, H, D, T in (("configs[3]", 512, 8, 64, 1024), ("configs[4]", 64, 8, 128, 3584)):
         q, k, v = (torch.randn((B, T, H, D), generator=g, device=dev).to(dt) for _ in range(3))
+        fc = precompute_freqs_cis(D, 2 * T, 10000).to(dev).to(dt)[:T].view(1, T, 1, D // 2, 2)
+        k_rot = torch.empty_like(k)
+        _native.ops().rope_qknorm_append(None, k, None, fc, None, k_rot, None, True)
         y = torch.empty_like(q)
-        t = timed(lambda: _native.attention_(q, k, v, y, D ** -0.5))
-        tf = 2.0 * B * H * D * T * (T + 1) / t / 1e12
-        out.append({"workload": f"{name} causal prefill attention B={B} H={H} T={T} D={D} bf16",
-                    "ms": t * 1e3, "tflops": tf, "frac": tf / BF16_PEAK_TFLOPS})
+        flop = 2.0 * B * H * D * T * (T + 1)
+        # the model's prefill kernel: q rotated and normalised as it is
+        # loaded, normalised keys, bounded softmax
+        t = timed(lambda: _native.prefill_rope_(q, fc, k_rot, v, y, D ** -0.5, True, keys_normed=True))
+        # the general kernel (any q, k: running maximum)
+        t_gen = timed(lambda: _native.attention_(q, k, v, y, D ** -0.5))
+        tf = flop / t / 1e12
+        out.append({"workload": f"{name} causal prefill attention B={B} H={H} T={T} D={D} bf16, "
+                                "q RoPE + QK-norm fused, bounded softmax (the model's kernel)",
+                    "ms": t * 1e3, "tflops": tf, "frac": tf / BF16_PEAK_TFLOPS,
+                    "general_kernel_tflops": flop / t_gen / 1e12})
         log(f"shapes: {out[-1]}")
-        del q, k, v, y
+        del q, k, v, y, k_rot
     # configs[0] and configs[1] prefill (D = 16, fp32): launch-bound, so the
     # figure is latency per launch, with no roofline
     for name, B in (("configs[0]", 32), ("configs[1] per series", 1)):
@@ -364,6 +440,125 @@ def shapes_leg(reps: int = 20):
                     "us": t * 1e6, "bound": "latency"})
         log(f"shapes: {out[-1]}")
         del q, k, v, y
+    return out
+
+
+DECODE_JOBS = {  # name: (rows, heads, head_dim, layers, prompt length, decode steps)
+    "configs[3]": (512, 8, 64, 8, 1024, 512),
+    "configs[4]": (64, 8, 128, 4, 3584, 96),
+}
+
+
+def decode_job_leg(name: str, reps: int = 2):
+    """A whole decode job of configs[3] / configs[4] through the decode-step
+    entry point, bf16: the cache (L,2,B,H,capacity,D) holds the prompt's
+    keys and values, then every step appends one position per row and
+    attends over all of them, layer by layer (dg_decode_step: RoPE + QK-norm
+    + append + decode attention with key splits), on synthetic projections
+    resident in HBM.  The step is captured once with the position read on the
+    device (as the Engine replays it) and replayed for every step of the job.
+    Bytes per (row, head, step) = es*(2*L_kv*D + 4*D) (every visible position's
+    K and V, q, y, the new k and v read and appended)."""
+    import torch
+
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, D, L, T0, steps = DECODE_JOBS[name]
+    dev = torch.device("cuda:0")
+    dt, es = torch.bfloat16, 2
+    cap = T0 + steps
+    g = torch.Generator(device=dev).manual_seed(0)
+    cache = torch.empty((L, 2, B, H, cap, D), dtype=dt, device=dev)
+    for layer in range(L):
+        cache[layer, :, :, :, :T0] = torch.randn((2, B, H, T0, D), generator=g, device=dev).to(dt)
+    proj = torch.randn((L, 3, B, 1, H, D), generator=g, device=dev).to(dt)
+    table = precompute_freqs_cis(D, 2 * cap, 10000).to(dev).to(dt)
+    pos = torch.full((1,), T0, dtype=torch.int32, device=dev)
+    y = torch.empty((B, 1, H, D), dtype=dt, device=dev)
+
+    def step():
+        for layer in range(L):
+            q, k, v = proj[layer]
+            _native.decode_step_(q, k, v, table, cache[layer, 0].transpose(1, 2), cache[layer, 1].transpose(1, 2),
+                                 y, D ** -0.5, pos)
+        pos.add_(1)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        step()
+    times = []
+    with torch.cuda.stream(side):
+        for _ in range(reps):
+            pos.fill_(T0)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(side)
+            for _ in range(steps):
+                graph.replay()
+            b.record(side)
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / 1e3)
+    t = min(times)
+    nbytes = sum(B * H * es * (2 * (T0 + s + 1) * D + 4 * D) for s in range(steps)) * L
+    out = {"workload": f"{name} decode job: B={B} H={H} D={D} {L} layers, {steps} steps, "
+                       f"L_kv {T0 + 1}..{cap}, bf16, dg_decode_step per layer-step (captured)",
+           "tokens_per_s": B * steps / t, "seconds": t, "bytes": nbytes,
+           "achieved_gbs": nbytes / t / 1e9, "frac": nbytes / t / 1e9 / HBM_PEAK_GBS}
+    del cache, proj
+    return out
+
+
+def engine_multi_leg(name: str):
+    """A configuration end to end through Engine.generate_multi_batch (the
+    whole model, prefill included, random-init weights, bf16):
+    configs[3] -- 512 prompts of 1024 uniform ids, 512 greedy steps;
+    configs[4] -- 64 prompts of 3584 ids (7 channels x 512 steps), 96 steps
+    with a schedule per prompt forcing channels 0, 1 and 2 from seeded
+    uniform ids, greedy elsewhere.  One warm-up call (captures the decode
+    step), then one timed call."""
+    import numpy as np
+    import torch
+
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    dev = torch.device("cuda:0")
+    if name == "configs[3]":
+        C, H, L, n, T, steps = 512, 8, 8, 512, 1024, 512
+    else:
+        C, H, L, n, T, steps = 1024, 8, 4, 64, 3584, 96
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=C, block_size=2048, n_head=H, n_layer=L,
+                use_checkpoint=False).eval().to(dev).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(1)
+    prompts = torch.randint(0, 256, (n, T), generator=g).tolist()
+    sched = None
+    if name == "configs[4]":
+        rng = np.random.default_rng(2)
+        sched = [[int(rng.integers(0, 256)) if (T + s) % 7 in (0, 1, 2) else None for s in range(steps)]
+                 for _ in range(n)]
+    engine = Engine(model)
+    greedy = TemperatureSampler(0.0)
+    kw = dict(num_samples=1, max_tokens=steps, sampler=greedy, force_schedule=sched)
+    engine.generate_multi_batch(prompts, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    results, _ = engine.generate_multi_batch(prompts, **kw)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    assert len(results) == n and len(results[0]) == T + steps
+    out = {"workload": f"{name} end to end through Engine.generate_multi_batch: GPT(n_embd={C}, n_head={H}, "
+                       f"n_layer={L}) bf16, {n} prompts x {T} tokens, {steps} decode steps"
+                       + (", force_schedule per prompt (channels 0-2 of 7)" if sched else ", greedy"),
+           "seconds": el, "generated_tokens_per_s": n * steps / el}
+    del model, engine
+    torch.cuda.empty_cache()
     return out
 
 
@@ -397,28 +592,33 @@ def engine_leg(dtype_name: str):
         engine.generate_batch(prompt, num_samples=TRAJ, max_tokens=NEW, sampler=sampler, seed=s)
     torch.cuda.synchronize()
     per_series = time.perf_counter() - t0
-    engine.generate_batch(prompts[0], num_samples=SERIES * TRAJ, max_tokens=NEW, sampler=sampler)
+    # the whole job as one call: 64 prompts x 100 trajectories, one decode loop
+    engine.generate_multi_batch(prompts, num_samples=TRAJ, max_tokens=NEW, sampler=sampler)  # capture
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    engine.generate_batch(prompts[0], num_samples=SERIES * TRAJ, max_tokens=NEW, sampler=sampler)
+    engine.generate_multi_batch(prompts, num_samples=TRAJ, max_tokens=NEW, sampler=sampler)
     torch.cuda.synchronize()
-    batched = time.perf_counter() - t0
+    multi = time.perf_counter() - t0
     tokens = SERIES * TRAJ * NEW
     return {
-        "workload": "configs[1] through Engine.generate_batch: 64 calls x 100 trajectories, "
-                    "96-token prompt, 48 temperature-1 steps, README GPT (2 layers, d64, h4)",
+        "workload": "configs[1] through the Engine: 64 series x 100 trajectories, 96-token prompts, "
+                    "48 temperature-1 steps, README GPT (2 layers, d64, h4); tokens_per_s: one "
+                    "generate_multi_batch call (one prefill of the 64 prompts, one decode loop over the "
+                    "6400 rows, each series' prompt cache stored once)",
         "dtype": dtype_name,
-        "tokens_per_s": tokens / per_series,
-        "seconds": per_series,
-        "one_call_6400_rows_tokens_per_s": tokens / batched,
+        "tokens_per_s": tokens / multi,
+        "seconds": multi,
+        "per_series_calls_tokens_per_s": tokens / per_series,
+        "per_series_calls_seconds": per_series,
     }
 
 
-def engine_cpu_baseline(dtype_name: str, budget_s: float = 10.0):
-    """The reference's engine pattern on the host cores (oracle.torch_ref): per
-    series a batch-1 prefill, the cache broadcast to 100 rows, 48 steps of
-    softmax + multinomial and a 100-row forward -- for as many series as fit
-    the budget."""
+def engine_cpu_baseline(dtype_name: str, runs: int = 5):
+    """The reference's engine pattern on the host cores (oracle.torch_ref) for
+    one configs[1] series: a batch-1 prefill, the cache broadcast to 100 rows,
+    48 steps of softmax + multinomial and a 100-row forward.  One warm-up
+    series, then `runs` series; tokens/s from the median series time (the 64
+    series of the job cost the same)."""
     import torch
 
     from diff_gpt.model.gpt import GPT
@@ -433,36 +633,45 @@ def engine_cpu_baseline(dtype_name: str, budget_s: float = 10.0):
     cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=138, n_head=HEADS, n_layer=LAYERS)
     table = tr.freqs_table(HEAD_DIM, 2 * 138, 10000)
     g = torch.Generator().manual_seed(1)
-    done, t0 = 0, time.perf_counter()
+
+    def series(seed):
+        prompt = torch.randint(0, 256, (1, PREFIX), generator=g)
+        pc = tr.RefCache(1, HEADS, PREFIX, HEAD_DIM, LAYERS)
+        logits = tr.forward(p, cfg, prompt, pc, table)[:, -1].expand(TRAJ, -1)
+        cache = tr.RefCache(TRAJ, HEADS, PREFIX + NEW, HEAD_DIM, LAYERS)
+        cache.broadcast_from(pc)
+        rng = torch.Generator().manual_seed(seed)
+        for _ in range(NEW):
+            nxt = torch.multinomial(torch.softmax(logits.float(), -1), 1, generator=rng)
+            logits = tr.forward(p, cfg, nxt, cache, table)[:, -1]
+
+    ts = []
     with torch.no_grad():
-        while done < SERIES:
-            prompt = torch.randint(0, 256, (1, PREFIX), generator=g)
-            pc = tr.RefCache(1, HEADS, PREFIX, HEAD_DIM, LAYERS)
-            logits = tr.forward(p, cfg, prompt, pc, table)[:, -1].expand(TRAJ, -1)
-            cache = tr.RefCache(TRAJ, HEADS, PREFIX + NEW, HEAD_DIM, LAYERS)
-            cache.broadcast_from(pc)
-            rng = torch.Generator().manual_seed(done)
-            for _ in range(NEW):
-                nxt = torch.multinomial(torch.softmax(logits.float(), -1), 1, generator=rng)
-                logits = tr.forward(p, cfg, nxt, cache, table)[:, -1]
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-    el = time.perf_counter() - t0
+        series(0)
+        for s in range(runs):
+            t0 = time.perf_counter()
+            series(s + 1)
+            ts.append(time.perf_counter() - t0)
+    med = sorted(ts)[len(ts) // 2]
     return {
-        "value": done * TRAJ * NEW / el,
+        "value": TRAJ * NEW / med,
         "unit": "tokens/s",
         "cores": threads,
+        "cpu": cpu_model(),
         "kind": "port",
-        "sample": f"{done} of 64 series (100 trajectories x 48 steps each), {dtype_name}, "
-                  "oracle.torch_ref model on the host cores",
+        "sample": f"{runs} configs[1] series after a warm-up (100 trajectories x 48 steps each), {dtype_name}, "
+                  f"oracle.torch_ref model on the host cores; median {med:.2f} s per series",
     }
 
 
-def cpu_baseline(dtype_name: str, budget_s: float = 12.0):
+def cpu_baseline(dtype_name: str, runs: int = 5):
     """The oracle's torch-CPU restatement of the reference decode path
     (rope.py, rms_norm.py, kv_cache.py insert, mha.py:68 SDPA) on the same
-    configs[1] shapes, for as many of the 48 decode steps as fit the budget."""
+    configs[1] shapes -- 6400 rows, both layers -- at decode steps spread over
+    the job (L_kv 97 .. 144): one warm-up step, then each sampled step `runs`
+    times; per sampled step the median; tokens/s = 6400 / mean of the
+    medians (the job's steps cost about linearly in L_kv, so the sampled mean
+    stands for the job's)."""
     import torch
 
     from oracle import torch_ref as tr
@@ -472,30 +681,43 @@ def cpu_baseline(dtype_name: str, budget_s: float = 12.0):
     dt = {"fp32": torch.float32, "bf16": torch.bfloat16}[dtype_name]
     B, H, D, L = SERIES * TRAJ, HEADS, HEAD_DIM, LAYERS
     g = torch.Generator().manual_seed(0)
-    cache = tr.RefCache(B, H, PREFIX + NEW, D, L)
-    cache.data = torch.randn((L, 2, B, H, PREFIX + NEW, D), generator=g).to(dt)
-    cache.pos = PREFIX
+    data = torch.randn((L, 2, B, H, PREFIX + NEW, D), generator=g).to(dt)
     table = tr.freqs_table(D, 2 * 138, 10000).to(dt)
-    done, t0 = 0, time.perf_counter()
+    proj = [(torch.randn((B, 1, H, D), generator=g).to(dt) for _ in range(3)) for _ in range(L)]
+    proj = [tuple(p) for p in proj]
+
+    def step(s):
+        cache = tr.RefCache(B, H, PREFIX + NEW, D, L)
+        cache.data = data
+        cache.pos = PREFIX + s
+        fc = table[PREFIX + s:PREFIX + s + 1].view(1, 1, 1, -1, 2)
+        for layer in range(L):
+            q, k, v = proj[layer]
+            q, k = tr.rms(tr.rope(q, fc)), tr.rms(tr.rope(k, fc))
+            kk, vv = cache.insert(layer, k.transpose(1, 2), v.transpose(1, 2))
+            tr.sdpa(q.transpose(1, 2), kk, vv).transpose(1, 2).contiguous()
+
+    sampled = [0, 12, 24, 36, 47]
+    meds = []
     with torch.no_grad():
-        for s in range(NEW):
-            fc = table[PREFIX + s:PREFIX + s + 1].view(1, 1, 1, -1, 2)
-            for layer in range(L):
-                q, k, v = (torch.randn((B, 1, H, D), generator=g).to(dt) for _ in range(3))
-                q, k = tr.rms(tr.rope(q, fc)), tr.rms(tr.rope(k, fc))
-                kk, vv = cache.insert(layer, k.transpose(1, 2), v.transpose(1, 2))
-                tr.sdpa(q.transpose(1, 2), kk, vv).transpose(1, 2).contiguous()
-            done += 1
-            if time.perf_counter() - t0 > budget_s:
-                break
-    el = time.perf_counter() - t0
+        step(0)
+        for s in sampled:
+            ts = []
+            for _ in range(runs):
+                t0 = time.perf_counter()
+                step(s)
+                ts.append(time.perf_counter() - t0)
+            meds.append(sorted(ts)[len(ts) // 2])
+    per_step = sum(meds) / len(meds)
     return {
-        "value": B * done / el,
+        "value": B / per_step,
         "unit": "tokens/s",
         "cores": threads,
+        "cpu": cpu_model(),
         "kind": "port",
-        "sample": f"configs[1] {dtype_name}: decode steps 1..{done} of 48 (both layers, 6400 seqs), "
-                  "torch CPU restatement (oracle.torch_ref)",
+        "sample": f"configs[1] {dtype_name}: decode steps {sampled} of 48 (both layers, 6400 seqs), "
+                  f"median of {runs} per step after a warm-up, torch CPU restatement (oracle.torch_ref); "
+                  f"{per_step * 1e3:.1f} ms per step",
     }
 
 
@@ -533,6 +755,8 @@ def main():
     ap.add_argument("--single-mode", action="store_true", help="skip the other decode-mode leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--no-jobs", action="store_true",
+                    help="skip the configs[3] / configs[4] whole-job legs (decode jobs and end-to-end Engine)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (no multi-GPU path); run with --gpus 1",
@@ -580,7 +804,19 @@ def main():
     prefill = None if args.no_prefill else prefill_leg(traffic_json=args.traffic_json)
     if prefill:
         log(f"prefill: {prefill}")
+        if not args.no_cpu_baseline:
+            prefill["cpu_baseline"] = prefill_cpu_baseline()
+            log(f"prefill cpu: {prefill['cpu_baseline']}")
     shapes = None if args.no_shapes else shapes_leg()
+    jobs = None
+    if not args.no_jobs:
+        jobs = []
+        for name in DECODE_JOBS:
+            jobs.append(decode_job_leg(name))
+            log(f"job: {jobs[-1]}")
+        for name in DECODE_JOBS:
+            jobs.append(engine_multi_leg(name))
+            log(f"job: {jobs[-1]}")
     engine = None if args.no_engine else engine_leg(args.dtype)
     if engine:
         log(f"engine: {engine}")
@@ -630,6 +866,7 @@ def main():
             "frac": res_other["achieved_gbs"] / HBM_PEAK_GBS},
         "prefill": prefill,
         "shapes": shapes,
+        "jobs": jobs,
         "engine": engine,
     }
     print(json.dumps(out), flush=True)
