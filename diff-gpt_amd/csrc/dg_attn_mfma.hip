@@ -233,26 +233,12 @@ __device__ __forceinline__ int piece_swz(int r) {
 #ifndef DG_PREFILL_BUFFER_DMA
 #define DG_PREFILL_BUFFER_DMA 1
 #endif
-// Third dword of a raw buffer resource on gfx9-family chips (gfx950 included):
-// 32-bit data format, no swizzle, no stride.
-constexpr int kBufferWord3 = 0x00020000;
 
-// 16 bytes per lane from global memory straight into LDS: lane l of the wave
-// writes lds + 16*l (lds wave-uniform), no registers involved
-__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
 // The same through a buffer resource: 16 bytes per lane from byte offset
 // voff + soff of the resource (zeros past its range) into lds + 16*l.  The
 // address-space cast stays inside this device function.
 __device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, void* lds) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
-}
-// ds_read_b64_tr_b16: within each 16 lanes, lane t receives element t & 3 of
-// the 8-byte chunks addressed by lanes t/4, 4 + t/4, 8 + t/4, 12 + t/4
-__device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
-  const i16x4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)lds);
-  return __builtin_bit_cast(uint2, r);
 }
 
 // Resident workgroups per CU the register allocation must allow: D = 64 fits

@@ -145,6 +145,49 @@ __device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
   }
 }
 
+// O^T += V^T P^T over one 16-key tile on the 16-bit matrix cores
+// (v_mfma_f32_16x16x16_{bf16,f16}): lane (c, g) feeds va[t] = V[4g + i][16t + c]
+// and P[c][4g + i], i = 0..3 -- the four scores it holds after the S^T product.
+// P is split as hi + lo, both rounded to T (lo = the rounding error of hi), so
+// the two products carry about twice T's mantissa of each probability; the
+// values are exact in T and every product is accumulated in fp32.
+template <typename T, int DT>
+__device__ __forceinline__ void pv_mfma16(const uint32_t (&va)[DT][2], const f32x4_t& p, f32x4_t (&oacc)[DT]) {
+  uint32_t hi[2], lo[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    if constexpr (__is_same(T, bf16_t)) {
+      // pairs through v_cvt_pk_bf16_f32 (round to nearest even); p - hi is
+      // exact in fp32
+      typedef float f2_t __attribute__((ext_vector_type(2)));
+      typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+      const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{p[2 * w], p[2 * w + 1]}, b2_t));
+      const f2_t r{p[2 * w] - __uint_as_float(h << 16), p[2 * w + 1] - __uint_as_float(h & 0xffff0000u)};
+      hi[w] = h;
+      lo[w] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, b2_t));
+    } else {
+      const T h0 = from_f32<T>(p[2 * w]), h1 = from_f32<T>(p[2 * w + 1]);
+      const T l0 = from_f32<T>(p[2 * w] - to_f32(h0)), l1 = from_f32<T>(p[2 * w + 1] - to_f32(h1));
+      hi[w] = (uint32_t)h0.bits | ((uint32_t)h1.bits << 16);
+      lo[w] = (uint32_t)l0.bits | ((uint32_t)l1.bits << 16);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    if constexpr (__is_same(T, bf16_t)) {
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, va[t]),
+                                                          __builtin_bit_cast(i16x4_t, hi), oacc[t], 0, 0, 0);
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4_t, va[t]),
+                                                          __builtin_bit_cast(i16x4_t, lo), oacc[t], 0, 0, 0);
+    } else {
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, va[t]),
+                                                      __builtin_bit_cast(f16x4_t, hi), oacc[t], 0, 0, 0);
+      oacc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, va[t]),
+                                                      __builtin_bit_cast(f16x4_t, lo), oacc[t], 0, 0, 0);
+    }
+  }
+}
+
 // Two wavefronts per work unit, running at the same time: wave 0 takes the
 // prefix on the matrix cores, wave 1 streams the rows' own keys on the vector
 // ALUs from the start of the launch, so the prefix phase (latency-bound: a few
@@ -162,10 +205,16 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   constexpr int LPK = O::LPK, KPQ = O::KPQ, EPL = O::EPL;
   using Op = RowRegs<T, DQ>;
   using Slice = RowRegs<T, EPL>;
-  constexpr int UO = 16 / Slice::WORDS;  // key slots per register set: two sets of K+V = 64 VGPRs
+  constexpr int UO = 16 / Slice::WORDS;  // key slots per register set (K + V: 32 VGPRs)
   constexpr int STEP = UO * KPQ;         // keys per row and register set
-  constexpr int RS = D + 4;              // floats per row of the hand-over buffer (16-byte rows)
-  __shared__ __attribute__((aligned(16))) float part[16 * RS];
+  constexpr int NSW = 2;                 // register sets of own keys in flight (64 VGPRs)
+  constexpr int RS = D + 4;              // floats per row of a hand-over buffer (16-byte rows)
+  constexpr int NCB = D == 16 ? 2 : 1;   // prefix chunk buffers
+  constexpr bool VLDS = sizeof(T) == 2;  // prefix values staged in LDS, read transposed
+  constexpr int NTV = VLDS ? 1 : NT;     // fp32: values gathered into registers per key tile
+  using VRow = RowRegs<T, D>;            // a whole value row
+  __shared__ __attribute__((aligned(16))) float part[16 * RS];  // wave 1's partial
+  __shared__ __attribute__((aligned(16))) uint16_t vst[VLDS ? NCB * 64 * D : 8];
 
   const int lane = threadIdx.x & 63;
   const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 0: prefix, 1: own keys
@@ -189,19 +238,17 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
 
   // keys 0 .. Tk-1; the fused step appends key Tk-1 = pos and takes it from
   // registers, so the cache is read for keys below Tc only
-  int Tk, Tc;
+  int Tc;
   if constexpr (FUSED) {
     const int pos = a.pos_dev != nullptr ? *a.pos_dev : a.pos;
     // uniform over the grid; the append goes to the rows' own pages
     if (pos < a.pre.own_start || pos >= a.max_pos) return;
-    Tk = pos + 1;
     Tc = pos;
   } else {
-    Tk = a.Tk;
+    int Tk = a.Tk;
     if (a.pos_dev != nullptr) Tk = min(*a.pos_dev + 1, a.Tk);
     Tc = Tk;
   }
-  (void)Tk;
   const int P = min(a.pre.len, Tc);
   const float cl = a.scale_log2;
   const int kt = (int)a.kt, vt = (int)a.vt;  // host: Tk * stride < 2^31
@@ -209,7 +256,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)h * a.vh;
   const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * a.qh;
 
-  // --- query rows in the quad layout: a quad of lanes holds one tile row -----
+  // --- quad layout (own keys): a quad of lanes holds one tile row ------------
   const int orow = lane >> 2, kk = (lane & 3) / LPK, piece = (lane & 3) % LPK;
   bool ovalid;
   const int64_t bo = row_of(orow, ovalid);
@@ -222,7 +269,114 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   };
   const FT* fbase = FUSED ? static_cast<const FT*>(a.freqs) + (int64_t)Tc * a.fpos + piece * EPL : nullptr;
 
-  // wave 0's state, merged after the hand-over
+  // --- own keys P .. Tc-1 (wave 1), in sets of STEP keys per row: set i
+  // holds keys P + i*STEP ...  Loads go through buffer resources on the
+  // head's K and V pages with one 32-bit byte offset for both (the host takes
+  // this kernel only when the pages share their row and position strides and
+  // every offset is below 2^31): key j of the lane's row at rowoff + j * ktb.
+  // A key lane at or past Tc gets an offset past the resource's range, which
+  // reads zeros without touching memory, so every set issues the same loads
+  // on every path (the compiler's wait counts stay exact) and no masked key
+  // reads uninitialised memory.
+  constexpr uint32_t kOobOffset = 0x80000000u;  // past the 2^31 - 1 byte range, no wrap-around
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kbase), (short)0, 0x7fffffff, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vbase), (short)0, 0x7fffffff, kBufferWord3);
+  const uint32_t ktb = (uint32_t)kt * (uint32_t)sizeof(T);
+  const uint32_t rowoff = (uint32_t)(bo * a.kb + piece * EPL) * (uint32_t)sizeof(T);
+  auto load_kv = [&](Slice& kr, Slice& vr, int jb) __attribute__((always_inline)) {
+    const int j = jb + kk;  // jb wave-uniform
+    const uint32_t off = j < Tc ? rowoff + (uint32_t)j * ktb : kOobOffset;
+    static_assert(Slice::WORDS % 4 == 0, "own-key slices are whole 16-byte pieces");
+#pragma unroll
+    for (int c4 = 0; c4 < Slice::WORDS / 4; ++c4) {
+      const u32x4_t x = __builtin_amdgcn_raw_buffer_load_b128(krs, (int)(off + 16 * c4), 0, 0);
+      const u32x4_t y = __builtin_amdgcn_raw_buffer_load_b128(vrs, (int)(off + 16 * c4), 0, 0);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        kr.w[4 * c4 + w] = x[w];
+        vr.w[4 * c4 + w] = y[w];
+      }
+    }
+  };
+  Slice kr[NSW][UO], vr[NSW][UO];
+  auto load_set = [&](int k, int i) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < UO; ++u) load_kv(kr[k][u], vr[k][u], P + i * STEP + KPQ * u);
+  };
+
+  float mo = kNegInf, lo = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  // raise the quad's offset to mt when a score exceeds it by more than the
+  // lazy margin (one offset per quad row)
+  auto raise_offset = [&](float mt) __attribute__((always_inline)) {
+    if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
+    if (mt > mo + a.lazy_raw) {
+      const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
+      mo = mt;
+      lo *= alpha;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+    }
+  };
+  auto add_key = [&](float score, const Slice& vs, float moff) __attribute__((always_inline)) {
+    const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(score, cl, -moff));
+    lo += p;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vs, e), acc[e]);
+  };
+  // one register set: a key lane at or past Tc (zeros in its registers)
+  // scores -inf and adds p = 0; a set that starts at or past Tc is skipped
+  auto process = [&](const Slice (&ks)[UO], const Slice (&vs)[UO], int j0, const Slice& qs)
+                     __attribute__((always_inline)) {
+    float sv[UO];
+    float mt = kNegInf;
+#pragma unroll
+    for (int u = 0; u < UO; ++u) {
+      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, ks[u]));
+      sv[u] = (j0 + KPQ * u + kk < Tc) ? dot : kNegInf;
+      mt = fmaxf(mt, sv[u]);
+    }
+    raise_offset(mt);
+    const float moff = mo * cl;
+#pragma unroll
+    for (int u = 0; u < UO; ++u) add_key(sv[u], vs[u], moff);
+  };
+  // whole rounds of NSW sets, so that the loop body has one path: each set
+  // is refilled with the set NSW further on once it has been consumed
+  auto own_stream = [&](const Slice& qs) __attribute__((always_inline)) {
+    const int nsets = Tc > P ? (Tc - P + STEP - 1) / STEP : 0;
+    for (int r0 = 0; r0 < nsets; r0 += NSW) {
+#pragma unroll
+      for (int k = 0; k < NSW; ++k) {
+        const int i = r0 + k;
+        if (i < nsets) process(kr[k], vr[k], P + i * STEP, qs);
+        load_set(k, i + NSW);
+      }
+    }
+  };
+  // wave 1's partial to LDS: row orow's offset, sum and weighted values
+  auto hand_over = [&]() __attribute__((always_inline)) {
+    if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
+      lo += dpp<kDppQuadXor2>(lo);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] += dpp<kDppQuadXor2>(acc[e]);
+    }
+    if (kk == 0) {
+      float* pr = part + orow * RS;
+#pragma unroll
+      for (int e4 = 0; e4 < EPL / 4; ++e4)
+        *reinterpret_cast<f32x4_t*>(pr + piece * EPL + 4 * e4) =
+            f32x4_t{acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]};
+      if (piece == 0) {
+        pr[D] = mo;
+        pr[D + 1] = lo;
+      }
+    }
+  };
+
+  // wave 0's prefix state, merged after the hand-over
   const int c = lane & 15, g = lane >> 4;  // MFMA layout: tile row c, lane group g
   bool cvalid;
   const int64_t bc = row_of(c, cvalid);
@@ -231,36 +385,50 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Each wave issues its first cache loads right behind its query loads, as a
-  // fixed number of loads (rows clamped to ones that exist, position 0 at
-  // least; the extra rows are masked), so that waiting for the query does not
-  // wait for them.
+  // Each wave issues its first cache loads right behind its query loads (wave
+  // 1 with a scheduling barrier between them: waits count loads in the order
+  // they were issued), so that waiting for the query does not wait for them.
   if (role == 0) {
     // --- prefix on MFMA: lane (c, g) -------------------------------------------
     const T* kpre = static_cast<const T*>(a.pre.k) + grp * a.pre.kb + (int64_t)h * a.pre.kh;
     const T* vpre = static_cast<const T*>(a.pre.v) + grp * a.pre.vb + (int64_t)h * a.pre.vh;
-    Op kopA[NT], kopB[D == 16 ? NT : 1];
-    T vvA[NT][4][DT], vvB[D == 16 ? NT : 1][4][DT];
+    Op kopA[NT], kopB[NT];  // B: the second chunk buffer (D = 16 only)
+    T vvA[NTV][4][DT], vvB[NTV][4][DT];
+    VRow vrA, vrB;
+    // Values of one 64-key chunk: 16-bit types load value row c0 + l into
+    // lane l (whole rows, wide loads) and write it to row l of an LDS buffer
+    // just before the products, which read it transposed; fp32 gathers
+    // V[4g + s][16t + c] per key tile.  Rows past the prefix re-read its last
+    // key (masked, probability 0).
+    auto load_values = [&](int c0, int last, T (&vv)[NTV][4][DT], VRow& vrow) __attribute__((always_inline)) {
+      if constexpr (VLDS) {
+        load_row<T, D>(vrow, vpre + min(c0 + lane, last) * vt);
+      } else {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) {
+            const T* vq = vpre + min(c0 + 16 * j + 4 * g + s4, last) * vt + c;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
+          }
+        }
+      }
+    };
     // the first 128 prefix keys (64 at D = 32)
     auto first_chunks = [&]() __attribute__((always_inline)) {
       const int last = max(P - 1, 0);
 #pragma unroll
-      for (int half = 0; half < (D == 16 ? 2 : 1); ++half) {
+      for (int half = 0; half < NCB; ++half) {
 #pragma unroll
         for (int j = 0; j < NT; ++j) {
-          const int base = 16 * NT * half + 16 * j;
-          Op& kop = half ? kopB[D == 16 ? j : 0] : kopA[j];
-          load_row<T, DQ>(kop, kpre + min(base + c, last) * kt + g * DQ);
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
-            const T* vq = vpre + min(base + 4 * g + s4, last) * vt + c;
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-              T& dst = half ? vvB[D == 16 ? j : 0][s4][t] : vvA[j][s4][t];
-              dst = vq[16 * t];
-            }
-          }
+          Op& kop = half ? kopB[j] : kopA[j];
+          load_row<T, DQ>(kop, kpre + min(16 * NT * half + 16 * j + c, last) * kt + g * DQ);
         }
+        if (half)
+          load_values(16 * NT * half, last, vvB, vrB);
+        else
+          load_values(0, last, vvA, vrA);
       }
     };
     Op qop;  // q row c, elements g*DQ .. g*DQ + DQ - 1
@@ -290,21 +458,23 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
       load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
       first_chunks();
     }
-    auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+    auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NTV][4][DT], VRow& vrow) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        const int base = c0 + 16 * j;
-        if (base >= P) break;  // wave-uniform
-        load_row<T, DQ>(kop[j], kpre + min(base + c, P - 1) * kt + g * DQ);
+      for (int j = 0; j < NT; ++j)
+        load_row<T, DQ>(kop[j], kpre + min(c0 + 16 * j + c, P - 1) * kt + g * DQ);
+      load_values(c0, P - 1, vv, vrow);
+    };
+    // 16-bit types: value rows into LDS buffer buf, row l from lane l
+    auto stage_values = [&](const VRow& vrow, int buf) __attribute__((always_inline)) {
+      if constexpr (VLDS) {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(vst + buf * 64 * D + lane * D);
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-          const T* vq = vpre + min(base + 4 * g + s4, P - 1) * vt + c;
-#pragma unroll
-          for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
-        }
+        for (int c4 = 0; c4 < VRow::WORDS / 4; ++c4)
+          dst[c4] = u32x4_t{vrow.w[4 * c4], vrow.w[4 * c4 + 1], vrow.w[4 * c4 + 2], vrow.w[4 * c4 + 3]};
       }
     };
-    auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NT][4][DT]) __attribute__((always_inline)) {
+    auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NTV][4][DT], int buf)
+                            __attribute__((always_inline)) {
       f32x4_t sc[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
@@ -312,15 +482,24 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
         if (c0 + 16 * j >= P) continue;  // wave-uniform
         sc[j] = qk_mfma<T, DQ>(kop[j], qop, sc[j]);
       }
+      // keys past the prefix: a tile wholly past it at once, element by
+      // element only in the tile that holds key P - 1 (wave-uniform tests)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int k0 = c0 + 16 * j;
+        if (k0 + 16 <= P) continue;
+        if (k0 >= P) {
+          sc[j] = f32x4_t{kNegInf, kNegInf, kNegInf, kNegInf};
+          continue;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[j][r] = (k0 + 4 * g + r < P) ? sc[j][r] : kNegInf;
+      }
       float mx = kNegInf;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const bool in = c0 + 16 * j + 4 * g + r < P;
-          sc[j][r] = in ? sc[j][r] : kNegInf;
-          mx = fmaxf(mx, sc[j][r]);
-        }
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sc[j][r]);
       }
       mx = row_max4(mx);  // every chunk holds a prefix key: finite
       if (mx > m + a.lazy_raw) {
@@ -340,67 +519,74 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
           lp += p;
         }
       }
+      const uint16_t* vb = vst + buf * 64 * D;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
-        if (c0 + 16 * j >= P) continue;
+        if (c0 + 16 * j >= P) continue;  // wave-uniform
+        if constexpr (VLDS) {
+          // V^T operand: lane l reads the 8 bytes at row 16j + l/4, columns
+          // 16t + 4(l & 3) .. +3 of the buffer
+          uint32_t va[DT][2];
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
+          for (int t = 0; t < DT; ++t) {
+            const uint2 w = lds_read_tr16(vb + (16 * j + (lane >> 2)) * D + 16 * t + 4 * (lane & 3));
+            va[t][0] = w.x;
+            va[t][1] = w.y;
+          }
+          pv_mfma16<T, DT>(va, sc[j], oacc);
+        } else {
 #pragma unroll
-          for (int t = 0; t < DT; ++t)
-            oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
+          for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+              oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
+          }
         }
       }
     };
+    // the first chunks' values go to LDS as soon as they arrive (their
+    // registers are then free while the own keys stream in); a later chunk's
+    // right before its products, after the previous reads of its buffer fed
+    // their products
+    stage_values(vrA, 0);
+    if constexpr (NCB == 2) stage_values(vrB, 1);
     if constexpr (D == 16) {  // two chunk buffers fit the register budget at D = 16
       for (int c0 = 0; c0 < P; c0 += 32 * NT) {
-        if (c0 > 0 && c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB);
-        prefix_chunk(c0, kopA, vvA);
+        if (c0 > 0 && c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB, vrB);
+        if (c0 > 0) stage_values(vrA, 0);
+        prefix_chunk(c0, kopA, vvA, 0);
         if (c0 + 16 * NT >= P) break;
-        if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA);
-        prefix_chunk(c0 + 16 * NT, kopB, vvB);
+        if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA, vrA);
+        if (c0 > 0) stage_values(vrB, 1);
+        prefix_chunk(c0 + 16 * NT, kopB, vvB, 1);
       }
     } else {
       for (int c0 = 0; c0 < P; c0 += 16 * NT) {
-        if (c0 > 0) load_chunk(c0, kopA, vvA);
-        prefix_chunk(c0, kopA, vvA);
+        if (c0 > 0) {
+          load_chunk(c0, kopA, vvA, vrA);
+          stage_values(vrA, 0);
+        }
+        prefix_chunk(c0, kopA, vvA, 0);
       }
     }
-
   } else {
-    // --- own keys on the vector ALUs: lane (orow, kk, piece) --------------------
-    const T* kown = kbase + bo * a.kb + piece * EPL;
-    const T* vown = vbase + bo * a.vb + piece * EPL;
-    Slice kA[UO], vA[UO], kB[UO], vB[UO];
-    auto load_set = [&](Slice (&kr)[UO], Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
-#pragma unroll
-      for (int u = 0; u < UO; ++u) {
-        if (j0 + KPQ * u >= Tc) break;  // wave-uniform
-        const int j = min(j0 + KPQ * u + kk, Tc - 1);  // past Tc: a valid row, masked below
-        load_row<T, EPL>(kr[u], kown + j * kt);
-        load_row<T, EPL>(vr[u], vown + j * vt);
-      }
-    };
-    // the first two sets (only when there are own keys: the own pages may
-    // start at P, so no position below it is read from them)
-    auto first_sets = [&]() __attribute__((always_inline)) {
-      if (Tc <= P) return;  // wave-uniform
-      const int last = Tc - 1;
-#pragma unroll
-      for (int u = 0; u < 2 * UO; ++u) {
-        const int j = min(P + KPQ * u + kk, last);
-        load_row<T, EPL>(u < UO ? kA[u] : kB[u - UO], kown + j * kt);
-        load_row<T, EPL>(u < UO ? vA[u] : vB[u - UO], vown + j * vt);
-      }
-    };
+    // --- wave 1: own keys on the vector ALUs; fused: the new token -----------------
     Slice qs;
     Slice knew, vnew;  // fused: the appended key and value
+    float xq[EPL], xk[EPL], cs[EPL];
     if constexpr (FUSED) {
-      float xq[EPL], xk[EPL], cs[EPL];
       load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
       load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
       load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
       load_vec<FT, EPL>(fbase, cs);
-      first_sets();
+    } else {
+      load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NSW; ++k) load_set(k, k);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FUSED) {
       rotate_q(xq, cs, qs);
       rope_rotate<T, EPL>(xk, cs);
       if (a.qknorm) qk_rms_norm<EPL, LPK>(xk, D);
@@ -410,88 +596,20 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
         store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
         store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
       }
-    } else {
-      load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
-      first_sets();
     }
-    float mo = kNegInf, lo = 0.f;
-    float acc[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-    // raise the quad's offset to mt when a score exceeds it by more than the
-    // lazy margin (one offset per quad row)
-    auto raise_offset = [&](float mt) __attribute__((always_inline)) {
-      if constexpr (KPQ == 2) mt = fmaxf(mt, dpp<kDppQuadXor2>(mt));
-      if (mt > mo + a.lazy_raw) {
-        const float alpha = (mo == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((mo - mt) * cl);
-        mo = mt;
-        lo *= alpha;
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
-      }
-    };
-    auto add_key = [&](float score, const Slice& vr, float moff) __attribute__((always_inline)) {
-      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(score, cl, -moff));
-      lo += p;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] = __builtin_fmaf(p, elem<T, EPL>(vr, e), acc[e]);
-    };
-    auto process = [&](const Slice (&kr)[UO], const Slice (&vr)[UO], int j0) __attribute__((always_inline)) {
-      float sv[UO];
-      float mt = kNegInf;
-#pragma unroll
-      for (int u = 0; u < UO; ++u) {
-        sv[u] = kNegInf;
-        if (j0 + KPQ * u >= Tc) continue;  // slot not loaded (wave-uniform)
-        const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, kr[u]));
-        sv[u] = (j0 + KPQ * u + kk < Tc) ? dot : kNegInf;
-        mt = fmaxf(mt, sv[u]);
-      }
-      raise_offset(mt);
-      const float moff = mo * cl;
-#pragma unroll
-      for (int u = 0; u < UO; ++u) {
-        if (j0 + KPQ * u >= Tc) continue;
-        add_key(sv[u], vr[u], moff);
-      }
-    };
-    for (int j0 = P; j0 < Tc;) {
-      process(kA, vA, j0);
-      j0 += STEP;
-      if (j0 + STEP < Tc) load_set(kA, vA, j0 + STEP);
-      if (j0 >= Tc) break;
-      process(kB, vB, j0);
-      j0 += STEP;
-      if (j0 + STEP < Tc) load_set(kB, vB, j0 + STEP);
-    }
+    own_stream(qs);
     if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
       const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
       const float sn = kk == 0 ? dot : kNegInf;
       raise_offset(sn);
       add_key(sn, vnew, mo * cl);
     }
-    if constexpr (KPQ == 2) {  // the two keys of a quad: same offset, partials add
-      lo += dpp<kDppQuadXor2>(lo);
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] += dpp<kDppQuadXor2>(acc[e]);
-    }
-    // hand-over: row orow's offset, sum and weighted values
-    if (kk == 0) {
-      float* pr = part + orow * RS;
-#pragma unroll
-      for (int e4 = 0; e4 < EPL / 4; ++e4)
-        *reinterpret_cast<f32x4_t*>(pr + piece * EPL + 4 * e4) =
-            f32x4_t{acc[4 * e4], acc[4 * e4 + 1], acc[4 * e4 + 2], acc[4 * e4 + 3]};
-      if (piece == 0) {
-        pr[D] = mo;
-        pr[D + 1] = lo;
-      }
-    }
+    hand_over();
   }
   __syncthreads();
   if (role == 1) return;
 
-  // --- merge (wave 0): lane (c, g) holds columns 16t + 4g + r of row c ---------
+  // --- merge (wave 0): lane (c, g) holds columns 16t + 4g + r of row c --------
   const float* pr = part + c * RS;
   const float m_own = pr[D], l_own = pr[D + 1];
   const float M = fmaxf(m, m_own);
@@ -565,8 +683,11 @@ bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype,
   if (!st16(v_st->b) || !st16(v_st->t) || !st16(v_st->h)) return false;
   if (!al16(pre.k) || !al16(pre.v) || !st16(pre.kb) || !st16(pre.kh) || !st16(pre.vb) || !st16(pre.vh))
     return false;
-  if (k_st->t < 0 || v_st->t < 0) return false;
+  if (k_st->t < 0 || v_st->t < 0 || k_st->b < 0) return false;
   if ((int64_t)Tk * k_st->t >= ((int64_t)1 << 31) || (int64_t)Tk * v_st->t >= ((int64_t)1 << 31)) return false;
+  // the rows' own keys are addressed by one 32-bit byte offset for K and V
+  if (k_st->b != v_st->b || k_st->t != v_st->t) return false;
+  if (((int64_t)(B - 1) * k_st->b + (int64_t)(Tk - 1) * k_st->t + D) * es >= ((int64_t)1 << 31)) return false;
   const int64_t groups = ((int64_t)B + group - 1) / group;
   const int64_t tiles = (group + 15) / 16;
   const int64_t units = groups * tiles * H;
