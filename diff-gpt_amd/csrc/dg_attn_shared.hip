@@ -282,7 +282,9 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(kbase), (short)0, 0x7fffffff, kBufferWord3);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(vbase), (short)0, 0x7fffffff, kBufferWord3);
   const uint32_t ktb = (uint32_t)kt * (uint32_t)sizeof(T);
-  const uint32_t rowoff = (uint32_t)(bo * a.kb + piece * EPL) * (uint32_t)sizeof(T);
+  // rows past the group start past the range too: their keys read zeros
+  // without touching memory (rowoff + j * ktb stays in [2^31, 2^32))
+  const uint32_t rowoff = ovalid ? (uint32_t)(bo * a.kb + piece * EPL) * (uint32_t)sizeof(T) : kOobOffset;
   auto load_kv = [&](Slice& kr, Slice& vr, int jb) __attribute__((always_inline)) {
     const int j = jb + kk;  // jb wave-uniform
     const uint32_t off = j < Tc ? rowoff + (uint32_t)j * ktb : kOobOffset;
