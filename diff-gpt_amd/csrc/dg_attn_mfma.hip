@@ -404,9 +404,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       for (int c = 0; c < NC; ++c) {
         uint32_t w[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          w[i] = (uint32_t)from_f32<T>(x[qb][c][2 * i]).bits |
-                 ((uint32_t)from_f32<T>(x[qb][c][2 * i + 1]).bits << 16);
+        for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(x[qb][c][2 * i], x[qb][c][2 * i + 1]);
         qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
       }
     }

@@ -127,8 +127,7 @@ __device__ __forceinline__ void pack_row(RowRegs<T, EPL>& r, const float (&x)[EP
     for (int e = 0; e < EPL; ++e) r.w[e] = __float_as_uint(x[e]);
   } else {
 #pragma unroll
-    for (int w = 0; w < EPL / 2; ++w)
-      r.w[w] = (uint32_t)from_f32<T>(x[2 * w]).bits | ((uint32_t)from_f32<T>(x[2 * w + 1]).bits << 16);
+    for (int w = 0; w < EPL / 2; ++w) r.w[w] = pack_pair<T>(x[2 * w], x[2 * w + 1]);
   }
 }
 

@@ -60,6 +60,21 @@ __device__ __forceinline__ f16_t from_f32<f16_t>(float x) {
   return r;
 }
 
+// Two fp32 values rounded to T (nearest even) in one 32-bit word, a in the
+// low half: bf16 pairs through one v_cvt_pk_bf16_f32, with the same guard
+// as from_f32 against folding a producer into the conversion.
+template <typename T>
+__device__ __forceinline__ uint32_t pack_pair(float a, float b) {
+  if constexpr (__is_same(T, bf16_t)) {
+    asm("" : "+v"(a), "+v"(b));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{a, b}, b2_t));
+  } else {
+    return (uint32_t)from_f32<T>(a).bits | ((uint32_t)from_f32<T>(b).bits << 16);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Vector loads of EPL consecutive elements (EPL*sizeof(T) bytes, naturally
 // aligned by the host-side checks) converted to fp32.

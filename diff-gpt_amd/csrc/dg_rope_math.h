@@ -27,8 +27,15 @@ __device__ __forceinline__ void rope_rotate(float (&x)[EPL], const float (&cs)[E
     const float a0 = re * c, a1 = im * sn;
     const float b0 = re * sn, b1 = im * c;
     // rounding to the storage dtype happens here (type_as), before the norm
-    x[2 * p] = to_f32(from_f32<T>(a0 - a1));
-    x[2 * p + 1] = to_f32(from_f32<T>(b0 + b1));
+    if constexpr (__is_same(T, bf16_t)) {
+      // both outputs rounded by one packed conversion, unpacked by shift and mask
+      const uint32_t w = pack_pair<T>(a0 - a1, b0 + b1);
+      x[2 * p] = __uint_as_float(w << 16);
+      x[2 * p + 1] = __uint_as_float(w & 0xffff0000u);
+    } else {
+      x[2 * p] = to_f32(from_f32<T>(a0 - a1));
+      x[2 * p + 1] = to_f32(from_f32<T>(b0 + b1));
+    }
   }
 }
 
