@@ -134,9 +134,10 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * dg_rope_qknorm_append with q = NULL appending them).  freqs / f_st /
  * freqs_dtype as in dg_rope_qknorm_append, for the Tq query rows; flags:
  * DG_QKNORM or 0, optionally with DG_KEYS_NORMED (DG_QKNORM | DG_KEYS_NORMED:
- * the keys are normalised too; the softmax then runs without a running
- * maximum, with the scale folded into the rounded query operand, so y agrees
- * with dg_attention's within the bf16/fp16 bar rather than bit for bit).
+ * the keys are normalised too; for bf16 data the softmax then runs without a
+ * running maximum, with the scale folded into the rounded query operand, so y
+ * agrees with dg_attention's within the bf16 bar rather than bit for bit;
+ * fp16 data ignores the flag and gives dg_attention's y bit for bit).
  * Only the MFMA prefill kernel's shapes are taken (bf16 or
  * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
  * freqs in the data's dtype or fp32): anything else returns DG_EUNSUPPORTED
