@@ -25,15 +25,22 @@
 //   back the scores of row c against keys 4g .. 4g+3 of the tile.  The
 //   online softmax runs over chunks of 64 keys (max over the chunk, lazy
 //   rescale as in the vector kernel), then
-//   O^T (D x 16 rows) += V^T P^T in steps of 4 keys: lane (c, g) feeds
-//   V[4g+s][16t+c] and its own probability of key 4g+s, and holds O^T for
-//   row c, columns 16t + 4g .. 16t + 4g + 3.
+//   O^T (D x 16 rows) += V^T P^T: lane (c, g) feeds V[4g+s][16t+c] and its
+//   own probability of key 4g+s, and holds O^T for row c, columns
+//   16t + 4g .. 16t + 4g + 3.  Each 64-key chunk of V goes through LDS, one
+//   row per lane with wide loads: fp32 writes it transposed (column-wise,
+//   padded rows) and takes four 16x16x4 products per key tile from one
+//   ds_read_b128; bf16 / fp16 write it row-major, read it back transposed
+//   (ds_read_b64_tr_b16) and take two 16x16x16 products, P split as hi + lo
+//   in T.
 // Own keys (wave 1, VALU): a quad of lanes holds one tile row, 16 bytes of a
 //   cache row per lane (OwnCfg), so every quad reads whole cache rows; the
 //   lanes of a key row add their partial dot products with DPP, and each
 //   lane accumulates p * v for its slice of the row.  The wave streams its
 //   keys from the start of the launch, two register sets in flight, while
-//   wave 0's prefix phase (a few dependent cache round trips) runs.
+//   wave 0's prefix phase (a few dependent cache round trips) runs.  Keys
+//   are loaded through buffer resources with one 32-bit offset for K and V;
+//   a key past the last cached position reads zeros from past the range.
 // Merge: wave 1 writes each row's softmax offset, sum and weighted values to
 //   LDS; after one barrier wave 0 rescales both parts to the larger offset,
 //   adds them and stores its O^T columns.
@@ -209,11 +216,17 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   constexpr int NSW = 2;                 // register sets of own keys in flight (64 VGPRs)
   constexpr int RS = D + 4;              // floats per row of a hand-over buffer (16-byte rows)
   constexpr int NCB = D == 16 ? 2 : 1;   // prefix chunk buffers
-  constexpr bool VLDS = sizeof(T) == 2;  // prefix values staged in LDS, read transposed
-  constexpr int NTV = VLDS ? 1 : NT;     // fp32: values gathered into registers per key tile
   using VRow = RowRegs<T, D>;            // a whole value row
+  // Prefix values go through LDS, 64 keys per buffer.  16-bit types: row-major
+  // (64 rows of D), read transposed by ds_read_b64_tr_b16.  fp32: transposed
+  // on the write, D rows of 64 keys padded to VT_STRIDE floats, so that one
+  // ds_read_b128 gives a lane the 4 consecutive keys of one column that its
+  // four 16x16x4 products take, with no bank conflicts (16 lanes of one read
+  // sit 4 banks apart).
+  constexpr int VT_STRIDE = 68;
+  constexpr int VBUF_BYTES = sizeof(T) == 2 ? 64 * D * 2 : D * VT_STRIDE * 4;
   __shared__ __attribute__((aligned(16))) float part[16 * RS];  // wave 1's partial
-  __shared__ __attribute__((aligned(16))) uint16_t vst[VLDS ? NCB * 64 * D : 8];
+  __shared__ __attribute__((aligned(16))) unsigned char vst[NCB * VBUF_BYTES];
 
   const int lane = threadIdx.x & 63;
   const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 0: prefix, 1: own keys
@@ -394,27 +407,12 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     const T* kpre = static_cast<const T*>(a.pre.k) + grp * a.pre.kb + (int64_t)h * a.pre.kh;
     const T* vpre = static_cast<const T*>(a.pre.v) + grp * a.pre.vb + (int64_t)h * a.pre.vh;
     Op kopA[NT], kopB[NT];  // B: the second chunk buffer (D = 16 only)
-    T vvA[NTV][4][DT], vvB[NTV][4][DT];
     VRow vrA, vrB;
-    // Values of one 64-key chunk: 16-bit types load value row c0 + l into
-    // lane l (whole rows, wide loads) and write it to row l of an LDS buffer
-    // just before the products, which read it transposed; fp32 gathers
-    // V[4g + s][16t + c] per key tile.  Rows past the prefix re-read its last
-    // key (masked, probability 0).
-    auto load_values = [&](int c0, int last, T (&vv)[NTV][4][DT], VRow& vrow) __attribute__((always_inline)) {
-      if constexpr (VLDS) {
-        load_row<T, D>(vrow, vpre + min(c0 + lane, last) * vt);
-      } else {
-#pragma unroll
-        for (int j = 0; j < NT; ++j) {
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
-            const T* vq = vpre + min(c0 + 16 * j + 4 * g + s4, last) * vt + c;
-#pragma unroll
-            for (int t = 0; t < DT; ++t) vv[j][s4][t] = vq[16 * t];
-          }
-        }
-      }
+    // Values of one 64-key chunk: lane l loads value row c0 + l (whole rows,
+    // wide loads) and later writes it to an LDS buffer.  Rows past the prefix
+    // re-read its last key (masked, probability 0).
+    auto load_values = [&](int c0, int last, VRow& vrow) __attribute__((always_inline)) {
+      load_row<T, D>(vrow, vpre + min(c0 + lane, last) * vt);
     };
     // the first 128 prefix keys (64 at D = 32)
     auto first_chunks = [&]() __attribute__((always_inline)) {
@@ -426,10 +424,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
           Op& kop = half ? kopB[j] : kopA[j];
           load_row<T, DQ>(kop, kpre + min(16 * NT * half + 16 * j + c, last) * kt + g * DQ);
         }
-        if (half)
-          load_values(16 * NT * half, last, vvB, vrB);
-        else
-          load_values(0, last, vvA, vrA);
+        load_values(16 * NT * half, last, half ? vrB : vrA);
       }
     };
     Op qop;  // q row c, elements g*DQ .. g*DQ + DQ - 1
@@ -459,23 +454,28 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
       load_row<T, DQ>(qop, qbase + bc * a.qb + g * DQ);
       first_chunks();
     }
-    auto load_chunk = [&](int c0, Op (&kop)[NT], T (&vv)[NTV][4][DT], VRow& vrow) __attribute__((always_inline)) {
+    auto load_chunk = [&](int c0, Op (&kop)[NT], VRow& vrow) __attribute__((always_inline)) {
 #pragma unroll
       for (int j = 0; j < NT; ++j)
         load_row<T, DQ>(kop[j], kpre + min(c0 + 16 * j + c, P - 1) * kt + g * DQ);
-      load_values(c0, P - 1, vv, vrow);
+      load_values(c0, P - 1, vrow);
     };
-    // 16-bit types: value rows into LDS buffer buf, row l from lane l
+    // the chunk's value rows into LDS buffer buf: 16-bit types row l from
+    // lane l; fp32 column d of key l at d * VT_STRIDE + l
     auto stage_values = [&](const VRow& vrow, int buf) __attribute__((always_inline)) {
-      if constexpr (VLDS) {
-        u32x4_t* dst = reinterpret_cast<u32x4_t*>(vst + buf * 64 * D + lane * D);
+      unsigned char* vb = vst + buf * VBUF_BYTES;
+      if constexpr (sizeof(T) == 2) {
+        u32x4_t* dst = reinterpret_cast<u32x4_t*>(vb) + lane * (D / 8);
 #pragma unroll
         for (int c4 = 0; c4 < VRow::WORDS / 4; ++c4)
           dst[c4] = u32x4_t{vrow.w[4 * c4], vrow.w[4 * c4 + 1], vrow.w[4 * c4 + 2], vrow.w[4 * c4 + 3]};
+      } else {
+        float* dst = reinterpret_cast<float*>(vb) + lane;
+#pragma unroll
+        for (int d = 0; d < D; ++d) dst[d * VT_STRIDE] = __uint_as_float(vrow.w[d]);
       }
     };
-    auto prefix_chunk = [&](int c0, const Op (&kop)[NT], const T (&vv)[NTV][4][DT], int buf)
-                            __attribute__((always_inline)) {
+    auto prefix_chunk = [&](int c0, const Op (&kop)[NT], int buf) __attribute__((always_inline)) {
       f32x4_t sc[NT];
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
@@ -520,27 +520,31 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
           lp += p;
         }
       }
-      const uint16_t* vb = vst + buf * 64 * D;
+      const unsigned char* vb = vst + buf * VBUF_BYTES;
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         if (c0 + 16 * j >= P) continue;  // wave-uniform
-        if constexpr (VLDS) {
+        if constexpr (sizeof(T) == 2) {
           // V^T operand: lane l reads the 8 bytes at row 16j + l/4, columns
           // 16t + 4(l & 3) .. +3 of the buffer
+          const uint16_t* vb16 = reinterpret_cast<const uint16_t*>(vb);
           uint32_t va[DT][2];
 #pragma unroll
           for (int t = 0; t < DT; ++t) {
-            const uint2 w = lds_read_tr16(vb + (16 * j + (lane >> 2)) * D + 16 * t + 4 * (lane & 3));
+            const uint2 w = lds_read_tr16(vb16 + (16 * j + (lane >> 2)) * D + 16 * t + 4 * (lane & 3));
             va[t][0] = w.x;
             va[t][1] = w.y;
           }
           pv_mfma16<T, DT>(va, sc[j], oacc);
         } else {
+          // lane (c, g): V[16j + 4g + s][16t + c], s = 0..3, in one read
+          const float* vbf = reinterpret_cast<const float*>(vb);
 #pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) {
+          for (int t = 0; t < DT; ++t) {
+            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(vbf + (16 * t + c) * VT_STRIDE + 16 * j + 4 * g);
 #pragma unroll
-            for (int t = 0; t < DT; ++t)
-              oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(vv[j][s4][t]), sc[j][s4], oacc[t], 0, 0, 0);
+            for (int s4 = 0; s4 < 4; ++s4)
+              oacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(w[s4], sc[j][s4], oacc[t], 0, 0, 0);
           }
         }
       }
@@ -553,21 +557,21 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     if constexpr (NCB == 2) stage_values(vrB, 1);
     if constexpr (D == 16) {  // two chunk buffers fit the register budget at D = 16
       for (int c0 = 0; c0 < P; c0 += 32 * NT) {
-        if (c0 > 0 && c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vvB, vrB);
+        if (c0 > 0 && c0 + 16 * NT < P) load_chunk(c0 + 16 * NT, kopB, vrB);
         if (c0 > 0) stage_values(vrA, 0);
-        prefix_chunk(c0, kopA, vvA, 0);
+        prefix_chunk(c0, kopA, 0);
         if (c0 + 16 * NT >= P) break;
-        if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vvA, vrA);
+        if (c0 + 32 * NT < P) load_chunk(c0 + 32 * NT, kopA, vrA);
         if (c0 > 0) stage_values(vrB, 1);
-        prefix_chunk(c0 + 16 * NT, kopB, vvB, 1);
+        prefix_chunk(c0 + 16 * NT, kopB, 1);
       }
     } else {
       for (int c0 = 0; c0 < P; c0 += 16 * NT) {
         if (c0 > 0) {
-          load_chunk(c0, kopA, vvA, vrA);
+          load_chunk(c0, kopA, vrA);
           stage_values(vrA, 0);
         }
-        prefix_chunk(c0, kopA, vvA, 0);
+        prefix_chunk(c0, kopA, 0);
       }
     }
   } else {
