@@ -116,7 +116,7 @@ def _bf16_model(dev, n_embd, n_head, n_layer, block_size=2048):
 
 
 @torch.no_grad()
-def _oracle_decode(params16, cfg, prompts, steps, schedule, exact=True, tokens=None):
+def _oracle_decode(params16, cfg, prompts, steps, schedule, exact=True, tokens=None, bf16_table=True):
     """The oracle model on the bf16 weights: prefill, then ``steps``
     single-token steps.  exact=True evaluates in float32 (the exact function
     of those weights, with the bf16 RoPE table the bf16 model holds);
@@ -128,7 +128,7 @@ def _oracle_decode(params16, cfg, prompts, steps, schedule, exact=True, tokens=N
     B, T = prompts.shape
     cache = tr.RefCache(B, cfg.n_head, T + steps, cfg.head_dim, cfg.n_layer)
     table = tr.freqs_table(cfg.head_dim, 2 * cfg.block_size, cfg.rope_theta)
-    if exact:
+    if exact and bf16_table:  # the RoPE table a bf16 model holds
         table = table.to(torch.bfloat16).float()
     logits = tr.forward(p, cfg, prompts, cache, table)[:, -1]
     toks, outs = [], []
@@ -188,6 +188,102 @@ def test_cfg3_geometry_prefill_and_decode(dev):
           f"2e-2*max|exact| {2e-2 * span:.4g}; greedy ids checked {checked}/{B * steps}")
     assert worst_ours <= 1.5 * worst_ref + 1e-3, (worst_ours, worst_ref)
     assert kv.get_pos() == T + steps
+
+
+def test_cfg3_geometry_fp32_greedy_ids(dev):
+    """configs[3] geometry (n_embd 512, 8 heads of 64, 8 layers) in fp32 at
+    B = 2: a 1024-token prefill and 8 greedy decode steps over the KV cache
+    (the decode attention's key splits included), against the oracle model
+    in fp32.  In fp32 the model's rounding noise is far below the logit
+    margins, so -- unlike the bf16 run above, where bf16 rounding swamps the
+    margins of a random-weight model -- the greedy ids are checked at nearly
+    every step: equal to the oracle's wherever the top-1/top-2 margin exceeds
+    twice the step's deviation.  Logits within 1e-5 * max|ref| (through 8
+    layers of width 512 the GEMMs' summation
+    order against the CPU's could move them, but they stay within 1e-5)."""
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.model.kv_cache import KVCache
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=512, block_size=2048, n_head=8, n_layer=8, use_checkpoint=False).eval()
+    params = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=512, block_size=2048, n_head=8, n_layer=8)
+    model = model.to(dev)
+    B, T, steps = 2, 1024, 8
+    prompts = torch.randint(0, 256, (B, T), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        ref_tokens, ref_logits = tr.greedy_decode(params, cfg, prompts, steps)
+    kv = KVCache(batch_size=B, num_heads=8, seq_len=T + steps, head_dim=64, num_layers=8)
+    worst, checked = 0.0, 0
+    with torch.inference_mode():
+        logits = model(prompts.to(dev), kv_cache=kv)[0][:, -1]
+        for s in range(steps):
+            got, ref = logits.float().cpu(), ref_logits[s].float()
+            err = (got - ref).abs().max().item()
+            worst = max(worst, err / ref.abs().max().item())
+            clear = _margin(ref) > 2 * err
+            checked += int(clear.sum())
+            assert torch.equal(got.argmax(-1)[clear], ref.argmax(-1)[clear]), s
+            nxt = ref_tokens[:, s]
+            logits = model(nxt[:, None].to(dev), kv_cache=kv)[0][:, -1]
+    print(f"cfg3 geometry fp32: worst |logit err| {worst:.3g} x max|ref|; greedy ids checked {checked}/{B * steps}")
+    assert worst <= 1e-5, worst
+    assert checked >= B * steps - 2, checked
+    assert kv.get_pos() == T + steps
+
+
+def test_cfg4_geometry_fp32_engine_with_force_schedule(dev):
+    """configs[4] geometry (n_embd 1024, 8 heads of 128, 4 layers) in fp32: a
+    3584-token prompt through Engine.generate_batch with 2 greedy
+    trajectories and 16 steps of configs[4]'s force schedule, against the
+    oracle model in fp32 driven by the same schedule.  The prompt's logits
+    agree within 1e-5 * max|ref|; forced positions carry the schedule with
+    mask 0; every sampled position (mask 1) whose top-1/top-2 margin exceeds
+    twice that deviation equals the oracle's greedy token, up to a near-tie
+    that the two decide differently (where the trajectories may part).  16
+    steps, so that several sampled positions are compared."""
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=1024, block_size=2048, n_head=8, n_layer=4, use_checkpoint=False).eval()
+    params = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=1024, block_size=2048, n_head=8, n_layer=4)
+    model = model.to(dev)
+    T, steps = 3584, 16
+    prompt = torch.randint(0, 256, (1, T), generator=torch.Generator().manual_seed(4))
+    rng = torch.Generator().manual_seed(5)
+    draws = torch.randint(0, 256, (steps,), generator=rng).tolist()
+    schedule = [draws[s] if (T + s) % 7 in (0, 1, 2) else None for s in range(steps)]
+    tokens, ref = _oracle_decode(params, cfg, prompt, steps, schedule, bf16_table=False)
+
+    with torch.inference_mode():
+        first, _ = model(prompt.to(dev))
+    err = (first[:, -1].float().cpu() - ref[0]).abs().max().item()
+    rel = err / ref[0].abs().max().item()
+    results, masks = Engine(model).generate_batch(
+        tokens=prompt[0].tolist(), num_samples=2, max_tokens=steps,
+        sampler=TemperatureSampler(0.0), force_schedule=schedule)
+    assert len(results) == 2 and results[0] == results[1]
+    gen, mask = results[0][T:], masks[0][T:]
+    checked = 0
+    for s in range(steps):
+        if schedule[s] is not None:
+            assert gen[s] == schedule[s] and mask[s] == 0
+            continue
+        assert mask[s] == 1
+        if _margin(ref[s])[0] <= 2 * err:
+            # a near-tie may go either way; while both pick the same token the
+            # trajectories are still the same and the comparison goes on
+            if gen[s] != int(tokens[0, s]):
+                print(f"cfg4 geometry fp32: near-tie at step {s} decided differently; later steps not compared")
+                break
+            continue
+        assert gen[s] == int(tokens[0, s]), s
+        checked += 1
+    print(f"cfg4 geometry fp32: prompt logits |ours - ref| {rel:.3g} x max|ref|; sampled ids checked {checked}")
+    assert rel <= 1e-5, rel
 
 
 def test_cfg4_geometry_engine_with_force_schedule(dev):
