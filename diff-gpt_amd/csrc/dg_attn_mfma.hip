@@ -32,12 +32,16 @@
 // Softmax arithmetic per score: one max (v_max3), one FMA (scale and max
 // subtraction in log2 units), one exp2, half a bf16 pack and half a dot2 (the
 // row sum adds the packed bf16/fp16 probabilities that also feed the MFMA, so
-// numerator and denominator use the same rounded values).  The running max
+// numerator and denominator use the same rounded values; the bounded form
+// below sums the fp32 probabilities instead).  The running max
 // used as the exponent offset is raised only when a row's new maximum exceeds
 // it by more than kLazyLog2 (log2 units); in between, probabilities up to
 // 2^kLazyLog2 are accumulated exactly as the online softmax would after a
 // rescale, so the result is the same function -- only the rescale of the
 // accumulators is skipped.
+//
+// The output leaves through LDS (the stage arrays are free after the last
+// tile), so that every store instruction writes whole 128/256-byte rows.
 //
 // Causality: query i sees key j iff j <= i + (Tk - Tq).  Tiles entirely above
 // a wavefront's diagonal are skipped by that wavefront; only tiles crossing
@@ -374,13 +378,51 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       }
     }
     dma_tile(ks0, vs0, 0);
+    if constexpr (BND && D == 64) {
+      // Bounded form at D = 64 (launched with the norm): the operand only has
+      // to carry q's direction to the bf16 bar, so the row is rotated in fp32
+      // (FMAs), its sum of squares taken on the fp32 rotation, and the
+      // rotation times rsqrt(mean + eps) * scale * log2(e) rounded once -- one
+      // rounding where the reference rounds the rotation and the normalised
+      // row.  (At D = 128 this form holds more values live than the register
+      // budget of three workgroups per CU allows; it takes the path below.)
+#pragma unroll
+      for (int qb = 0; qb < QW; ++qb) {
+        float ssq[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          float acc = 0.f;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const float re = x[qb][c][2 * p], im = x[qb][c][2 * p + 1];
+            const float co = cs[qb][c][2 * p], sn = cs[qb][c][2 * p + 1];
+            const float y0 = __builtin_fmaf(re, co, -(im * sn));
+            const float y1 = __builtin_fmaf(re, sn, im * co);
+            acc = __builtin_fmaf(y1, y1, __builtin_fmaf(y0, y0, acc));
+            x[qb][c][2 * p] = y0;
+            x[qb][c][2 * p + 1] = y1;
+          }
+          ssq[c] = acc;
+        }
+        // lanes l and l^32 hold the two halves of one row
+        const float ss = half_pair_sum(tree_sum<NC>(ssq));
+        const float r = __builtin_amdgcn_rsqf(__builtin_fmaf(ss, 1.0f / (float)D, FLT_EPSILON)) * a.scale_log2;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          uint32_t w[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(x[qb][c][2 * i] * r, x[qb][c][2 * i + 1] * r);
+          qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+      }
+    } else {
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb) {
       // rows past Tq hold row Tq - 1 (finite, normalised) and are never stored
 #pragma unroll
       for (int c = 0; c < NC; ++c) rope_rotate<T, 8>(x[qb][c], cs[qb][c]);
-      // the bounded form is launched with the norm only; lanes l and l^32 hold
-      // the same row, so both take this branch
+      // the bounded form is launched with the norm; lanes l and l^32 hold the
+      // same row, so both take this branch
       if (BND || a.qknorm) {
         float s16[NC];
 #pragma unroll
@@ -407,6 +449,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
         for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(x[qb][c][2 * i], x[qb][c][2 * i + 1]);
         qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
       }
+    }
     }
   } else {
 #pragma unroll
@@ -529,6 +572,9 @@ void prefill_mfma_kernel(const PrefillArgs a) {
             if (8 * (r >> 2) + (r & 3) > lim) s[qb][r] = kNegInf;
         }
       }
+      // The row sum adds the fp32 probabilities with plain adds: measured on
+      // this chip, a v_dot2_f32_bf16 takes ~38 cycles instead of ~6 while
+      // another wave's MFMAs run on the same SIMD; a v_add_f32 loses ~1.
       vec8 pf[QW][2];
 #pragma unroll
       for (int qb = 0; qb < QW; ++qb) {
@@ -538,9 +584,10 @@ void prefill_mfma_kernel(const PrefillArgs a) {
           uint32_t w[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            w[i] = Ops::pack2(__builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i]),
-                              __builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i + 1]));
-            ls = Ops::add_pair(w[i], ls);
+            const float p0 = __builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i]);
+            const float p1 = __builtin_amdgcn_exp2f(s[qb][8 * c2 + 2 * i + 1]);
+            w[i] = Ops::pack2(p0, p1);
+            ls += p0 + p1;
           }
           pf[qb][c2] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
         }
@@ -682,24 +729,49 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   }
 
   if (!wave_live) return;
+  // The output goes out through LDS, row-major: a lane's accumulators hold 4
+  // dims of its query per register group, so stored directly every store
+  // instruction would write 16 bytes into each of 32 rows (8 partial-line
+  // writes per row).  Each wave owns one of the four stage arrays (every wave
+  // has passed the barrier after its last tile, so none is read any more; one
+  // array holds 32 rows of D elements); the 16-byte pieces of row r sit at
+  // slot piece ^ (r mod D/8), which spreads the 32 rows' writes of one piece
+  // over the banks.  Read back, PPQ lanes cover one whole row, so a store
+  // instruction writes RPS full rows.
+  constexpr int PPQ = D / 8;     // 16-byte pieces per output row
+  constexpr int RPS = 64 / PPQ;  // rows per wave-wide store
+  static_assert(32 * D <= C::TILE, "a stage array holds one wave's output rows");
+  uint16_t* stg = wv == 0 ? ks0 : wv == 1 ? vs0 : wv == 2 ? ks1 : vs1;
+  T* yb0 = static_cast<T*>(a.y) + b * a.yb + (int64_t)head * a.yh;
 #pragma unroll
   for (int qb = 0; qb < QW; ++qb) {
-    const int qi = qw + 32 * qb + r32;
-    const float lt = half_pair_sum(l[qb]);
-    if (qi >= a.Tq) continue;
-    const float inv = 1.0f / lt;
-    T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)qi * a.yt + (int64_t)head * a.yh;
+    // rows past Tq carry finite values and are not stored
+    const float inv = 1.0f / half_pair_sum(l[qb]);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        T e[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) e[i] = from_f32<T>(o[qb][nb][4 * g + i] * inv);
-        uint2 raw;
-        __builtin_memcpy(&raw, e, 8);
-        *reinterpret_cast<uint2*>(yp + 32 * nb + 8 * g + 4 * hh) = raw;
+        const uint32_t w0 = pack_pair<T>(o[qb][nb][4 * g] * inv, o[qb][nb][4 * g + 1] * inv);
+        const uint32_t w1 = pack_pair<T>(o[qb][nb][4 * g + 2] * inv, o[qb][nb][4 * g + 3] * inv);
+        const int slot = (4 * nb + g) ^ (r32 & (PPQ - 1));
+        *reinterpret_cast<uint2*>(stg + r32 * D + 8 * slot + 4 * hh) = make_uint2(w0, w1);
       }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int piece = lane % PPQ;
+#pragma unroll
+    for (int p = 0; p < 32 / RPS; ++p) {
+      const int row = p * RPS + lane / PPQ;
+      const u32x4_t val = *reinterpret_cast<const u32x4_t*>(stg + row * D + 8 * (piece ^ (row & (PPQ - 1))));
+      const int qi = qw + 32 * qb + row;
+      if (qi < a.Tq) *reinterpret_cast<u32x4_t*>(yb0 + (int64_t)qi * a.yt + 8 * piece) = val;
+    }
+    if (qb + 1 < QW) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
 }
