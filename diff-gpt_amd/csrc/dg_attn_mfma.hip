@@ -268,7 +268,10 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   // then tell the stage being copied into from the one being read
   __shared__ __attribute__((aligned(16))) uint16_t ks0[C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t vs0[C::TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t ks1[C::TILE];
+  // in the RoPE instances at D = 64 the second K stage is twice as long:
+  // before the first barrier it stages the four waves' query rows (4 KB
+  // each); 40 KB per workgroup still lets four workgroups share a CU's 160 KB
+  __shared__ __attribute__((aligned(16))) uint16_t ks1[(D == 64 && ROPE ? 2 : 1) * C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t vs1[C::TILE];
 
   const int tid = threadIdx.x;
@@ -357,7 +360,83 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   // Q^T fragments (B operand): lane holds Q[qi][16c + 8hh .. +8].  The first
   // key tile's copies go out right behind the query loads.
   vec8 qf[QW][NC];
-  if constexpr (ROPE) {
+  if constexpr (ROPE && D == 64 && QW == 1) {
+    // RoPE instances at D = 64: the query rows and their (cos, sin) rows are
+    // loaded whole-line coalesced -- 8 lanes per 128-byte row, lane
+    // (r, p) = (l / 8, l % 8) holding elements 8p .. 8p+7 of rows r, r + 8,
+    // r + 16, r + 24 of the wave -- and rotated, normalised and packed in
+    // that layout; one LDS round trip then hands each lane its operand
+    // chunks.  (Loaded in the operand layout, every load instruction touches
+    // 32 rows for 32 bytes each: measured 3-4x the cost per byte through the
+    // vector memory path.)  The exact form's lanes and reduction tree are
+    // those of rope_qknorm_kernel at D = 64 (8 elements per lane, 8 lanes per
+    // row), so its bits are the same.  Each wave stages its 32 rows (4 KB,
+    // 16-byte pieces XOR-swizzled by row) in the second K stage, which nothing
+    // else touches before the barrier that precedes the loop.  (The general
+    // kernel's plain q loads measured faster without the round trip.)
+    const int prow = lane >> 3, ppc = lane & 7;
+    auto qswz = [](int r) { return (r >> 1) & 7; };
+    uint4 packed[4];
+    {
+#pragma clang fp contract(off)
+      float x[4][8], cs[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // rows past Tq hold row Tq - 1 (finite, normalised) and are never stored
+        const int qi = min(qw + 8 * i + prow, a.Tq - 1);
+        load_vec<T, 8>(qp + (int64_t)qi * a.qt + 8 * ppc, x[i]);
+        load_vec<FT, 8>(static_cast<const FT*>(a.freqs) + b * a.fb + (int64_t)qi * a.ft + (int64_t)head * a.fh + 8 * ppc,
+                        cs[i]);
+      }
+      dma_tile(ks0, vs0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t w[4];
+        if constexpr (BND) {
+          // Bounded form (launched with the norm): the operand only has to
+          // carry q's direction to the bf16 bar, so the row is rotated in fp32
+          // (FMAs), its sum of squares taken on the fp32 rotation, and the
+          // rotation times rsqrt(mean + eps) * scale * log2(e) rounded once --
+          // one rounding where the reference rounds the rotation and the
+          // normalised row.
+          float acc = 0.f;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const float re = x[i][2 * p], im = x[i][2 * p + 1];
+            const float co = cs[i][2 * p], sn = cs[i][2 * p + 1];
+            x[i][2 * p] = __builtin_fmaf(re, co, -(im * sn));
+            x[i][2 * p + 1] = __builtin_fmaf(re, sn, im * co);
+            acc = __builtin_fmaf(x[i][2 * p + 1], x[i][2 * p + 1], __builtin_fmaf(x[i][2 * p], x[i][2 * p], acc));
+          }
+          const float ss = group_sum_dpp<8>(acc);
+          const float r = __builtin_amdgcn_rsqf(__builtin_fmaf(ss, 1.0f / (float)D, FLT_EPSILON)) * a.scale_log2;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) w[p] = pack_pair<T>(x[i][2 * p] * r, x[i][2 * p + 1] * r);
+        } else {
+          rope_rotate<T, 8>(x[i], cs[i]);
+          if (a.qknorm) qk_rms_norm<8, 8, true>(x[i], D);
+#pragma unroll
+          for (int p = 0; p < 4; ++p) w[p] = pack_pair<T>(x[i][2 * p], x[i][2 * p + 1]);
+        }
+        packed[i] = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+    // all four waves stage in the one array ks1 (a pointer chosen between two
+    // arrays would leave the compiler unable to tell these accesses from the
+    // copies into the first stage, and it would make them wait for those)
+    uint16_t* qst = ks1 + wv * 32 * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 8 * i + prow;
+      *reinterpret_cast<uint4*>(qst + r * D + 8 * (ppc ^ qswz(r))) = packed[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qf[0][c] = __builtin_bit_cast(vec8, *reinterpret_cast<const uint4*>(qst + r32 * D + 8 * ((2 * c + hh) ^ qswz(r32))));
+  } else if constexpr (ROPE) {
     // RoPE + QK-norm of the query rows as they are loaded (mha.py:44-48), with
     // the arithmetic and roundings of dg_rope_qknorm_append, so the operand
     // has the bits that kernel would store: each 8-element chunk 16c + 8hh
@@ -378,44 +457,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       }
     }
     dma_tile(ks0, vs0, 0);
-    if constexpr (BND && D == 64) {
-      // Bounded form at D = 64 (launched with the norm): the operand only has
-      // to carry q's direction to the bf16 bar, so the row is rotated in fp32
-      // (FMAs), its sum of squares taken on the fp32 rotation, and the
-      // rotation times rsqrt(mean + eps) * scale * log2(e) rounded once -- one
-      // rounding where the reference rounds the rotation and the normalised
-      // row.  (At D = 128 this form holds more values live than the register
-      // budget of three workgroups per CU allows; it takes the path below.)
-#pragma unroll
-      for (int qb = 0; qb < QW; ++qb) {
-        float ssq[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          float acc = 0.f;
-#pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            const float re = x[qb][c][2 * p], im = x[qb][c][2 * p + 1];
-            const float co = cs[qb][c][2 * p], sn = cs[qb][c][2 * p + 1];
-            const float y0 = __builtin_fmaf(re, co, -(im * sn));
-            const float y1 = __builtin_fmaf(re, sn, im * co);
-            acc = __builtin_fmaf(y1, y1, __builtin_fmaf(y0, y0, acc));
-            x[qb][c][2 * p] = y0;
-            x[qb][c][2 * p + 1] = y1;
-          }
-          ssq[c] = acc;
-        }
-        // lanes l and l^32 hold the two halves of one row
-        const float ss = half_pair_sum(tree_sum<NC>(ssq));
-        const float r = __builtin_amdgcn_rsqf(__builtin_fmaf(ss, 1.0f / (float)D, FLT_EPSILON)) * a.scale_log2;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          uint32_t w[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(x[qb][c][2 * i] * r, x[qb][c][2 * i + 1] * r);
-          qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
-        }
-      }
-    } else {
 #pragma unroll
     for (int qb = 0; qb < QW; ++qb) {
       // rows past Tq hold row Tq - 1 (finite, normalised) and are never stored
@@ -449,7 +490,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
         for (int i = 0; i < 4; ++i) w[i] = pack_pair<T>(x[qb][c][2 * i], x[qb][c][2 * i + 1]);
         qf[qb][c] = __builtin_bit_cast(vec8, make_uint4(w[0], w[1], w[2], w[3]));
       }
-    }
     }
   } else {
 #pragma unroll

@@ -44,15 +44,17 @@ __device__ __forceinline__ void rope_rotate(float (&x)[EPL], const float (&cs)[E
 // the pairwise tree over the row padded to a power of two (tree_sum inside the
 // lane, then the xor-1, 2, ... butterfly across lanes), mean = sum / D,
 // r = 1 / sqrt(mean + FLT_EPSILON) with correctly rounded sqrt and divide,
-// y = x * r.  The caller rounds y to the storage dtype.
-template <int EPL, int LPK>
+// y = x * r.  The caller rounds y to the storage dtype.  DPP selects the
+// register-only butterfly (group_sum_dpp), which adds the same pairs in the
+// same order: the same bits without LDS traffic.
+template <int EPL, int LPK, bool DPP = false>
 __device__ __forceinline__ void qk_rms_norm(float (&x)[EPL], int D) {
 #pragma clang fp contract(off)
   float sq[EPL];
 #pragma unroll
   for (int i = 0; i < EPL; ++i) sq[i] = x[i] * x[i];
   float ss = tree_sum<EPL>(sq);
-  ss = group_sum<LPK>(ss);
+  ss = DPP ? group_sum_dpp<LPK>(ss) : group_sum<LPK>(ss);
   const float mean = ss / (float)D;
   const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
 #pragma unroll
