@@ -372,8 +372,8 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     // those of rope_qknorm_kernel at D = 64 (8 elements per lane, 8 lanes per
     // row), so its bits are the same.  Each wave stages its 32 rows (4 KB,
     // 16-byte pieces XOR-swizzled by row) in the second K stage, which nothing
-    // else touches before the barrier that precedes the loop.  (The general
-    // kernel's plain q loads measured faster without the round trip.)
+    // else touches before the barrier that precedes the loop.  (For the
+    // general kernel's plain q loads the round trip measured neutral.)
     const int prow = lane >> 3, ppc = lane & 7;
     auto qswz = [](int r) { return (r >> 1) & 7; };
     uint4 packed[4];
