@@ -79,7 +79,7 @@ struct PrefillArgs {
   int64_t yb, yt, yh;
   int H, Tq, Tk, q_offset;
   int nqb;     // query blocks per (b, h)
-  int nwg;     // total workgroups
+  int nbh;     // B*H
   int win;     // (b, h) pairs per scheduling window
   float scale_log2;  // SDPA scale * log2(e)
   float lazy_raw;    // kLazyLog2 / scale_log2: allowed growth of a row max in raw score units
@@ -280,20 +280,18 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   const int hh = lane >> 5;
   const int r32 = lane & 31;
 
-  // Schedule: the (b, h) pairs go in windows of a.win; inside a window the
-  // blocks run longest query block first (blocks are dispatched in index
-  // order, so long ones start early and short ones fill in at the end), and
+  // Schedule: the (b, h) pairs go in windows of a.win; the grid is
+  // (win, nqb, windows) and block (x, y, z) takes pair z*win + x and query
+  // block nqb - 1 - y.  Blocks are dispatched in linear order
+  // x + win*(y + nqb*z), so inside a window the blocks run longest query
+  // block first (long ones start early, short ones fill in at the end) and
   // the window's K/V stays cache-resident while its query blocks run.  Block
-  // i runs on XCD i % 8: with a.win and B*H multiples of 8 all query blocks of
-  // a (b, h) share one XCD and its L2.
-  const int nbh = a.nwg / a.nqb;
-  const int per_win = a.win * a.nqb;
-  const int win_id = blockIdx.x / per_win;
-  const int wbh0 = win_id * a.win;
-  const int wsize = min(a.win, nbh - wbh0);
-  const int wj = blockIdx.x - win_id * per_win;
-  const int bh = wbh0 + wj % wsize;
-  const int qblk = a.nqb - 1 - wj / wsize;
+  // i runs on XCD i % 8: with a.win a multiple of 8 all query blocks of a
+  // (b, h) share one XCD and its L2.  (No divisions: this grid replaces the
+  // index arithmetic of a 1-D one.)
+  const int bh = blockIdx.z * a.win + blockIdx.x;
+  if (bh >= a.nbh) return;  // the last window's spare columns (whole workgroup, before any barrier)
+  const int qblk = a.nqb - 1 - blockIdx.y;
   const int head = bh % a.H;
   const int64_t b = bh / a.H;
 
@@ -786,7 +784,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 #pragma unroll
   for (int qb = 0; qb < QW; ++qb) {
     // rows past Tq carry finite values and are not stored
-    const float inv = 1.0f / half_pair_sum(l[qb]);
+    const float inv = __builtin_amdgcn_rcpf(half_pair_sum(l[qb]));
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -832,10 +830,10 @@ int launch_prefill(PrefillArgs a, hipStream_t s) {
   constexpr int QW = qw_for<D>();
   constexpr int BM = PrefillCfg<T, D, QW>::BM;
   a.nqb = (a.Tq + BM - 1) / BM;
-  const int64_t nwg = (int64_t)(a.nwg) * a.nqb;  // a.nwg holds B*H on entry
-  DG_REQUIRE(nwg <= 0x7fffffffLL, DG_EINVAL, "prefill: too many workgroups");
-  a.nwg = (int)nwg;
-  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW, ROPE, FT, BND>), dim3((unsigned)a.nwg),
+  const int nwin = (a.nbh + a.win - 1) / a.win;
+  DG_REQUIRE(a.nqb <= 65535 && nwin <= 65535, DG_EINVAL, "prefill: %d query blocks, %d windows, at most 65535 each",
+             a.nqb, nwin);
+  hipLaunchKernelGGL((prefill_mfma_kernel<T, D, QW, ROPE, FT, BND>), dim3((unsigned)a.win, (unsigned)a.nqb, (unsigned)nwin),
                      dim3(PrefillCfg<T, D, QW>::NT), 0, s, a);
   return check_launch("prefill_mfma_kernel");
 }
@@ -851,8 +849,10 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
   if (dtype != DG_BF16 && dtype != DG_F16) return false;
   if (D != 64 && D != 128) return false;
   if (Tq < 16) return false;  // decode and tiny chunks: vector kernel
-  const int64_t nwg = (int64_t)B * H * ((Tq + 127) / 128);
-  if (nwg <= 0 || nwg > 0x7fffffffLL) return false;
+  // grid (window, query blocks, windows): at most 65535 query blocks of 128
+  // and 65535 windows of kPrefillWindow pairs
+  const int64_t nbh = (int64_t)B * H;
+  if (nbh <= 0 || (Tq + 127) / 128 > 65535 || (nbh + kPrefillWindow - 1) / kPrefillWindow > 65535) return false;
   // per-head byte offsets (buffer ranges) are 32-bit signed inside the kernel
   const int64_t span = (int64_t)Tk * (k_st->t > v_st->t ? k_st->t : v_st->t);
   if (span >= (int64_t)1 << 30 || k_st->t < 0 || v_st->t < 0) return false;
@@ -872,7 +872,7 @@ PrefillArgs prefill_args(int B, int H, int Tq, int Tk, const void* q, const dg_s
   a.yb = y_st->b; a.yt = y_st->t; a.yh = y_st->h;
   a.H = H; a.Tq = Tq; a.Tk = Tk;
   a.q_offset = Tk - Tq;
-  a.nwg = B * H;
+  a.nbh = B * H;
   // 64 (b, h) pairs per window: measured best or within 1 % of it from
   // B*H = 64 to 2048 at T = 1024 and 3584, D = 64 and 128
   a.win = B * H < kPrefillWindow ? B * H : kPrefillWindow;
