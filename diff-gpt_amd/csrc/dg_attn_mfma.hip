@@ -264,15 +264,16 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   constexpr bool kPrefillPipe = prefill_pipe<D>();
   constexpr bool kPrefillPrefetch = prefill_prefetch<D>();
 
-  // two ring stages, K and V each in an array of its own: the compiler can
-  // then tell the stage being copied into from the one being read
-  __shared__ __attribute__((aligned(16))) uint16_t ks0[C::TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t vs0[C::TILE];
-  // in the RoPE instances at D = 64 the second K stage is twice as long:
-  // before the first barrier it stages the four waves' query rows (4 KB
-  // each); 40 KB per workgroup still lets four workgroups share a CU's 160 KB
-  __shared__ __attribute__((aligned(16))) uint16_t ks1[(D == 64 && ROPE ? 2 : 1) * C::TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t vs1[C::TILE];
+  // two ring stages, each an array of its own (K tile, then V tile): the
+  // compiler can then tell the stage being copied into from the one being
+  // read.  32 KB per workgroup at D = 64 lets four workgroups share a CU
+  // (measured: with 40 KB at most three were ever resident)
+  __shared__ __attribute__((aligned(16))) uint16_t kv0[2 * C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t kv1[2 * C::TILE];
+  uint16_t* const ks0 = kv0;
+  uint16_t* const vs0 = kv0 + C::TILE;
+  uint16_t* const ks1 = kv1;
+  uint16_t* const vs1 = kv1 + C::TILE;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -369,7 +370,7 @@ void prefill_mfma_kernel(const PrefillArgs a) {
     // vector memory path.)  The exact form's lanes and reduction tree are
     // those of rope_qknorm_kernel at D = 64 (8 elements per lane, 8 lanes per
     // row), so its bits are the same.  Each wave stages its 32 rows (4 KB,
-    // 16-byte pieces XOR-swizzled by row) in the second K stage, which nothing
+    // 16-byte pieces XOR-swizzled by row) in the second stage, which nothing
     // else touches before the barrier that precedes the loop.  (For the
     // general kernel's plain q loads the round trip measured neutral.)
     const int prow = lane >> 3, ppc = lane & 7;
@@ -419,10 +420,10 @@ void prefill_mfma_kernel(const PrefillArgs a) {
         packed[i] = make_uint4(w[0], w[1], w[2], w[3]);
       }
     }
-    // all four waves stage in the one array ks1 (a pointer chosen between two
+    // all four waves stage in the one array kv1 (a pointer chosen between two
     // arrays would leave the compiler unable to tell these accesses from the
     // copies into the first stage, and it would make them wait for those)
-    uint16_t* qst = ks1 + wv * 32 * D;
+    uint16_t* qst = kv1 + wv * 32 * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 8 * i + prow;
