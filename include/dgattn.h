@@ -140,8 +140,9 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * fp16 data ignores the flag and gives dg_attention's y bit for bit).
  * Only the MFMA prefill kernel's shapes are taken (bf16 or
  * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
- * freqs in the data's dtype or fp32): anything else returns DG_EUNSUPPORTED
- * and does nothing, and the caller makes the two calls.
+ * freqs in the data's dtype or fp32, Tq <= 65535 * 128 and B*H <= 65535 * 64,
+ * one head's K and V rows within 2^30 elements): anything else returns
+ * DG_EUNSUPPORTED and does nothing, and the caller makes the two calls.
  */
 DG_API int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype,
                            const void* q, const dg_stride3* q_st,
