@@ -5,11 +5,11 @@
 // (b, h), so a workgroup covers BM = 128*QW queries.  Keys stream through two
 // LDS stages in tiles of BN keys (64 at D = 64, 32 at D = 128; the text below
 // writes BN = 64): every wave copies its share of the next tile
-// straight from global memory into LDS (global_load_lds_dwordx4: no registers,
-// no shuffles) while the current tile is computed, then waits for its own
-// copies and meets the others at one barrier per tile.  K and V tiles are kept
-// row-major with the 16-byte pieces of row r XOR-swizzled (piece_swz), which
-// makes both operand reads below free of bank conflicts.  Both products are
+// straight from global memory into LDS (buffer_load_dwordx4 ... lds: no
+// registers, no shuffles) while the current tile is computed, then waits for
+// its own copies and meets the others at one barrier per tile.  K and V tiles
+// are kept row-major with the 16-byte pieces of row r XOR-swizzled
+// (piece_swz), which makes both operand reads below free of bank conflicts.  Both products are
 // issued transposed so that a lane's statistics all belong to ONE query:
 //
 //   S^T (64 keys x 32 queries) = K (64 x D) . Q^T (D x 32)
