@@ -276,7 +276,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
   // standalone kernel stores it; both waves compute it (same bits)
   auto rotate_q = [&](float (&xq)[EPL], const float (&cs)[EPL], Slice& qs) __attribute__((always_inline)) {
     rope_rotate<T, EPL>(xq, cs);
-    if (a.qknorm) qk_rms_norm<EPL, LPK>(xq, D);
+    if (a.qknorm) qk_rms_norm<EPL, LPK, true>(xq, D);
     pack_row<T, EPL>(qs, xq);
   };
   const FT* fbase = FUSED ? static_cast<const FT*>(a.freqs) + (int64_t)Tc * a.fpos + piece * EPL : nullptr;
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     if constexpr (FUSED) {
       rotate_q(xq, cs, qs);
       rope_rotate<T, EPL>(xk, cs);
-      if (a.qknorm) qk_rms_norm<EPL, LPK>(xk, D);
+      if (a.qknorm) qk_rms_norm<EPL, LPK, true>(xk, D);
       pack_row<T, EPL>(knew, xk);
       // the append (kv_cache.py:108-109)
       if (ovalid && kk == 0) {

@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
     float (&x)[EPL] = xs[w];
     if (w < 2) {
       rope_rotate<T, EPL>(x, cs);
-      if (a.qknorm) qk_rms_norm<EPL, LPK>(x, a.D);
+      if (a.qknorm) qk_rms_norm<EPL, LPK, true>(x, a.D);
     }
     if (active) {
       T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + b * a.db[w] + (int64_t)t * a.dt[w] +
