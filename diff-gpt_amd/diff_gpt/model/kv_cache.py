@@ -53,7 +53,8 @@ class KVCache:
         "pos",
         "shared_prefix",
         "pos_dev",
-        "keys_normed",
+        "_normed",
+        "_exposed",
     )
 
     def __init__(
@@ -82,25 +83,47 @@ class KVCache:
         # step advances both copies.  None in ordinary (eager) use.
         self.pos_dev: torch.Tensor | None = None
         # True while every key below pos was written by the model's attention
-        # (RoPE + QK-norm, mha.py:44-48), i.e. every key row is RMS-normalised;
-        # the prefill kernel then runs its softmax without a running maximum.
-        # insert_kv with caller-supplied keys clears it.
-        self.keys_normed = True
+        # (RoPE + QK-norm, mha.py:44-48); insert_kv with caller-supplied keys
+        # clears it.  See keys_normed.
+        self._normed = True
+        # True once the cache tensor was handed to or taken from a caller
+        self._exposed = False
+
+    @property
+    def keys_normed(self) -> bool:
+        """True while every key row below pos is known to be RMS-normalised:
+        each was written by the model's attention (RoPE + QK-norm,
+        mha.py:44-48), and the cache tensor never passed through the
+        ``kv_cache`` attribute, whose holder may write keys into it in place
+        at any later time.  The prefill kernel then runs its softmax without a
+        running maximum; otherwise it keeps one."""
+        return self._normed and not self._exposed
+
+    @keys_normed.setter
+    def keys_normed(self, value: bool) -> None:
+        self._normed = bool(value)
 
     # -- the reference's tensor ------------------------------------------------
     @property
     def kv_cache(self) -> torch.Tensor:
         """The (L, 2, B, H, Tcap, D) cache tensor (kv_cache.py:25); a cache whose
-        prefix lives in separate pages is expanded into it first."""
-        if self._prefix_kv is not None:
-            self._expand()
-        return self._kv
+        prefix lives in separate pages is expanded into it first.  The caller
+        may write into it, so from here on keys_normed is False."""
+        self._exposed = True
+        return self._tensor()
 
     @kv_cache.setter
     def kv_cache(self, value: torch.Tensor) -> None:
         self._kv = value
         self._prefix_kv = None
-        self.keys_normed = False  # contents from the caller
+        self._exposed = True  # contents from the caller
+
+    def _tensor(self) -> torch.Tensor:
+        """The (L, 2, B, H, Tcap, D) cache tensor for the library's own reads
+        and writes (prefix pages expanded first); keys_normed is unaffected."""
+        if self._prefix_kv is not None:
+            self._expand()
+        return self._kv
 
     @property
     def own_start(self) -> int:
@@ -182,7 +205,7 @@ class KVCache:
             group = sb if ob == 1 else 1
         assert st >= ot, f"Sequence length mismatch: {st} < {ot}"
 
-        src = other.kv_cache
+        src = other._tensor()
         _native.require_device("KVCache.prefill", src)
         n = other.pos
         ops = _native.ops()
@@ -255,7 +278,7 @@ class KVCache:
 
     def layer_views(self, layer_idx: int, t1: int) -> tuple[torch.Tensor, torch.Tensor]:
         """(B,H,t1,D) views of layer ``layer_idx``'s keys and values."""
-        cache = self.kv_cache
+        cache = self._tensor()
         return (
             cache[layer_idx, 0, :, :, :t1, :],
             cache[layer_idx, 1, :, :, :t1, :],

@@ -146,7 +146,7 @@ class MultiHeadAttention(nn.Module):
             keys_normed = True
         else:
             t0, t1 = kv_cache.ensure_window(T, k.dtype, k.device)
-            cache = kv_cache.kv_cache
+            cache = kv_cache._tensor()
             if cache.dtype != k.dtype:
                 raise TypeError(
                     f"KV cache holds {cache.dtype} but the layer computes in {k.dtype}"

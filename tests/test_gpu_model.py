@@ -259,6 +259,44 @@ def test_mha_bf16_prefill_fused_rope_equals_two_calls(dev, monkeypatch, D):
         assert ((b.float() - p.float()).abs().max() / p.float().abs().max()).item() <= 2e-2
 
 
+def test_mha_bf16_prefill_over_caller_written_keys(dev, monkeypatch):
+    """Keys a caller writes into the cache through its kv_cache tensor carry
+    no norm, so the continuation prefill must keep a running maximum: keys 64
+    times a normalised row put scores near 2^9 in log2 units, where the
+    bounded form's exp2 would overflow.  The result is finite and has the bits
+    of the two-call path (rotate q, then the running-maximum kernel)."""
+    from diff_gpt import _native
+    from diff_gpt.model.kv_cache import KVCache
+    from diff_gpt.model.mha import MultiHeadAttention
+
+    torch.manual_seed(5)
+    H, D = 2, 64
+    m = MultiHeadAttention(H * D, H, 0).to(dev).to(torch.bfloat16).eval()
+    x = torch.randn(2, 48, H * D, device=dev).to(torch.bfloat16)
+    fc = _fc(48, D, dev, seed=5)
+    real = _native.prefill_rope_
+    flags = []
+
+    def spy(q, freqs, k, v, y, scale, qknorm, keys_normed=False):
+        flags.append(keys_normed)
+        return real(q, freqs, k, v, y, scale, qknorm, keys_normed)
+
+    def run():
+        kv = KVCache(batch_size=2, num_heads=H, seq_len=64, head_dim=D, num_layers=1)
+        with torch.no_grad():
+            m(x[:, :20], fc[:, :20], kv)
+            kv.kv_cache[0, 0, :, :, :20] *= 64
+            return m(x[:, 20:], fc[:, 20:], kv)
+
+    monkeypatch.setattr(_native, "prefill_rope_", spy)
+    got = run()
+    assert flags == [True, False]
+    monkeypatch.setattr(_native, "prefill_rope_", lambda *a, **k: False)
+    plain = run()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, plain)
+
+
 def test_block_kv_step_consistency(dev):
     # test_block.py:129-166 (AttnRes active, layers_per_block=2)
     from diff_gpt.model.block import Block

@@ -61,6 +61,26 @@ def test_kv_cache_initial_state():
     assert c.get_pos() == 0
 
 
+def test_kv_cache_keys_normed_withdrawn_once_the_tensor_is_exposed():
+    # the bounded prefill softmax relies on keys_normed; a caller holding the
+    # cache tensor may write arbitrary keys into it at any time, reset included
+    c = KVCache(1, 2, 8, 4, 1)
+    assert c.keys_normed
+    c._tensor()
+    assert c.keys_normed  # the library's own accessor leaves it
+    c.kv_cache
+    assert not c.keys_normed
+    c.reset()
+    assert not c.keys_normed
+    d = KVCache(1, 2, 8, 4, 1)
+    d.kv_cache = torch.zeros(1, 2, 1, 2, 8, 4)
+    assert not d.keys_normed
+    e = KVCache(1, 2, 8, 4, 1)
+    e.keys_normed = False
+    e.reset()
+    assert e.keys_normed  # the model rewrites every position from 0
+
+
 def test_kv_cache_prefill_assertions():
     a, b = KVCache(3, 2, 20, 4, 1), KVCache(1, 2, 10, 4, 1)
     with pytest.raises(AssertionError, match="Cannot prefill with a None KV cache"):
