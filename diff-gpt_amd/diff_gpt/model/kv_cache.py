@@ -83,8 +83,7 @@ class KVCache:
         # step advances both copies.  None in ordinary (eager) use.
         self.pos_dev: torch.Tensor | None = None
         # True while every key below pos was written by the model's attention
-        # (RoPE + QK-norm, mha.py:44-48); insert_kv with caller-supplied keys
-        # clears it.  See keys_normed.
+        # (RoPE + QK-norm, mha.py:44-48).  See keys_normed.
         self._normed = True
         # True once the cache tensor was handed to or taken from a caller
         self._exposed = False
@@ -94,8 +93,8 @@ class KVCache:
         """True while every key row below pos is known to be RMS-normalised:
         each was written by the model's attention (RoPE + QK-norm,
         mha.py:44-48), and the cache tensor never passed through the
-        ``kv_cache`` attribute, whose holder may write keys into it in place
-        at any later time.  The prefill kernel then runs its softmax without a
+        ``kv_cache`` attribute or ``insert_kv`` (which returns views of it),
+        whose holder may write keys into it in place at any later time.  The prefill kernel then runs its softmax without a
         running maximum; otherwise it keeps one."""
         return self._normed and not self._exposed
 
@@ -323,7 +322,8 @@ class KVCache:
             v = v.to(cache.dtype)
         _native.ops().copy4d(k, cache[layer_idx, 0, :, :, t0:t1, :])
         _native.ops().copy4d(v, cache[layer_idx, 1, :, :, t0:t1, :])
-        self.keys_normed = False  # keys from the caller: no norm to rely on
+        # keys from the caller, and views of the cache handed back: no norm to rely on
+        self._exposed = True
         key_view, value_view = self.layer_views(layer_idx, t1)
         self.advance(layer_idx, t1)
         return key_view, value_view

@@ -75,6 +75,8 @@ def test_kv_cache_keys_normed_withdrawn_once_the_tensor_is_exposed():
     d = KVCache(1, 2, 8, 4, 1)
     d.kv_cache = torch.zeros(1, 2, 1, 2, 8, 4)
     assert not d.keys_normed
+    d.reset()
+    assert not d.keys_normed
     e = KVCache(1, 2, 8, 4, 1)
     e.keys_normed = False
     e.reset()
