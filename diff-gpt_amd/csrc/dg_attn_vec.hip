@@ -313,7 +313,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, con
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int64_t kTargetWaves = 8192;  // 256 CUs x 32 resident waves
+// Key splits aim at 4096 waves: 16 per CU, all resident from the start (the
+// kernel takes 72 VGPRs, room for 7 waves per SIMD).  Measured at the
+// configs[3] and configs[4] decode shapes: 1.3-2.5 % faster than 8192 waves
+// of 4-slot trips (144 VGPRs, 3 waves per SIMD, the grid in 2.7 rounds), and
+// within 1-3 % of a bare kernel streaming the same pages.
+constexpr int64_t kTargetWaves = 4096;
 constexpr int kMinSplitKeys = 128;
 constexpr int kMaxSplits = 64;
 
@@ -341,28 +346,20 @@ int pick_splits(int64_t base_units, int Tk) {
   return (int)n;
 }
 
-// Key slots per trip.  16-byte lane slices: 2 slots when a unit's keys end
-// within one or two trips (fewer registers, more resident waves) and 4 above
-// 128 keys (more loads in flight per wave: cfg4's 230-key splits run at 61 %
-// of HBM peak instead of 58 %, cfg1 and cfg3 unchanged).  Narrower slices
-// double both.
-constexpr int kShortRowKeys = 128;
+// Key slots per trip: 2 with 16-byte lane slices, 4 with narrower ones (the
+// same bytes in flight per wave).  Two register sets of two slots keep the
+// kernel at 72 VGPRs.
 template <typename T, int EPL>
-constexpr int slots_for(bool long_rows) {
-  const int wide = EPL * (int)sizeof(T) >= 16 ? 1 : 2;
-  return (long_rows ? 4 : 2) * wide;
+constexpr int slots_for() {
+  return EPL * (int)sizeof(T) >= 16 ? 2 : 4;
 }
 
 template <typename T, int DPAD, int EPL>
 int launch_attn(AttnArgs a, hipStream_t s) {
   const int64_t blocks = (a.units + 3) / 4;
   DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-  if (a.split_len > kShortRowKeys)
-    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(true)>), dim3((unsigned)blocks),
-                       dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(false)>), dim3((unsigned)blocks),
-                       dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>()>), dim3((unsigned)blocks), dim3(256), 0,
+                     s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
   // combine: C chunks of 4 floats per row times SP split slots, SP <= nsplit

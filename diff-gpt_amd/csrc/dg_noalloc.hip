@@ -20,9 +20,9 @@
 #include <mutex>
 
 // Largest key-split workspace of a decode step with head_dim <= 128: splits
-// are used only while B*H < 8192 (kTargetWaves), so B*H*splits < 2*8192 units
-// of (128 + 2) floats, i.e. < 8.6 MB.  head_dim 256 fits while B*H*splits <=
-// 16260; larger requests are rejected.
+// are used only while B*H < 4096 (kTargetWaves), so B*H*splits < 2*4096 units
+// of (128 + 2) floats, i.e. < 4.3 MB.  head_dim 256 fits while B*H*splits <=
+// 16260, which holds as well; larger requests are rejected.
 constexpr size_t kStaticScratchBytes = size_t(16) << 20;
 
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
