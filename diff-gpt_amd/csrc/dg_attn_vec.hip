@@ -52,9 +52,15 @@ struct AttnArgs {
 };
 
 constexpr float kVecLazyLog2 = 8.0f;
+// Key splits of one (b, h, i) run as the waves of one workgroup and merge in
+// LDS when there are at most this many; more go through the workspace and
+// attn_combine_kernel.
+constexpr int kMaxBlockSplits = 16;
 
-template <typename T, int DPAD, int EPL, int U>
-__global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
+// MERGE: the workgroup's nsplit waves are the key splits of one (b, h, i)
+// (blockDim = 64 * nsplit); otherwise a workgroup holds 4 independent units.
+template <typename T, int DPAD, int EPL, int U, bool MERGE>
+__global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_kernel(const AttnArgs a) {
   constexpr int LPK = DPAD / EPL;
   constexpr int KPI = 64 / LPK;
   constexpr int STEP = KPI * U;  // keys per trip
@@ -67,8 +73,10 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
   int blk = blockIdx.x;
   if ((gridDim.x & 7) == 0) blk = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
   // wave-uniform unit index (the host keeps units below 2^31)
-  const int unit = blk * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (unit >= a.units) return;  // whole wave exits; kernel has no barriers
+  const int unit = blk * (int)(blockDim.x >> 6) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if constexpr (!MERGE) {
+    if (unit >= a.units) return;  // whole wave exits; no barrier follows
+  }
 
   const int sub = lane % LPK;
   const int grp = lane / LPK;
@@ -202,6 +210,42 @@ __global__ __launch_bounds__(256) void attn_vec_kernel(const AttnArgs a) {
 #pragma unroll
   for (int e = 0; e < EPL; ++e) acc[e] = sum_over_groups<LPK>(acc[e]);
 
+  if constexpr (MERGE) {
+    // each wave (split) leaves its partial in LDS; after the barrier the
+    // workgroup's threads take the output dims in pairs and merge the splits:
+    // weights exp2((m_j - M) c) against the largest offset M, as the combine
+    // kernel does.  Every wave reaches the barrier (no early exit above).
+    __shared__ float lds_acc[kMaxBlockSplits][DPAD];
+    __shared__ float lds_ml[kMaxBlockSplits][2];
+    if (grp == 0 && active) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) lds_acc[split][d0 + e] = acc[e];
+    }
+    if (lane == 0) {
+      lds_ml[split][0] = m;
+      lds_ml[split][1] = l;
+    }
+    __syncthreads();
+    const int ns = a.nsplit;
+    float M = kNegInf;
+    for (int j = 0; j < ns; ++j) M = fmaxf(M, lds_ml[j][0]);  // split 0 holds key 0: M is finite
+    T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh;
+    for (int d = 2 * (int)threadIdx.x; d < a.D; d += 2 * (int)blockDim.x) {
+      float L = 0.f, o[2] = {0.f, 0.f};
+      for (int j = 0; j < ns; ++j) {
+        const float mj = lds_ml[j][0];
+        const float w = mj == kNegInf ? 0.f : __builtin_amdgcn_exp2f((mj - M) * c);
+        L += w * lds_ml[j][1];
+        o[0] += w * lds_acc[j][d];
+        o[1] += w * lds_acc[j][d + 1];
+      }
+      const float inv = 1.0f / L;
+      o[0] *= inv;
+      o[1] *= inv;
+      store_vec<T, 2>(yp + d, o);  // D is even; y is aligned to a pair (host check)
+    }
+    return;
+  }
   if (grp != 0 || !active) return;
   if (a.nsplit == 1) {
     const float inv = 1.0f / l;
@@ -356,10 +400,18 @@ constexpr int slots_for() {
 
 template <typename T, int DPAD, int EPL>
 int launch_attn(AttnArgs a, hipStream_t s) {
+  if (a.nsplit > 1 && a.nsplit <= kMaxBlockSplits) {
+    // one workgroup per (b, h, i), one wave per key split, merged in LDS
+    const int64_t blocks = a.units / a.nsplit;
+    DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
+    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), true>), dim3((unsigned)blocks),
+                       dim3(64 * a.nsplit), 0, s, a);
+    return check_launch("attn_vec_kernel");
+  }
   const int64_t blocks = (a.units + 3) / 4;
   DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>()>), dim3((unsigned)blocks), dim3(256), 0,
-                     s, a);
+  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), false>), dim3((unsigned)blocks),
+                     dim3(256), 0, s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
   // combine: C chunks of 4 floats per row times SP split slots, SP <= nsplit
@@ -413,7 +465,7 @@ int vec_attention_splits(int B, int H, int Tq, int Tk, int D) {
 
 size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
   const int ns = vec_attention_splits(B, H, Tq, Tk, D);
-  if (ns <= 1) return 0;
+  if (ns <= kMaxBlockSplits) return 0;  // merged inside the workgroup
   return (size_t)B * H * Tq * ns * (size_t)(next_pow2(D) + 2) * sizeof(float);
 }
 
@@ -464,15 +516,16 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
 
   int ns = vec_attention_splits(B, H, Tq, Tk, D);
   const size_t need = vec_attention_workspace(B, H, Tq, Tk, D);
-  if (ns > 1 && (workspace == nullptr || workspace_bytes < need)) {
+  if (ns > kMaxBlockSplits && (workspace == nullptr || workspace_bytes < need)) {
     DG_REQUIRE(workspace == nullptr, DG_EWORKSPACE,
                "attention: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
-    ns = 1;  // no workspace: single pass over all keys
+    ns = kMaxBlockSplits;  // no workspace: as many splits as one workgroup merges
   }
   a.nsplit = ns;
   a.split_len = ns == 1 ? Tk : (((Tk + ns - 1) / ns + 15) / 16) * 16;
-  a.part = ns == 1 ? nullptr : static_cast<float*>(workspace);
-  DG_REQUIRE(ns == 1 || aligned(workspace, 16), DG_EINVAL, "attention: workspace must be 16-byte aligned");
+  const bool global_splits = ns > kMaxBlockSplits;
+  a.part = global_splits ? static_cast<float*>(workspace) : nullptr;
+  DG_REQUIRE(!global_splits || aligned(workspace, 16), DG_EINVAL, "attention: workspace must be 16-byte aligned");
   a.units = (int64_t)B * H * Tq * ns;
   DG_REQUIRE(a.units < ((int64_t)1 << 31), DG_EINVAL, "attention: B*H*Tq*splits must be below 2^31");
 

@@ -19,11 +19,12 @@
 
 #include <mutex>
 
-// Largest key-split workspace of a decode step with head_dim <= 128: splits
-// are used only while B*H < 4096 (kTargetWaves), so B*H*splits < 2*4096 units
-// of (128 + 2) floats, i.e. < 4.3 MB.  head_dim 256 fits while B*H*splits <=
-// 16260, which holds as well; larger requests are rejected.
-constexpr size_t kStaticScratchBytes = size_t(16) << 20;
+// Largest key-split workspace of a decode step: up to 16 splits merge inside
+// the workgroup and need none; more happen only while B*H < 256 (they aim at
+// 4096 waves), so B*H*splits < 4096 + 255 partials of at most 256 + 2
+// floats: < 4.5 MB for any head_dim the library takes.  The check below
+// stays as a guard.
+constexpr size_t kStaticScratchBytes = size_t(8) << 20;
 
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 

@@ -283,10 +283,10 @@ DG_API int dg_decode_step(int B, int H, int D, int dtype,
  * under HIP graph capture that must not allocate, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
  * dg_decode_step; the key-split partials live in a static device array of
- * dg_decode_step_noalloc_scratch_bytes() bytes (16 MiB) that the library
- * holds on every GPU it runs on until the process ends.  Sizes whose split
- * workspace (dg_decode_step_workspace_size) exceeds it return DG_EWORKSPACE
- * before any GPU work; head_dim <= 128 always fits.  It allocates nothing
+ * dg_decode_step_noalloc_scratch_bytes() bytes (8 MiB) that the library
+ * holds on every GPU it runs on until the process ends.  Every size fits:
+ * the split workspace (dg_decode_step_workspace_size) is at most 4.5 MB; a
+ * size beyond the array would return DG_EWORKSPACE before any GPU work.  It allocates nothing
  * and frees nothing.  All calls on one GPU share that array: calls that
  * overlap on one GPU (other streams, other host threads) race and must be
  * serialised by the caller.  The stream must belong to the current device.

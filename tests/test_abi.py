@@ -118,9 +118,11 @@ def test_workspace_sizes():
     lib = _native.lib()
     # many rows: no split, no workspace
     assert lib.dg_attention_workspace_size(6400, 4, 1, 144, 16, 0) == 0
-    # few long rows (cfg4 decode): split partials of (D + 2) fp32 per unit
-    ws = lib.dg_attention_workspace_size(64, 8, 1, 3680, 128, 1)
-    assert ws > 0 and ws % (130 * 4) == 0
+    # cfg4 decode: 8 key splits per (row, head), merged inside the workgroup
+    assert lib.dg_attention_workspace_size(64, 8, 1, 3680, 128, 1) == 0
+    # very few long rows: more than 16 splits, partials of (D + 2) fp32 per unit
+    ws = lib.dg_attention_workspace_size(1, 8, 1, 8192, 128, 1)
+    assert ws == 8 * 64 * 130 * 4
     # prefill never splits
     assert lib.dg_attention_workspace_size(1, 1, 512, 512, 64, 1) == 0
 

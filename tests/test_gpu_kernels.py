@@ -309,26 +309,33 @@ def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
     assert bool((y == 7.0).all())
 
 
-def test_decode_without_workspace_matches_split(dev):
-    """A NULL workspace forces the single-pass path; both agree with fp64."""
+@pytest.mark.parametrize("Tk", [2048, 4096])
+def test_decode_split_paths_agree_with_f64(dev, Tk):
+    """Key splits of one (row, head) merge inside its workgroup up to 16 of
+    them, with no workspace (B*H = 32 at Tk = 2048: 16 splits); more go
+    through the workspace and the combine kernel (Tk = 4096: 32 splits) or,
+    given no workspace, drop to 16 merged in the workgroup.  Every path
+    agrees with fp64."""
     from diff_gpt import _native
 
-    B, H, Tk, D = 4, 8, 2048, 64
+    B, H, D = 4, 8, 64
     q = _randn((B, 1, H, D), 1, "bf16").to(dev)
     k = _randn((B, Tk, H, D), 2, "bf16").to(dev)
     v = _randn((B, Tk, H, D), 3, "bf16").to(dev)
     lib = _native.lib()
-    assert lib.dg_attention_workspace_size(B, H, 1, Tk, D, 1) > 0
-    y_split = _native.ops().attention(q, k, v, 0.125)
-    y_single = torch.empty_like(q)
-    st = [ctypes.pointer(_native._bthd_strides(t)) for t in (q, k, v, y_single)]
+    assert (lib.dg_attention_workspace_size(B, H, 1, Tk, D, 1) > 0) == (Tk == 4096)
+    y_ws = _native.ops().attention(q, k, v, 0.125)  # with the workspace the library asks for
+    y_null = torch.empty_like(q)
+    st = [ctypes.pointer(_native._bthd_strides(t)) for t in (q, k, v, y_null)]
     rc = lib.dg_attention(B, H, 1, Tk, D, 1, ctypes.c_void_p(q.data_ptr()), st[0],
                           ctypes.c_void_p(k.data_ptr()), st[1], ctypes.c_void_p(v.data_ptr()), st[2],
-                          ctypes.c_void_p(y_single.data_ptr()), st[3], 0.125, None, 0,
+                          ctypes.c_void_p(y_null.data_ptr()), st[3], 0.125, None, 0,
                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0
+    if Tk == 2048:
+        assert torch.equal(y_ws, y_null)  # one path: no workspace involved
     ref = on.attention_f64(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(), 0.125)
-    for y in (y_split, y_single):
+    for y in (y_ws, y_null):
         err = np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max()
         assert err <= 2e-2
 
@@ -340,7 +347,7 @@ GROUPED = [  # (B, group, H, prefix, Tk, D)
 ]
 # Groups of >= 16 rows with head_dim 16 / 32 take the matrix-core kernel
 # (dg_attn_shared.hip) whenever the vector kernel would not split the keys
-# (Tk < 256, or B*H >= 8192): cfg1 (series of 100 rows), a ragged last group,
+# (Tk < 256, or B*H >= 4096): cfg1 (series of 100 rows), a ragged last group,
 # a prefix not a multiple of 16 or spanning several 64-key chunks, one own
 # key, many own keys, no own key at all.
 GROUPED_MFMA = [
@@ -351,7 +358,8 @@ GROUPED_MFMA = [
     (40, 40, 2, 5, 250, 16),
     (32, 16, 2, 50, 50, 32),
     (17, 17, 1, 200, 250, 32),
-    (1100, 100, 8, 64, 260, 16),  # B*H >= 8192: no key splits at Tk >= 256 either
+    (1100, 100, 8, 64, 260, 16),  # B*H >= 4096: no key splits at Tk >= 256 either
+    (520, 100, 8, 64, 300, 16),   # B*H = 4160, just past the split threshold
 ]
 
 
