@@ -113,8 +113,11 @@ DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
  * scale is the SDPA scale (the reference uses the default 1/sqrt(D)).
  *
  * workspace: split-KV partials; dg_attention_workspace_size() gives the bytes
- * needed for these sizes (0 when no split is used).  With workspace == NULL
- * the library uses no split (always correct, slower for few long rows).
+ * needed for these sizes: 0 unless a single-token decode splits the keys of
+ * a (b, h) over more than 16 workgroups' waves (B*H < 256 with long rows;
+ * up to 16 splits merge inside one workgroup and need none).  With
+ * workspace == NULL such a launch uses 16 splits merged in the workgroup
+ * (always correct, slower for very few long rows).
  */
 DG_API size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int D, int dtype);
 
@@ -261,7 +264,7 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
  * two-call result within fp32 rounding (the new key is accumulated last).
  * Other shapes run the two calls, with the rotated q staged in y.  The
  * workspace (dg_decode_step_workspace_size) serves the second call's key
- * splits; NULL runs it without splits.
+ * splits beyond 16 per (b, h); NULL caps them at 16.
  */
 DG_API size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype);
 
@@ -286,8 +289,8 @@ DG_API int dg_decode_step(int B, int H, int D, int dtype,
  * dg_decode_step_noalloc_scratch_bytes() bytes (8 MiB) that the library
  * holds on every GPU it runs on until the process ends.  Every size fits:
  * the split workspace (dg_decode_step_workspace_size) is at most 4.5 MB; a
- * size beyond the array would return DG_EWORKSPACE before any GPU work.  It allocates nothing
- * and frees nothing.  All calls on one GPU share that array: calls that
+ * size beyond the array would return DG_EWORKSPACE before any GPU work.
+ * It allocates nothing and frees nothing.  All calls on one GPU share that array: calls that
  * overlap on one GPU (other streams, other host threads) race and must be
  * serialised by the caller.  The stream must belong to the current device.
  */
