@@ -118,6 +118,11 @@ struct OwnCfg {
   static constexpr int STEP = UO * KPQ;           // keys per row and register set
 };
 
+template <int N>
+struct IntConst {
+  static constexpr int value = N;
+};
+
 // Lane `src` of the wave's value x (ds_bpermute: a gather over the wave).
 __device__ __forceinline__ float lane_get(float x, int src) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute(src << 2, __float_as_int(x)));
@@ -357,17 +362,29 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
 #pragma unroll
     for (int u = 0; u < UO; ++u) add_key(sv[u], vs[u], moff);
   };
-  // whole rounds of NSW sets, so that the loop body has one path: each set
-  // is refilled with the set NSW further on once it has been consumed
-  auto own_stream = [&](const Slice& qs) __attribute__((always_inline)) {
-    const int nsets = Tc > P ? (Tc - P + STEP - 1) / STEP : 0;
-    for (int r0 = 0; r0 < nsets; r0 += NSW) {
-#pragma unroll
-      for (int k = 0; k < NSW; ++k) {
-        const int i = r0 + k;
-        if (i < nsets) process(kr[k], vr[k], P + i * STEP, qs);
-        load_set(k, i + NSW);
-      }
+  // Sets 0 and 1 are in flight on entry (nsets >= 2).  Rounds that refill
+  // both sets run while sets i + 2 and i + 3 exist; the last two or three
+  // sets are then consumed with at most one refill.  No load is issued for
+  // a set past the last key: such loads touch no memory but still take the
+  // CU's address-unit issue slots, which every wave of the CU shares.  Each
+  // path issues a fixed number of loads, so the compiler's wait counts stay
+  // exact (a data-dependent number would make it wait for every load).
+  static_assert(NSW == 2, "the own-key stream is written for two register sets");
+  auto own_stream = [&](const Slice& qs, int nsets) __attribute__((always_inline)) {
+    int i = 0;
+    for (; i + 2 * NSW <= nsets; i += NSW) {
+      process(kr[0], vr[0], P + i * STEP, qs);
+      load_set(0, i + 2);
+      process(kr[1], vr[1], P + (i + 1) * STEP, qs);
+      load_set(1, i + 3);
+    }
+    process(kr[0], vr[0], P + i * STEP, qs);
+    if (nsets - i == 3) {
+      load_set(0, i + 2);
+      process(kr[1], vr[1], P + (i + 1) * STEP, qs);
+      process(kr[0], vr[0], P + (i + 2) * STEP, qs);
+    } else {
+      process(kr[1], vr[1], P + (i + 1) * STEP, qs);
     }
   };
   // wave 1's partial to LDS: row orow's offset, sum and weighted values
@@ -576,40 +593,51 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     }
   } else {
     // --- wave 1: own keys on the vector ALUs; fused: the new token -----------------
-    Slice qs;
-    Slice knew, vnew;  // fused: the appended key and value
-    float xq[EPL], xk[EPL], cs[EPL];
-    if constexpr (FUSED) {
-      load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
-      load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
-      load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
-      load_vec<FT, EPL>(fbase, cs);
-    } else {
-      load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < NSW; ++k) load_set(k, k);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (FUSED) {
-      rotate_q(xq, cs, qs);
-      rope_rotate<T, EPL>(xk, cs);
-      if (a.qknorm) qk_rms_norm<EPL, LPK, true>(xk, D);
-      pack_row<T, EPL>(knew, xk);
-      // the append (kv_cache.py:108-109)
-      if (ovalid && kk == 0) {
-        store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
-        store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
+    // One path per number of register sets issued up front (wave-uniform):
+    // the query, projection and table loads are issued before the sets, and
+    // their waits count the sets issued after them.
+    const int nsets = Tc > P ? (Tc - P + STEP - 1) / STEP : 0;
+    auto own_wave = [&](auto ns) __attribute__((always_inline)) {
+      constexpr int NS = decltype(ns)::value;
+      Slice qs;
+      Slice knew, vnew;  // fused: the appended key and value
+      float xq[EPL], xk[EPL], cs[EPL];
+      if constexpr (FUSED) {
+        load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
+        load_vec<T, EPL>(static_cast<const T*>(a.kp) + bo * a.kpb + (int64_t)h * a.kph + piece * EPL, xk);
+        load_row<T, EPL>(vnew, static_cast<const T*>(a.vp) + bo * a.vpb + (int64_t)h * a.vph + piece * EPL);
+        load_vec<FT, EPL>(fbase, cs);
+      } else {
+        load_row<T, EPL>(qs, qbase + bo * a.qb + piece * EPL);
       }
-    }
-    own_stream(qs);
-    if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
-      const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
-      const float sn = kk == 0 ? dot : kNegInf;
-      raise_offset(sn);
-      add_key(sn, vnew, mo * cl);
-    }
-    hand_over();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < NS; ++k) load_set(k, k);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (FUSED) {
+        rotate_q(xq, cs, qs);
+        rope_rotate<T, EPL>(xk, cs);
+        if (a.qknorm) qk_rms_norm<EPL, LPK, true>(xk, D);
+        pack_row<T, EPL>(knew, xk);
+        // the append (kv_cache.py:108-109)
+        if (ovalid && kk == 0) {
+          store_row<T, EPL>(const_cast<T*>(kbase) + bo * a.kb + (int64_t)Tc * kt + piece * EPL, knew);
+          store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
+        }
+      }
+      if constexpr (NS == 2) own_stream(qs, nsets);
+      if constexpr (NS == 1) process(kr[0], vr[0], P, qs);
+      if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
+        const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
+        const float sn = kk == 0 ? dot : kNegInf;
+        raise_offset(sn);
+        add_key(sn, vnew, mo * cl);
+      }
+      hand_over();
+    };
+    if (nsets >= 2) own_wave(IntConst<2>{});
+    else if (nsets == 1) own_wave(IntConst<1>{});
+    else own_wave(IntConst<0>{});
   }
   __syncthreads();
   if (role == 1) return;
