@@ -433,6 +433,11 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (300, 100, 4, 96, 120, 16, 144),  # cfg1 series: one launch
     (70, 16, 2, 33, 69, 32, 80),      # D = 32, prefix not a multiple of 16
     (45, 20, 3, 150, 150, 16, 160),   # no cached own key: the new one only
+    # own-key register sets of 4 (fp32) / 8 (16-bit) keys at D = 16: one set,
+    # two sets, and a refill round then two sets (fp32) / two sets (16-bit)
+    (40, 20, 2, 64, 66, 16, 80),
+    (40, 20, 2, 64, 71, 16, 80),
+    (40, 20, 2, 64, 79, 16, 96),
     (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: two launches
     (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): two launches
 ]
