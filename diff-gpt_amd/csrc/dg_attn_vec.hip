@@ -21,9 +21,10 @@
 // only when a score exceeds it by more than kLazyLog2/c, so probabilities stay
 // <= 2^kLazyLog2 and the rescale of (l, acc) is skipped on most trips; the
 // result is the same function.  Because m is common to all KPI lane groups,
-// they merge at the end by plain register sums of l and acc.  With several
-// key splits the unnormalised partials (acc, m, l) go to the caller's
-// workspace and attn_combine_kernel merges them.
+// they merge at the end by plain register sums of l and acc.  With key
+// splits, up to 16 splits of one (b, h, i) are the waves of one workgroup
+// and merge their unnormalised partials (acc, m, l) in LDS; more go to the
+// caller's workspace and attn_combine_kernel merges them.
 #include "dg_common.h"
 
 namespace dg {
