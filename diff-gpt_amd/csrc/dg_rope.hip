@@ -44,65 +44,85 @@ struct RopeArgs {
 // One row (b,t,h) of D elements is owned by LPK = DPAD/EPL consecutive lanes,
 // each holding EPL consecutive elements (EPL even, so a (re, im) pair never
 // straddles lanes).  Lanes whose slice starts at or beyond D (only when D is
-// not a power of two) hold zeros and store nothing.
-template <typename T, typename FT, int DPAD, int EPL>
+// not a power of two) hold zeros and store nothing.  A lane group takes RPT
+// rows, RPB apart (so that each wave instruction still covers consecutive
+// rows), and issues every load of them before any arithmetic: RPT times the
+// bytes in flight per wave, which a single row per lane leaves too few of to
+// keep HBM busy.  Each row's arithmetic is the same whatever RPT is.
+template <typename T, typename FT, int DPAD, int EPL, int RPT>
 __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPK = DPAD / EPL;
   static_assert(LPK >= 1 && LPK <= 64 && (EPL % 2) == 0, "row mapping");
-  constexpr int ROWS_PER_BLOCK = 256 / LPK;
+  constexpr int RPB = 256 / LPK;  // rows of a block in one pass
 
   const int sub = threadIdx.x % LPK;
-  const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / LPK;
-  if (row >= a.rows) return;  // a whole lane group leaves together; no barriers follow
+  const int64_t row0 = (int64_t)blockIdx.x * RPB * RPT + threadIdx.x / LPK;
+  if (row0 >= a.rows) return;  // a whole lane group leaves together; no barriers follow
   int64_t pos = 0;
   if (a.pos_dev != nullptr) {  // uniform over the grid
     pos = *a.pos_dev;
     if (pos < a.min_pos || pos >= a.max_pos) return;
   }
-
-  // the host keeps B*T*H below 2^31: 32-bit division
-  const uint32_t row32 = (uint32_t)row;
-  const int h = (int)(row32 % (uint32_t)a.H);
-  const uint32_t bt = row32 / (uint32_t)a.H;
-  const int t = (int)(bt % (uint32_t)a.T);
-  const int64_t b = (int64_t)(bt / (uint32_t)a.T);
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
 
-  float cs[EPL];  // (cos, sin) of the EPL/2 pairs of this lane, interleaved
-  if (active) {
-    const FT* f = static_cast<const FT*>(a.freqs) + pos * a.fpos + b * a.fb + (int64_t)t * a.ft +
-                  (int64_t)h * a.fh + d0;
-    load_vec<FT, EPL>(f, cs);
-  }
-
-  // all three sources are read before anything is stored: the destinations
-  // may alias them as far as the compiler knows, so this order keeps the
-  // loads of q, k and v in flight together
-  float xs[3][EPL];
+  // all sources of all RPT rows are read before anything is stored: the
+  // destinations may alias them as far as the compiler knows, so this order
+  // keeps every load in flight together
+  RowRegs<FT, EPL> cr[RPT];      // (cos, sin) of the lane's EPL/2 pairs, interleaved
+  RowRegs<T, EPL> xr[3][RPT];
+  int64_t off_b[RPT];
+  int off_t[RPT], off_h[RPT];
+  bool live[RPT];
 #pragma unroll
-  for (int w = 0; w < 3; ++w) {
+  for (int j = 0; j < RPT; ++j) {
+    const int64_t row = row0 + (int64_t)j * RPB;
+    live[j] = row < a.rows;  // uniform over the lane group
+    // the host keeps B*T*H below 2^31: 32-bit division
+    const uint32_t row32 = (uint32_t)(live[j] ? row : row0);
+    off_h[j] = (int)(row32 % (uint32_t)a.H);
+    const uint32_t bt = row32 / (uint32_t)a.H;
+    off_t[j] = (int)(bt % (uint32_t)a.T);
+    off_b[j] = (int64_t)(bt / (uint32_t)a.T);
 #pragma unroll
-    for (int i = 0; i < EPL; ++i) xs[w][i] = 0.f;
-    if (a.src[w] == nullptr || !active) continue;  // src: uniform over the grid
-    const T* s = static_cast<const T*>(a.src[w]) + b * a.sb[w] + (int64_t)t * a.st[w] +
-                 (int64_t)h * a.sh[w] + d0;
-    load_vec<T, EPL>(s, xs[w]);
-  }
-
-#pragma unroll
-  for (int w = 0; w < 3; ++w) {
-    if (a.src[w] == nullptr) continue;  // uniform over the grid
-    float (&x)[EPL] = xs[w];
-    if (w < 2) {
-      rope_rotate<T, EPL>(x, cs);
-      if (a.qknorm) qk_rms_norm<EPL, LPK, true>(x, a.D);
+    for (int w = 0; w < RowRegs<FT, EPL>::WORDS; ++w) cr[j].w[w] = 0u;
+    if (active && live[j]) {
+      const FT* f = static_cast<const FT*>(a.freqs) + pos * a.fpos + off_b[j] * a.fb + (int64_t)off_t[j] * a.ft +
+                    (int64_t)off_h[j] * a.fh + d0;
+      load_row<FT, EPL>(cr[j], f);
     }
-    if (active) {
-      T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + b * a.db[w] + (int64_t)t * a.dt[w] +
-             (int64_t)h * a.dh[w] + d0;
-      store_vec<T, EPL>(d, x);
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+#pragma unroll
+      for (int i = 0; i < RowRegs<T, EPL>::WORDS; ++i) xr[w][j].w[i] = 0u;
+      if (a.src[w] == nullptr || !active || !live[j]) continue;  // src: uniform over the grid
+      const T* sp = static_cast<const T*>(a.src[w]) + off_b[j] * a.sb[w] + (int64_t)off_t[j] * a.st[w] +
+                    (int64_t)off_h[j] * a.sh[w] + d0;
+      load_row<T, EPL>(xr[w][j], sp);
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < RPT; ++j) {
+    float cs[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) cs[e] = elem<FT, EPL>(cr[j], e);
+#pragma unroll
+    for (int w = 0; w < 3; ++w) {
+      if (a.src[w] == nullptr) continue;  // uniform over the grid
+      float x[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[e] = elem<T, EPL>(xr[w][j], e);
+      if (w < 2) {
+        rope_rotate<T, EPL>(x, cs);
+        if (a.qknorm) qk_rms_norm<EPL, LPK, true>(x, a.D);
+      }
+      if (active && live[j]) {
+        T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + off_b[j] * a.db[w] + (int64_t)off_t[j] * a.dt[w] +
+               (int64_t)off_h[j] * a.dh[w] + d0;
+        store_vec<T, EPL>(d, x);
+      }
     }
   }
 }
@@ -176,14 +196,25 @@ int next_pow2(int x) {
   return p;
 }
 
+// Rows per lane group: 4 once the launch still has >= 2048 workgroups with
+// them (a prefill's many rows), else 1 (a decode step's few rows would leave
+// CUs idle).
+constexpr int kRopeRowsPerGroup = 4;
+constexpr int64_t kRopeMinBlocks = 2048;
+
 template <typename T, typename FT, int DPAD, int EPL>
 int launch_rope(const RopeArgs& a, hipStream_t s) {
   constexpr int LPK = DPAD / EPL;
   constexpr int RPB = 256 / LPK;
-  const int64_t blocks = (a.rows + RPB - 1) / RPB;
   DG_REQUIRE(a.rows < 0x7fffffffLL, DG_EINVAL, "rope: B*T*H = %lld rows, at most 2^31 - 1", (long long)a.rows);
-  hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL>), dim3((unsigned)blocks), dim3(256), 0,
-                     s, a);
+  constexpr int R = kRopeRowsPerGroup;
+  if (a.rows >= kRopeMinBlocks * RPB * R) {
+    const int64_t blocks = (a.rows + RPB * R - 1) / (RPB * R);
+    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, R>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  } else {
+    const int64_t blocks = (a.rows + RPB - 1) / RPB;
+    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, 1>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  }
   return check_launch("rope_qknorm_kernel");
 }
 
