@@ -58,6 +58,15 @@ def test_rope_qknorm_append_random_shapes(dev, dtype, shape):
     _rope_append_case(dev, dtype, *shape)
 
 
+@pytest.mark.parametrize("dtype,B,T,H,D", [("bf16", 33, 1000, 8, 64), ("f32", 9, 2000, 30, 16),
+                                           ("f16", 11, 1500, 9, 128)])
+def test_rope_qknorm_append_many_rows(dev, dtype, B, T, H, D):
+    """Launches of at least 2048 workgroups of 4-row lane groups (a prefill's
+    rows) take several rows per lane group, with a ragged last workgroup
+    here: still bit-exact against the oracle."""
+    _rope_append_case(dev, dtype, B, T, H, D, 3, T + 5)
+
+
 def _rope_append_case(dev, dtype, B, T, H, D, pos, cap):
     from diff_gpt import _native
     from diff_gpt.model.rope import precompute_freqs_cis
