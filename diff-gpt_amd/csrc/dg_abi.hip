@@ -32,7 +32,7 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                   const PrefixRef& pre, const int* pos_dev, void* workspace,
-                  size_t workspace_bytes, hipStream_t s);
+                  size_t workspace_bytes, int size_keys, hipStream_t s);
 // dg_attn_shared.hip
 bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const PrefixRef& pre,
                                  const void* q, const dg_stride3* q_st, const void* k,
@@ -204,7 +204,7 @@ extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dty
       shared_attention_applicable(B, H, Tq, Tk, D, dtype, pre, q, q_st, kk, k_st, vv, v_st, y, y_st))
     return shared_attention(B, H, Tk, D, dtype, q, q_st, kk, k_st, vv, v_st, y, y_st, scale, pre, nullptr, s);
   return vec_attention(B, H, Tq, Tk, D, dtype, q, q_st, kk, k_st, vv, v_st, y, y_st, scale, pre, nullptr,
-                       workspace, workspace_bytes, s);
+                       workspace, workspace_bytes, Tk, s);
 }
 
 extern "C" int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
@@ -266,7 +266,7 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
     return shared_attention(B, H, max_keys, D, dtype, q, q_st, kk, kc_st, vv, vc_st, y, y_st, scale, pre, pos,
                             static_cast<hipStream_t>(stream));
   return vec_attention(B, H, 1, max_keys, D, dtype, q, q_st, kk, kc_st, vv, vc_st, y, y_st, scale, pre, pos,
-                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+                       workspace, workspace_bytes, max_keys, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype) {
@@ -329,7 +329,7 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
                ? shared_attention(B, H, max_pos, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
                                   pos_dev, s)
                : vec_attention(B, H, 1, max_pos, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
-                               pos_dev, workspace, workspace_bytes, s);
+                               pos_dev, workspace, workspace_bytes, max_pos, s);
   }
   const int64_t es = dtype == DG_F32 ? 4 : 2, fes = freqs_dtype == DG_F32 ? 4 : 2;
   const dg_stride3 f_st = {0, 0, 0};
@@ -339,13 +339,15 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
                              static_cast<const char*>(freqs) + (int64_t)pos * freqs_pos_stride * fes, &f_st,
                              freqs_dtype, flags, stream);
   if (rc != DG_OK) return rc;
-  return vec_attention_splits(B, H, 1, pos + 1, D) == 1 &&
-                 shared_attention_applicable(B, H, 1, pos + 1, D, dtype, pre, y, y_st, kw, kc_st, vw, vc_st, y,
+  // the kernel, its key splits and the workspace are chosen for max_pos, as
+  // the device-position form must: both forms give the same bits
+  return vec_attention_splits(B, H, 1, max_pos, D) == 1 &&
+                 shared_attention_applicable(B, H, 1, max_pos, D, dtype, pre, y, y_st, kw, kc_st, vw, vc_st, y,
                                              y_st)
              ? shared_attention(B, H, pos + 1, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
                                 nullptr, s)
              : vec_attention(B, H, 1, pos + 1, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
-                             nullptr, workspace, workspace_bytes, s);
+                             nullptr, workspace, workspace_bytes, max_pos, s);
 }
 
 extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,

@@ -474,7 +474,10 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                   const PrefixRef& pre, const int* pos_dev, void* workspace,
-                  size_t workspace_bytes, hipStream_t s) {
+                  size_t workspace_bytes, int size_keys, hipStream_t s) {
+  // size_keys (>= Tk) sizes the key splits and the workspace: a decode step
+  // passes its max_pos, so that the host- and device-position forms split
+  // the same way and give the same bits
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
   DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "attention: head_dim %d > 256", D);
@@ -515,8 +518,9 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.pre = pre;
   a.pos_dev = pos_dev;
 
-  int ns = vec_attention_splits(B, H, Tq, Tk, D);
-  const size_t need = vec_attention_workspace(B, H, Tq, Tk, D);
+  DG_REQUIRE(size_keys >= Tk, DG_EINVAL, "attention: split sizing for %d keys below Tk = %d", size_keys, Tk);
+  int ns = vec_attention_splits(B, H, Tq, size_keys, D);
+  const size_t need = vec_attention_workspace(B, H, Tq, size_keys, D);
   if (ns > kMaxBlockSplits && (workspace == nullptr || workspace_bytes < need)) {
     DG_REQUIRE(workspace == nullptr, DG_EWORKSPACE,
                "attention: workspace of %zu bytes given, %zu needed", workspace_bytes, need);

@@ -447,6 +447,11 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (40, 20, 2, 64, 66, 16, 80),
     (40, 20, 2, 64, 71, 16, 80),
     (40, 20, 2, 64, 79, 16, 96),
+    # pos + 1 below the 256 keys at which decode splits the keys, capacity
+    # above: both position forms choose the kernel and its splits for the
+    # capacity, so they still agree bit for bit (ragged last group)
+    (155, 100, 2, 188, 243, 32, 261),
+    (200, 100, 2, 188, 243, 16, 261),
     (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: two launches
     (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): two launches
 ]
