@@ -2,7 +2,7 @@
 the oracle's torch-on-CPU restatement on the same inputs.
 
 Bars: fp32 max-abs error <= 1e-5 * max|ref|,
-bf16 within 2e-2 * max|ref|; the one-source Block-AttnRes is dg_rms_norm bit
+bf16 and fp16 within 2e-2 * max|ref|; the one-source Block-AttnRes is dg_rms_norm bit
 for bit (the softmax of one score is 1)."""
 
 import numpy as np
@@ -13,8 +13,8 @@ from oracle import torch_ref as tr
 
 pytestmark = pytest.mark.gpu
 
-TDT = {"f32": torch.float32, "bf16": torch.bfloat16}
-TOL = {"f32": 1e-5, "bf16": 2e-2}
+TDT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+TOL = {"f32": 1e-5, "bf16": 2e-2, "f16": 2e-2}
 
 
 def _randn(shape, seed, dtype, scale=1.0):
@@ -37,7 +37,7 @@ RES = [  # (rows, C, sources)
 ]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", RES, ids=lambda s: "x".join(map(str, s)))
 def test_attn_res_norm_matches_reference(dev, dtype, shape):
     from diff_gpt import _native
@@ -57,14 +57,14 @@ def _random_res(seed, n):
              int(rng.integers(2, 13))) for _ in range(n)]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", _random_res(17, 8), ids=lambda s: "x".join(map(str, s)))
 def test_attn_res_norm_random_shapes(dev, dtype, shape):
     """Seeded random (rows, width, sources) through the same check."""
     test_attn_res_norm_matches_reference(dev, dtype, shape)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_attn_res_norm_one_source_is_rms_norm(dev, dtype):
     from diff_gpt import _native
 
@@ -87,7 +87,7 @@ def test_attn_res_norm_strided_sources(dev):
     assert _rel(got, ref) <= TOL["f32"]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_gate_matches_reference(dev, dtype):
     from diff_gpt import _native
 
@@ -100,7 +100,7 @@ def test_gate_matches_reference(dev, dtype):
     assert _rel(yd, ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("rows", [6400, 3])
 def test_swiglu_matches_reference(dev, dtype, rows):
     from diff_gpt import _native
@@ -115,7 +115,7 @@ def test_swiglu_matches_reference(dev, dtype, rows):
     assert _rel(got, ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_softcap_matches_reference(dev, dtype):
     from diff_gpt import _native
 
@@ -212,7 +212,7 @@ LM_HEAD = [  # (rows, C, V)
 ]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("cap", [15.0, 0.0], ids=["softcap", "nocap"])
 @pytest.mark.parametrize("shape", LM_HEAD, ids=lambda s: "x".join(map(str, s)))
 def test_lm_head_matches_linear_softcap_argmax(dev, dtype, cap, shape):
@@ -240,7 +240,7 @@ def _random_lm_heads(seed, n):
              int(rng.choice([64, 128, 256, 512, 1024]))) for _ in range(n)]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", _random_lm_heads(31, 8), ids=lambda s: "x".join(map(str, s)))
 def test_lm_head_random_shapes(dev, dtype, shape):
     """Seeded random (rows, width, vocabulary) within the kernel's range, with

@@ -101,7 +101,7 @@ def _rope_append_case(dev, dtype, B, T, H, D, pos, cap):
     assert (untouched == 7.0).all()
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_rope_only_bit_exact_with_broadcast_table(dev, dtype):
     from diff_gpt.model.rope import apply_rotary_emb
 
@@ -166,7 +166,7 @@ DECODE = [  # (B, H, Tk, D): cfg1 rows, cfg3 / cfg4 rows (few, long: key splits)
 ]
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", DECODE, ids=lambda s: "x".join(map(str, s)))
 def test_decode_attention_parity(dev, dtype, shape):
     B, H, Tk, D = shape
@@ -385,7 +385,7 @@ def _grouped_case(dtype, shape):
     return q, cache
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", GROUPED, ids=lambda s: "x".join(map(str, s)))
 def test_grouped_prefix_attention_equals_plain(dev, dtype, shape):
     """Rows of a group share their first `prefix` cache positions (a broadcast
@@ -539,7 +539,7 @@ def test_decode_step_random_shapes(dev, dtype, shape):
 # ------------------------------------------------------------------ strided copy
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_copy4d_exact_with_broadcast(dev, dtype):
     from diff_gpt import _native
 
@@ -553,7 +553,7 @@ def test_copy4d_exact_with_broadcast(dev, dtype):
     assert torch.equal(dst2.cpu(), src.cpu().expand(4, 3, 5, 7).transpose(0, 1).transpose(2, 3))
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_copy4d_row_vector_path(dev, dtype):
     """Rows with a contiguous, 16-byte-multiple last dimension take the
     row-vectorised kernel: batch broadcast of a cache prefix into strided
@@ -581,7 +581,7 @@ def _random_copies(seed, n):
     return out
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("case", _random_copies(5, 12), ids=lambda c: "x".join(map(str, c[0])) + "-" + "".join(
     "b" if b else "." for b in c[1]) + "-" + "".join(map(str, c[2])))
 def test_copy4d_random_strides(dev, dtype, case):
@@ -648,7 +648,7 @@ def _random_groups(seed, n):
     return out
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 @pytest.mark.parametrize("shape", _random_groups(7, 10), ids=lambda s: "x".join(map(str, s)))
 def test_grouped_prefix_random_shapes(dev, dtype, shape):
     """The two-wave shared-prefix kernel on seeded random groups (ragged
