@@ -51,13 +51,6 @@
 // head start first.
 #include "dg_rope_math.h"
 
-#ifndef DG_PREFILL_QW_D64
-#define DG_PREFILL_QW_D64 1
-#endif
-#ifndef DG_PREFILL_QW_D128
-#define DG_PREFILL_QW_D128 1
-#endif
-
 namespace dg {
 
 typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
@@ -130,36 +123,14 @@ struct MfmaOps<f16_t> {
   }
 };
 
-#ifndef DG_PREFILL_BN_D64
-#define DG_PREFILL_BN_D64 64
-#endif
-#ifndef DG_PREFILL_WGS_D64
-#define DG_PREFILL_WGS_D64 4
-#endif
-#ifndef DG_PREFILL_BN_D128
-#define DG_PREFILL_BN_D128 32
-#endif
-#ifndef DG_PREFILL_WGS_BND_D64
-#define DG_PREFILL_WGS_BND_D64 4
-#endif
-#ifndef DG_PREFILL_WGS_BND_D128
-#define DG_PREFILL_WGS_BND_D128 3
-#endif
-#ifndef DG_PREFILL_WGS_D128
-#define DG_PREFILL_WGS_D128 3
-#endif
-
 // Keys per tile: 64 at D = 64; 32 at D = 128, which halves the S and P
 // registers (168 VGPRs) and the LDS stages (32 KB per workgroup), so three
 // workgroups share a CU instead of two (+4 to +10 % at configs[4]'s shapes).
 template <int D>
 constexpr int prefill_bn() {
-  return D == 64 ? DG_PREFILL_BN_D64 : DG_PREFILL_BN_D128;
+  return D == 64 ? 64 : 32;
 }
-#ifndef DG_PREFILL_WINDOW
-#define DG_PREFILL_WINDOW 64
-#endif
-constexpr int kPrefillWindow = DG_PREFILL_WINDOW;  // (b, h) pairs per scheduling window
+constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 // Schedule of the bounded form's 32-key blocks, per head_dim (measured at
 // configs[2] / [4]: D = 64 gains 3-4 % from the prefetch, while the
@@ -169,25 +140,13 @@ constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescale
 //               of block mb (two S blocks live)
 //   prefetch -- a block's K fragments are all read before its S products and
 //               its V^T fragments before its softmax (one LDS wait each)
-#ifndef DG_PREFILL_BND_PIPE_D64
-#define DG_PREFILL_BND_PIPE_D64 0
-#endif
-#ifndef DG_PREFILL_BND_PREFETCH_D64
-#define DG_PREFILL_BND_PREFETCH_D64 1
-#endif
-#ifndef DG_PREFILL_BND_PIPE_D128
-#define DG_PREFILL_BND_PIPE_D128 1
-#endif
-#ifndef DG_PREFILL_BND_PREFETCH_D128
-#define DG_PREFILL_BND_PREFETCH_D128 0
-#endif
 template <int D>
 constexpr bool prefill_pipe() {
-  return D == 64 ? DG_PREFILL_BND_PIPE_D64 != 0 : DG_PREFILL_BND_PIPE_D128 != 0;
+  return D != 64;
 }
 template <int D>
 constexpr bool prefill_prefetch() {
-  return D == 64 ? DG_PREFILL_BND_PREFETCH_D64 != 0 : DG_PREFILL_BND_PREFETCH_D128 != 0;
+  return D == 64;
 }
 
 // max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
@@ -233,14 +192,10 @@ __device__ __forceinline__ int piece_swz(int r) {
   else return ((r & 3) << 2) | ((r >> 2) & 3);
 }
 
-
-#ifndef DG_PREFILL_BUFFER_DMA
-#define DG_PREFILL_BUFFER_DMA 1
-#endif
-
-// The same through a buffer resource: 16 bytes per lane from byte offset
-// voff + soff of the resource (zeros past its range) into lds + 16*l.  The
-// address-space cast stays inside this device function.
+// Global -> LDS copy through a buffer resource: 16 bytes per lane from byte
+// offset voff + soff of the resource (zeros past its range) into lds + 16*l
+// (buffer_load_dwordx4 ... lds).  The address-space cast stays inside this
+// device function.
 __device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, void* lds) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
@@ -250,8 +205,7 @@ __device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int vo
 // another's softmax); D = 128 with 32-key tiles 3 (<= 168 VGPRs).
 template <int D, bool BND>
 constexpr int prefill_wgs_per_cu() {
-  if constexpr (BND) return D == 64 ? DG_PREFILL_WGS_BND_D64 : DG_PREFILL_WGS_BND_D128;
-  return D == 64 ? DG_PREFILL_WGS_D64 : DG_PREFILL_WGS_D128;
+  return D == 64 ? 4 : 3;
 }
 
 template <typename T, int D, int QW, bool ROPE, typename FT, bool BND>
@@ -309,7 +263,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
   // fills slot l % PPR of row l / PPR with the piece that the swizzle puts
   // there.
   const int dma_row = lane / PPR, dma_slot = lane % PPR;
-#if DG_PREFILL_BUFFER_DMA
   // Buffer loads over this head's K and V rows: the per-lane byte offsets of
   // a tile's pieces are fixed, the tile's start goes into the scalar offset,
   // so a tile's copies cost no vector arithmetic.  Rows past Tk lie beyond
@@ -335,20 +288,6 @@ void prefill_mfma_kernel(const PrefillArgs a) {
       lds_copy16_buf(vrs, vvo[i], vs0, vs + blk * 512);
     }
   };
-#else
-  // Rows past Tk re-read the last key (masked, probability 0).
-  auto dma_tile = [&](uint16_t* ks, uint16_t* vs, int kt0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < C::DMA_PER_WAVE; ++i) {
-      const int blk = wv * C::DMA_PER_WAVE + i;
-      const int row = blk * C::ROWS_PER_DMA + dma_row;
-      const int piece = dma_slot ^ piece_swz<D>(row);
-      const int key = min(kt0 + row, a.Tk - 1);
-      lds_copy16(kp + key * (int)a.kt + 8 * piece, ks + blk * 512);
-      lds_copy16(vp + key * (int)a.vt + 8 * piece, vs + blk * 512);
-    }
-  };
-#endif
   // this wave's copies are in LDS (each wave waits for its own before the
   // barrier that hands the stage to all waves)
   auto stage_ready = [&]() __attribute__((always_inline)) {
@@ -540,8 +479,9 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 
   // Bounded form (BND): q and k rows are RMS-normalised and the scale is
   // folded into q, so every score s is a log2-unit logit with
-  // |s| <= log2(e) * sqrt(D) * (1 + 2^-7) (11.7 at D = 64, 16.5 at D = 128)
-  // and p = exp2(s) can neither overflow nor underflow: no running maximum,
+  // |s| <= scale * log2(e) * D * (1 + 2^-7) (11.7 at D = 64, 16.5 at D = 128
+  // with the SDPA scale; the host takes this form only while the bound is at
+  // most 64) and p = exp2(s) can neither overflow nor underflow: no running maximum,
   // no rescale.  Without a tile-wide maximum each 32-key block goes from S to
   // P to the PV products on its own, and the S products of block mb + 1 are
   // issued before the exponentials of block mb, so one wave's MFMAs overlap
@@ -821,9 +761,11 @@ namespace {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 bool strides8(const dg_stride3* s) { return s->b % 8 == 0 && s->t % 8 == 0 && s->h % 8 == 0; }
 
+// query blocks of 32 per wave (64 per wave spills at D = 64, and halves the
+// resident workgroups at D = 128)
 template <int D>
 constexpr int qw_for() {
-  return D == 64 ? DG_PREFILL_QW_D64 : DG_PREFILL_QW_D128;
+  return 1;
 }
 
 template <typename T, int D, bool ROPE = false, typename FT = T, bool BND = false>
@@ -926,9 +868,15 @@ int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void
   a.qknorm = qknorm;
   const bool f32 = fdtype == DG_F32;
   // normalised queries (here) and keys (the caller's guarantee): bounded
-  // scores.  bf16 only: p = exp2(s) reaches 2^16.5 at D = 128, beyond fp16's
-  // range, while bf16 has fp32's exponent range
-  const bool bounded = qknorm && keys_normed && dtype == DG_BF16;
+  // scores, |s| <= scale * log2(e) * D * (1 + 2^-7) in log2 units.  The form
+  // without a running maximum is taken while that bound is at most 64, so
+  // that exp2(s) of every score and the sum of up to 2^30 of them stay inside
+  // fp32's normal range (the SDPA scale 1/sqrt(D) gives 11.7 at D = 64, 16.5
+  // at D = 128; a scale above 0.68 / 0.34 there runs the running-maximum
+  // form).  bf16 only: p reaches 2^16.5 at D = 128 with the SDPA scale, beyond
+  // fp16's range, while bf16 has fp32's exponent range
+  const bool small_scores = (double)scale * 1.4426950408889634 * D * (1.0 + 1.0 / 128.0) <= 64.0;
+  const bool bounded = qknorm && keys_normed && dtype == DG_BF16 && small_scores;
   if (dtype == DG_BF16)
     return bounded ? launch_rope_prefill<bf16_t, true>(D, f32, a, s) : launch_rope_prefill<bf16_t, false>(D, f32, a, s);
   return launch_rope_prefill<f16_t, false>(D, f32, a, s);

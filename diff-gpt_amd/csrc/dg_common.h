@@ -379,11 +379,6 @@ __device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowR
 // 32-bit data format, no swizzle, no stride.
 constexpr int kBufferWord3 = 0x00020000;
 
-// 16 bytes per lane from global memory straight into LDS: lane l of the wave
-// writes lds + 16*l (lds wave-uniform), no registers involved
-__device__ __forceinline__ void lds_copy16(const void* g, void* lds) {
-  __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
 // ds_read_b64_tr_b16: within each 16 lanes, lane t receives element t & 3 of
 // the 8-byte chunks addressed by lanes t/4, 4 + t/4, 8 + t/4, 12 + t/4
 __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {

@@ -179,6 +179,19 @@ _SIGNATURES = {
 
 ABI_VERSION = 2
 
+# head_dim the kernels take: even sizes, up to 256 for powers of two and up to
+# 128 for others (those run with one (re, im) pair per lane, at most 64 lanes
+# per row)
+MAX_HEAD_DIM = 256
+MAX_HEAD_DIM_NON_POW2 = 128
+
+
+def head_dim_supported(D: int) -> bool:
+    """Whether every kernel of the attention path takes this head_dim."""
+    if D <= 0 or D % 2:
+        return False
+    return D <= (MAX_HEAD_DIM if D & (D - 1) == 0 else MAX_HEAD_DIM_NON_POW2)
+
 
 def lib() -> ctypes.CDLL:
     """Load libdgattn.so once; raise if it has not been built."""

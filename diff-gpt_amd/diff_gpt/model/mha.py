@@ -50,6 +50,14 @@ class MultiHeadAttention(nn.Module):
         self.n_head = n_head
         self.layer_idx = layer_idx
         self.head_dim = self.n_embd // self.n_head
+        # the reference's SDPA takes any even head_dim; the HIP kernels have
+        # limits, checked here rather than at the first launch
+        if not _native.head_dim_supported(self.head_dim):
+            raise ValueError(
+                f"head_dim {self.head_dim} (n_embd {n_embd} / n_head {n_head}) is beyond the HIP attention "
+                f"kernels, which take even head dims up to {_native.MAX_HEAD_DIM} (powers of two) or "
+                f"{_native.MAX_HEAD_DIM_NON_POW2} (other sizes)"
+            )
         inner = self.n_head * self.head_dim
         # creation order fixes the parameter initialisation order (seeded RNG)
         self.c_q = nn.Linear(self.n_embd, inner, bias=False)

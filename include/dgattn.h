@@ -59,9 +59,11 @@ enum dg_status {
 #define DG_QKNORM 1 /* apply the parameter-free RMSNorm after RoPE (mha.py:48) */
 /* dg_prefill_rope only, with DG_QKNORM: every key row of k is RMS-normalised
  * (as dg_rope_qknorm_append with DG_QKNORM writes it, mha.py:48).  With both
- * rows normalised every scaled score lies within log2(e)*sqrt(D)*(1+2^-7) in
- * log2 units, and for bf16 data the kernel drops the running maximum of the
- * softmax (fp16 data keeps it: exp2 of that bound can exceed fp16's range). */
+ * rows normalised every scaled score lies within scale*log2(e)*D*(1+2^-7) in
+ * log2 units (log2(e)*sqrt(D)*(1+2^-7) at the SDPA scale 1/sqrt(D)), and for
+ * bf16 data, while that bound is at most 64, the kernel drops the running
+ * maximum of the softmax (fp16 data keeps it: exp2 of the bound can exceed
+ * fp16's range; so does a larger scale). */
 #define DG_KEYS_NORMED 2
 
 /* Element strides of a (B,T,H,D) view; the D stride is always 1. */
@@ -139,8 +141,12 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * DG_QKNORM or 0, optionally with DG_KEYS_NORMED (DG_QKNORM | DG_KEYS_NORMED:
  * the keys are normalised too; for bf16 data the softmax then runs without a
  * running maximum, with the scale folded into the rounded query operand, so y
- * agrees with dg_attention's within the bf16 bar rather than bit for bit;
- * fp16 data ignores the flag and gives dg_attention's y bit for bit).
+ * agrees with dg_attention's within the bf16 bar rather than bit for bit.
+ * That form is taken only while scale * log2(e) * D * (1 + 2^-7) <= 64, the
+ * bound on a score in log2 units that keeps exp2 of every score inside
+ * fp32's normal range: scale up to about 0.68 at head_dim 64 and 0.34 at 128,
+ * the SDPA scale 1/sqrt(D) well inside.  A larger scale, and fp16 data,
+ * ignore the flag and give dg_attention's y bit for bit).
  * Only the MFMA prefill kernel's shapes are taken (bf16 or
  * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
  * freqs in the data's dtype or fp32, Tq <= 65535 * 128 and B*H <= 65535 * 64,
@@ -262,9 +268,17 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
  * key and value are appended and also used from registers.  The cache
  * contents are those of dg_rope_qknorm_append bit for bit; y equals the
  * two-call result within fp32 rounding (the new key is accumulated last).
- * Other shapes run the two calls, with the rotated q staged in y.  The
- * workspace (dg_decode_step_workspace_size) serves the second call's key
- * splits beyond 16 per (b, h); NULL caps them at 16.
+ * Other shapes run two launches, with the rotated q staged in y:
+ * dg_rope_qknorm_append at p, then the decode attention over 0 .. p with its
+ * kernel and key splits chosen for max_pos -- in both position forms, since
+ * the device form must fix them for every p a captured graph replays.  So y
+ * equals dg_decode_attention_at's (max_keys = max_pos) bit for bit, host and
+ * device position alike; it equals the two calls dg_rope_qknorm_append +
+ * dg_attention_grouped over p + 1 keys bit for bit when both choose the same
+ * number of key splits, and otherwise differs from them only in the order
+ * of the fp32 accumulation (with B*H below 4096, p + 1 and max_pos can lie
+ * on different sides of a multiple of 128 keys).  The workspace (dg_decode_step_workspace_size)
+ * serves key splits beyond 16 per (b, h); NULL caps them at 16.
  */
 DG_API size_t dg_decode_step_workspace_size(int B, int H, int max_pos, int D, int dtype);
 

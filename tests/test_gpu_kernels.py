@@ -303,6 +303,38 @@ def test_prefill_rope_bounded_against_f64(dev, dtype, fdt, shape):
     assert np.abs(got - two).max() / np.abs(two).max() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_prefill_rope_keys_normed_large_scale_keeps_running_max(dev, D):
+    """DG_KEYS_NORMED with scale = 1: a score reaches +-1.44 * D in log2 units,
+    beyond what exp2 keeps inside fp32 (query 0's only visible key is minus
+    its own normalised row, query 5 sees its own row as key 5), so the library
+    runs the running-maximum form instead: y finite and bit for bit
+    dg_attention's on the rotated, normalised q."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, T = 1, 2, 200
+    q = _randn((B, T, H, D), 95 + D, "bf16", 2.0)
+    k = _randn((B, T, H, D), 96 + D, "bf16")
+    k[:, 0] = -q[:, 0]
+    k[:, 5] = q[:, 5]
+    q, k = q.to(dev), k.to(dev)
+    v = _randn((B, T, H, D), 97 + D, "bf16").to(dev)
+    freqs = precompute_freqs_cis(D, 2 * T, 10000)[:T].view(1, T, 1, D // 2, 2).to(dev)
+    k_rot = torch.empty_like(k)
+    _native.rope_qknorm_append_(None, k, None, freqs, None, k_rot, None, True)
+    y = torch.empty_like(q)
+    assert _native.prefill_rope_(q, freqs, k_rot, v, y, 1.0, True, keys_normed=True)
+    q_rot = torch.empty_like(q)
+    _native.rope_qknorm_append_(q, None, None, freqs, q_rot, None, None, True)
+    y2 = torch.empty_like(q)
+    _native.attention_(q_rot, k_rot, v, y2, 1.0)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y.float()).all())
+    assert torch.equal(y, y2)
+    assert torch.equal(y[:, 0], v[:, 0])  # one visible key: its value
+
+
 @pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 64), "f32"),
                                          ((1, 2, 8, 8, 64), "bf16")])
 def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
@@ -438,6 +470,13 @@ def test_grouped_prefix_attention_mfma(dev, dtype, shape):
     assert torch.equal(y_at, y_grp)
 
 
+def _decode_splits(BH: int, keys: int) -> int:
+    """The host's key-split count for a decode launch over ``keys`` keys
+    (restated to tell which launches should agree bit for bit): enough splits
+    to give 4096 waves, at least 128 keys each, at most 64."""
+    return max(1, min(-(-4096 // BH), keys // 128, 64))
+
+
 DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (300, 100, 4, 96, 120, 16, 144),  # cfg1 series: one launch
     (70, 16, 2, 33, 69, 32, 80),      # D = 32, prefix not a multiple of 16
@@ -453,6 +492,9 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (155, 100, 2, 188, 243, 32, 261),
     (200, 100, 2, 188, 243, 16, 261),
     (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: two launches
+    # no shared prefix, pos + 1 = 201 keys (one split) but max_pos = 300 (two):
+    # y is dg_decode_attention_at's over max_pos, not the two calls' bits
+    (1, 1, 1, 0, 200, 16, 300),
     (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): two launches
 ]
 
@@ -461,10 +503,13 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
 @pytest.mark.parametrize("shape", DECODE_STEP, ids=lambda s: "x".join(map(str, s)))
 def test_decode_step_matches_two_calls(dev, dtype, shape):
     """dg_decode_step == dg_rope_qknorm_append at pos + dg_attention_grouped over
-    0 .. pos: the cache bit for bit; y bit for bit where it runs the two calls,
-    within the north-star bars (and against fp64) where it fuses them; the
-    device-position form equal to the host-position form; an out-of-range
-    device position leaves the cache untouched."""
+    0 .. pos: the cache bit for bit.  Where it makes two launches, y bit for
+    bit dg_decode_attention_at's over max_pos = cap (kernel and key splits
+    chosen for the capacity), and the two calls' wherever those choose the
+    same number of key splits; within the north-star bars of them and of fp64
+    where it fuses the step or the split counts differ.  The device-position
+    form equal to the host-position form; an out-of-range device position
+    leaves the cache untouched."""
     from diff_gpt import _native
     from diff_gpt.model.rope import precompute_freqs_cis
 
@@ -492,14 +537,21 @@ def test_decode_step_matches_two_calls(dev, dtype, shape):
     _native.decode_step_(q, k, v, table[pos], c2[0].transpose(1, 2), c2[1].transpose(1, 2), y2, scale, pos,
                          prefix, group)
     assert torch.equal(c2, c1)
-    if G >= 16 and D in (16, 32):
+    same_splits = _decode_splits(B * H, pos + 1) == _decode_splits(B * H, cap)
+    fused = G >= 16 and D in (16, 32) and _decode_splits(B * H, cap) == 1
+    if fused or not same_splits:
         ref = on.attention_f64(q_rot.float().cpu().numpy(), keys.float().cpu().numpy(), vals.float().cpu().numpy(),
                                scale)
         mag = np.abs(ref).max()
         assert np.abs(y2.float().cpu().numpy() - ref).max() <= TOL[dtype] * mag
         assert (y2.float() - y1.float()).abs().max().item() <= TOL[dtype] * mag
-    else:
-        assert torch.equal(y2, y1)
+    if not fused:
+        y_at = torch.empty_like(q)
+        _native.decode_attention_at_(q_rot, c1[0].transpose(1, 2), c1[1].transpose(1, 2), y_at, scale,
+                                     torch.tensor([pos], dtype=torch.int32, device=dev), prefix, group)
+        assert torch.equal(y2, y_at)
+        if same_splits:
+            assert torch.equal(y2, y1)
 
     c3, y3 = cache.to(dev), torch.empty_like(q)
     p = torch.tensor([pos], dtype=torch.int32, device=dev)

@@ -144,6 +144,28 @@ def test_gpt_constructor_assertions():
         GPT(vocab_size=64, n_embd=16, n_layer=1, n_head=2, label_smoothing_sigma=-0.1)
 
 
+@pytest.mark.parametrize("n_embd,n_head,ok", [
+    (1024, 2, False),  # head_dim 512: a power of two above 256
+    (1024, 4, True),   # 256: the largest power of two the kernels take
+    (768, 4, False),   # 192: not a power of two, above 128
+    (480, 4, True),    # 120: not a power of two, within 128
+    (96, 8, True),     # 12
+])
+def test_gpt_rejects_head_dims_beyond_the_kernels(n_embd, n_head, ok):
+    """The reference's SDPA takes any even head_dim; the HIP kernels take even
+    head dims up to 256 (powers of two) or 128 (other sizes).  A model outside
+    that range is refused when it is built, with the limit in the message,
+    not at its first launch."""
+    from diff_gpt import _native
+
+    assert _native.head_dim_supported(n_embd // n_head) == ok
+    if ok:
+        GPT(vocab_size=64, n_embd=n_embd, block_size=8, n_layer=1, n_head=n_head)
+    else:
+        with pytest.raises(ValueError, match=r"head_dim \d+ .*up to 256 \(powers of two\) or 128"):
+            GPT(vocab_size=64, n_embd=n_embd, block_size=8, n_layer=1, n_head=n_head)
+
+
 def test_projection_weights_are_views_of_one_storage():
     """c_q, c_k, c_v and c_g view one (3*inner + C, C) storage, so no copy of
     them can go stale: updates through .data, in-place ops and load_state_dict
