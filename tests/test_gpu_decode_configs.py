@@ -14,7 +14,7 @@ waves of one workgroup and merge in LDS):
     (a split count that is not a power of two, in fp32 at 1e-5 as well).
 
 Every output row is compared with float64 attention computed on the device
-(torch, float64 matrix products) over the same q, K and V; the first, middle
+(torch, float64 elementwise products and sums) over the same q, K and V; the first, middle
 and last unit and a few seeded ones are compared with the CPU oracle
 (oracle.numerics.attention_head_f64) as well.  Bars: fp32 1e-5, bf16 / fp16
 2e-2, each relative to the unit's own max|ref|.  Some units carry a planted
@@ -76,10 +76,11 @@ def _sampled_units(BH: int, seed: int) -> list[int]:
 
 
 def _plant_boundary_keys(q, kc, Tk, units, nsplit):
-    """Make key j*split_len - 1 (the last of split j - 1) the dominant key of
-    some sampled units and key j*split_len (the first of split j) that of
-    others: k <- 3 * q at that position (score 3*|q|^2*scale, far above the
-    rest)."""
+    """Plant a large score at key j*split_len - 1 (the last of split j - 1) of
+    some sampled units and at key j*split_len (the first of split j) of
+    others: k <- c * q there, with c = 3 (score 3*|q|^2*scale: the key takes
+    nearly all the weight) or c = 1/4 (about a fifth of it, the rest spread
+    over every split)."""
     B, _, H, D = q.shape
     if nsplit == 1:
         bounds = [Tk // 2 - 1, Tk // 2, Tk - 1]
@@ -88,12 +89,14 @@ def _plant_boundary_keys(q, kc, Tk, units, nsplit):
         bounds = [split_len * j + d for j in range(1, nsplit) for d in (-1, 0) if split_len * j < Tk]
     for n, u in enumerate(units[1:]):  # unit 0 keeps plain random keys
         b, h = divmod(u, H)
-        kc[b, h, bounds[n % len(bounds)]] = (3.0 * q[b, 0, h].float()).to(kc.dtype)
+        c = 3.0 if n % 2 == 0 else 0.25
+        kc[b, h, bounds[(n // 2) % len(bounds)]] = (c * q[b, 0, h].float()).to(kc.dtype)
 
 
-def _f64_rows(q, kc, vc, Tk, scale, chunk=512):
-    """float64 attention of every (row, head) on the device: q (B,1,H,D),
-    kc / vc (B,H,cap,D) -> (B*H, D) float64."""
+def _f64_rows(q, kc, vc, Tk, scale, chunk=256):
+    """float64 attention of every (row, head) on the device, by elementwise
+    products and sums (no library GEMM): q (B,1,H,D), kc / vc (B,H,cap,D) ->
+    (B*H, D) float64."""
     B, _, H, D = q.shape
     qq = q[:, 0].to(torch.float64).reshape(B * H, D)
     out = torch.empty((B * H, D), dtype=torch.float64, device=q.device)
@@ -101,10 +104,13 @@ def _f64_rows(q, kc, vc, Tk, scale, chunk=512):
     for u0 in range(0, B * H, chunk):
         u1 = min(B * H, u0 + chunk)
         kk = kf[u0:u1, :Tk].to(torch.float64)
+        s = (kk * qq[u0:u1, None, :]).sum(-1) * scale  # (n, Tk)
+        del kk
+        s = s - s.amax(dim=-1, keepdim=True)
+        p = torch.exp(s)
+        p = p / p.sum(dim=-1, keepdim=True)
         vv = vf[u0:u1, :Tk].to(torch.float64)
-        s = torch.bmm(kk, qq[u0:u1, :, None].contiguous())[..., 0] * scale  # (n, Tk)
-        p = torch.softmax(s, dim=-1)
-        out[u0:u1] = torch.bmm(p[:, None, :].contiguous(), vv)[:, 0]
+        out[u0:u1] = (p[..., None] * vv).sum(1)
     return out
 
 
@@ -151,8 +157,9 @@ def test_decode_attention_at_config_geometry(dev, shape):
         b, h = divmod(u, H)
         cpu[u] = on.attention_head_f64(q[b, :, h].float().cpu().numpy(), kc[b, h, :Tk].float().cpu().numpy(),
                                        vc[b, h, :Tk].float().cpu().numpy(), scale)[0]
-        # the device float64 reference agrees with the CPU oracle
-        assert np.abs(ref64[u].cpu().numpy() - cpu[u]).max() <= 1e-9 * np.abs(cpu[u]).max()
+        # the device float64 reference agrees with the CPU oracle (far inside
+        # the tightest bar, fp32's 1e-5)
+        assert np.abs(ref64[u].cpu().numpy() - cpu[u]).max() <= 1e-7 * np.abs(cpu[u]).max()
     worst = _check_rows(y, ref64, cpu, TOL[dtype], "dg_attention")
     print(f"  worst per-unit error {worst:.3g} (bar {TOL[dtype]})", flush=True)
 
