@@ -38,8 +38,10 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -562,14 +564,15 @@ def engine_multi_leg(name: str):
     return out
 
 
-def engine_leg(dtype_name: str):
+def engine_leg(dtype_name: str, per_series: bool = True):
     """configs[1] end to end through the drop-in API: the README GPT (random
     init, seed 0), 64 series of 96 uniform ids, each one
     Engine.generate_batch(prompt, num_samples=100, max_tokens=48) with a
     temperature-1 sampler -- the reference's call pattern (diff_gpt.py:229-235).
     Includes the non-attention model work (projections, FFN, Block-AttnRes,
     lm_head), sampling and the host-side result lists.  Also one batched call
-    with all 6400 rows on one prompt."""
+    with all 6400 rows on one prompt.  per_series=False skips the 64 calls
+    (the batched call alone, e.g. under a kernel trace)."""
     import torch
 
     from diff_gpt.model.engine import Engine
@@ -585,31 +588,41 @@ def engine_leg(dtype_name: str):
     prompts = [torch.randint(0, 256, (PREFIX,), generator=g).tolist() for _ in range(SERIES)]
     engine = Engine(model)
     sampler = TemperatureSampler(1.0)
-    engine.generate_batch(prompts[0], num_samples=TRAJ, max_tokens=NEW, sampler=sampler)  # warm-up
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s, prompt in enumerate(prompts):
-        engine.generate_batch(prompt, num_samples=TRAJ, max_tokens=NEW, sampler=sampler, seed=s)
-    torch.cuda.synchronize()
-    per_series = time.perf_counter() - t0
-    # the whole job as one call: 64 prompts x 100 trajectories, one decode loop
+    series_s = None
+    if per_series:
+        engine.generate_batch(prompts[0], num_samples=TRAJ, max_tokens=NEW, sampler=sampler)  # warm-up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s, prompt in enumerate(prompts):
+            engine.generate_batch(prompt, num_samples=TRAJ, max_tokens=NEW, sampler=sampler, seed=s)
+        torch.cuda.synchronize()
+        series_s = time.perf_counter() - t0
+    # the whole job as one call: 64 prompts x 100 trajectories, one decode
+    # loop; the median of 5 calls after the capturing one, from a collected
+    # heap (each call builds 12800 Python lists, and a full garbage
+    # collection that one call happens to trigger costs as much as the call)
     engine.generate_multi_batch(prompts, num_samples=TRAJ, max_tokens=NEW, sampler=sampler)  # capture
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    engine.generate_multi_batch(prompts, num_samples=TRAJ, max_tokens=NEW, sampler=sampler)
-    torch.cuda.synchronize()
-    multi = time.perf_counter() - t0
+    gc.collect()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        engine.generate_multi_batch(prompts, num_samples=TRAJ, max_tokens=NEW, sampler=sampler)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    multi = statistics.median(times)
     tokens = SERIES * TRAJ * NEW
     return {
         "workload": "configs[1] through the Engine: 64 series x 100 trajectories, 96-token prompts, "
                     "48 temperature-1 steps, README GPT (2 layers, d64, h4); tokens_per_s: one "
                     "generate_multi_batch call (one prefill of the 64 prompts, one decode loop over the "
-                    "6400 rows, each series' prompt cache stored once)",
+                    "6400 rows, each series' prompt cache stored once), median of 5 calls",
         "dtype": dtype_name,
         "tokens_per_s": tokens / multi,
         "seconds": multi,
-        "per_series_calls_tokens_per_s": tokens / per_series,
-        "per_series_calls_seconds": per_series,
+        "seconds_min_max": [min(times), max(times)],
+        "per_series_calls_tokens_per_s": None if series_s is None else tokens / series_s,
+        "per_series_calls_seconds": series_s,
     }
 
 
@@ -755,6 +768,9 @@ def main():
     ap.add_argument("--single-mode", action="store_true", help="skip the other decode-mode leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--engine-only", action="store_true",
+                    help="run only the engine leg's one-call configs[1] job (twice: capture, then timed) "
+                         "and print its JSON")
     ap.add_argument("--no-jobs", action="store_true",
                     help="skip the configs[3] / configs[4] whole-job legs (decode jobs and end-to-end Engine)")
     args = ap.parse_args()
@@ -770,6 +786,9 @@ def main():
         calib_copy()
     if args.shapes_only:
         print(json.dumps(shapes_leg()), flush=True)
+        return
+    if args.engine_only:
+        print(json.dumps(engine_leg(args.dtype, per_series=False)), flush=True)
         return
     shared = args.decode_mode == "shared"
     res = decode_job(args.dtype, args.steps, args.warmup, shared)

@@ -14,6 +14,7 @@ cache shared by its ``num_samples`` rows, one captured decode step for all
 rows -- with a schedule that may differ per prompt or per row.
 """
 
+import gc
 from collections import deque
 from typing import Generator, Sequence
 
@@ -23,6 +24,7 @@ import torch
 from diff_gpt.model.gpt import BaseGPT
 from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.sampler.sampler import Sampler
+from diff_gpt.sampler.temperature import draw_one
 
 
 class RowState:
@@ -261,15 +263,32 @@ class Engine:
             kwargs.get("force_schedule"), per_prompt=per_prompt,
         ):
             columns.append(column)
-            masks.append(mask if isinstance(mask, torch.Tensor) else torch.full((rows,), mask, dtype=torch.long))
-        T = len(prompts[0])
-        if columns:
-            generated = torch.stack(columns, dim=1).tolist()
-            mask_rows = torch.stack([m.to(columns[0].device) for m in masks], dim=1).tolist()
-        else:
-            generated = mask_rows = [[] for _ in range(rows)]
-        results = [list(prompts[r // num_samples]) + generated[r] for r in range(rows)]
-        out_masks = [[0] * T + mask_rows[r] for r in range(rows)]
+            masks.append(mask)
+        T, steps = len(prompts[0]), len(columns)
+        # the token columns reach the host in one copy; the mask of a step that
+        # samples or forces every row is known on the host already
+        mask_np = np.empty((rows, steps), dtype=np.int64)
+        on_device = [s for s, m in enumerate(masks) if isinstance(m, torch.Tensor)]
+        for s, m in enumerate(masks):
+            if not isinstance(m, torch.Tensor):
+                mask_np[:, s] = m
+        if on_device:
+            mask_np[:, on_device] = torch.stack([masks[s] for s in on_device], dim=1).cpu().numpy()
+        gen_np = torch.stack(columns, dim=1).cpu().numpy() if columns else np.empty((rows, 0), dtype=np.int64)
+        # about 2 * rows lists of Python ints are built here: with the garbage
+        # collector running, a full collection triggered meanwhile walks every
+        # list already built (measured: 100+ ms on a 6400-row call)
+        gc_enabled = gc.isenabled()
+        gc.disable()
+        try:
+            generated = gen_np.tolist()
+            mask_rows = mask_np.tolist()
+            results = [prompts[r // num_samples] + generated[r] for r in range(rows)]
+            zeros = [0] * T
+            out_masks = [zeros + mask_rows[r] for r in range(rows)]
+        finally:
+            if gc_enabled:
+                gc.enable()
         return results, out_masks
 
     def _schedule(self, force_schedule, steps: int, n_prompts: int, num_samples: int, per_prompt: bool,
@@ -393,9 +412,7 @@ class Engine:
                     if sampler is not None:
                         picked = sampler(logits, rng=rng)
                     else:
-                        picked = torch.multinomial(
-                            torch.softmax(logits, dim=-1), num_samples=1, generator=rng
-                        )
+                        picked = draw_one(torch.softmax(logits, dim=-1), rng)
                     column = picked[:, 0]
                     mask = 1
                     if kind == _MIXED:

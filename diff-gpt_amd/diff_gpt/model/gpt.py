@@ -18,7 +18,7 @@ from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.model.rms_norm import rms_norm
 from diff_gpt.model.rope import precompute_freqs_cis
 from diff_gpt.sampler.sampler import Sampler
-from diff_gpt.sampler.temperature import TemperatureSampler
+from diff_gpt.sampler.temperature import TemperatureSampler, draw_one
 
 
 def _ordinal_target_table(V: int, sigma: float, dtype: torch.dtype, device) -> torch.Tensor:
@@ -243,7 +243,7 @@ class GPT(BaseGPT):
             if sampler is not None:
                 nxt = sampler(last, rng=rng)
             else:
-                nxt = torch.multinomial(F.softmax(last, dim=-1), num_samples=1, generator=rng)
+                nxt = draw_one(F.softmax(last, dim=-1), rng)
             out[:, cur] = nxt.squeeze()
         return out
 

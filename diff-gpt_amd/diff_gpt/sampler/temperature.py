@@ -10,6 +10,19 @@ import torch
 from diff_gpt.sampler.sampler import Sampler
 
 
+def draw_one(probs: torch.Tensor, rng: torch.Generator | None = None) -> torch.Tensor:
+    """torch.multinomial(probs, num_samples=1, generator=rng): the same ids
+    and the same use of the generator's stream, by torch's own single-draw
+    algorithm -- an Exp(1) variate q per entry, then the first maximum of
+    probs / q along the last dim -- without multinomial's validity checks
+    (full-tensor min / max / sum reductions and device asserts, more than
+    half of the sampling step's device time on a (6400, 256) batch).  Rows
+    with inf, nan or negative entries, or summing to 0, which multinomial
+    would reject, get an id here."""
+    q = torch.empty_like(probs).exponential_(1, generator=rng)
+    return torch.argmax(probs / q, dim=-1, keepdim=True)
+
+
 class TemperatureSampler(Sampler):
     """Sampler with Temperature"""
 
@@ -23,5 +36,6 @@ class TemperatureSampler(Sampler):
     ) -> torch.Tensor:
         if self.temperature == 0:
             return torch.argmax(logits, dim=-1, keepdim=True)
-        probs = torch.softmax(logits / self.temperature, dim=-1)
-        return torch.multinomial(probs, num_samples=1, generator=rng)
+        # x / 1 is x bit for bit: no division pass at temperature 1
+        scaled = logits if self.temperature == 1 else logits / self.temperature
+        return draw_one(torch.softmax(scaled, dim=-1), rng)

@@ -162,3 +162,53 @@ def test_predict_samples_with_nucleus(dev):
     assert np.isfinite(a).all()
     assert np.array_equal(a, b)
     assert len({tuple(row) for row in a.reshape(16, -1)}) > 1
+
+
+def _gen_state(g):
+    return g.get_state()
+
+
+@pytest.mark.parametrize("device", DEVICES)
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("shape", [(6400, 256), (7, 50), (256,), (3, 1)])
+def test_draw_one_equals_torch_multinomial(device, dtype, shape):
+    """draw_one reproduces torch.multinomial(probs, 1, generator) bit for bit --
+    the same ids and the generator left in the same state -- on softmax
+    probabilities, on rows with zero entries (as the nucleus leaves them),
+    one-hot rows, and a 1-D distribution; with a generator and with the
+    default one."""
+    from diff_gpt.sampler.temperature import draw_one
+
+    logits = _randn(shape, 31 + len(shape), device).to(dtype)
+    probs = torch.softmax(logits, dim=-1)
+    if len(shape) == 2 and shape[1] > 2:
+        probs[: shape[0] // 2, ::3] = 0  # zero entries
+        probs[-1] = 0
+        probs[-1, -1] = 1  # one-hot row
+    for seed in (0, 5, 123):
+        g1, g2 = _gen(device, seed), _gen(device, seed)
+        want = torch.multinomial(probs, num_samples=1, generator=g1)
+        got = draw_one(probs, g2)
+        assert got.shape == want.shape and got.dtype == want.dtype
+        assert torch.equal(got, want), seed
+        assert torch.equal(_gen_state(g1), _gen_state(g2))
+        # again from the state both generators are left in
+        assert torch.equal(draw_one(probs, g2), torch.multinomial(probs, num_samples=1, generator=g1))
+    torch.manual_seed(9)
+    want = torch.multinomial(probs, num_samples=1)
+    torch.manual_seed(9)
+    assert torch.equal(draw_one(probs), want)
+
+
+@pytest.mark.parametrize("device", DEVICES)
+@pytest.mark.parametrize("temperature", [1.0, 0.7, 3.0])
+def test_temperature_sampler_equals_reference_formula(device, temperature):
+    """TemperatureSampler(T) returns the reference's
+    torch.multinomial(softmax(logits / T), 1, generator) ids, T = 1 included
+    (where it skips the division: x / 1 is x)."""
+    logits = _randn((500, 256), 77, device)
+    for dtype in (torch.float32, torch.bfloat16):
+        x = logits.to(dtype)
+        want = torch.multinomial(torch.softmax(x / temperature, dim=-1), num_samples=1, generator=_gen(device, 4))
+        got = TemperatureSampler(temperature)(x, rng=_gen(device, 4))
+        assert torch.equal(got, want)
