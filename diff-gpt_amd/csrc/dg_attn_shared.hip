@@ -55,6 +55,33 @@
 
 namespace dg {
 
+#ifdef DG_TIMELINE
+// Measurement build only (build.py --timeline, read by timeline.py): every
+// wave of attn_shared_kernel stamps the shader clock at its phase boundaries
+// and writes 8 values per (block, wave) to the buffer set by
+// dg_timeline_set -- 6 stamps, the end, and the HW_ID register.
+__device__ unsigned long long* g_timeline;
+__device__ __forceinline__ unsigned long long stamp_now() {
+  unsigned long long t;
+  asm volatile("s_memtime %0\n s_waitcnt lgkmcnt(0)" : "=s"(t) :: "memory");
+  return t;
+}
+#define DG_STAMP(i) (tl_[i] = stamp_now())
+#define DG_TIMELINE_FLUSH()                                                                               \
+  do {                                                                                                    \
+    const unsigned long long te_ = stamp_now();                                                           \
+    if (g_timeline && lane < 8) {                                                                         \
+      const unsigned long long v_ = lane == 0 ? tl_[0] : lane == 1 ? tl_[1] : lane == 2 ? tl_[2]          \
+                                  : lane == 3 ? tl_[3] : lane == 4 ? tl_[4] : lane == 5 ? tl_[5]          \
+                                  : lane == 6 ? te_ : (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4); \
+      g_timeline[((size_t)blockIdx.x * 2 + role) * 8 + lane] = v_;                                        \
+    }                                                                                                     \
+  } while (0)
+#else
+#define DG_STAMP(i) ((void)0)
+#define DG_TIMELINE_FLUSH() ((void)0)
+#endif
+
 struct SharedArgs {
   const void* q;  // attention q (unfused), or the step's q projection (fused)
   const void* k;  // cache pages (keys at position t: k + b*kb + t*kt + h*kh)
@@ -235,6 +262,9 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
 
   const int lane = threadIdx.x & 63;
   const int role = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // 0: prefix, 1: own keys
+#ifdef DG_TIMELINE
+  unsigned long long tl_[6] = {stamp_now(), 0, 0, 0, 0, 0};
+#endif
   // the tiles and heads of one group run on one XCD, whose L2 keeps the prefix
   int unit = blockIdx.x;
   if ((gridDim.x & 7) == 0) unit = (blockIdx.x & 7) * (gridDim.x >> 3) + (blockIdx.x >> 3);
@@ -450,6 +480,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
       load_vec<T, EPL>(qbase + bo * a.qb + piece * EPL, xq);
       load_vec<FT, EPL>(fbase, cs);
       first_chunks();
+      DG_STAMP(1);  // wave 0: q and the first prefix chunks issued
       Slice qs;
       rotate_q(xq, cs, qs);
       // gathered from the quad layout: own lane 4c + (g*DQ)/EPL (key lane 0)
@@ -591,6 +622,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
         prefix_chunk(c0, kopA, 0);
       }
     }
+    DG_STAMP(2);  // wave 0: prefix done
   } else {
     // --- wave 1: own keys on the vector ALUs; fused: the new token -----------------
     // One path per number of register sets issued up front (wave-uniform):
@@ -614,6 +646,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
 #pragma unroll
       for (int k = 0; k < NS; ++k) load_set(k, k);
       __builtin_amdgcn_sched_barrier(0);
+      DG_STAMP(1);  // wave 1: q and the first register sets issued
       if constexpr (FUSED) {
         rotate_q(xq, cs, qs);
         rope_rotate<T, EPL>(xk, cs);
@@ -625,8 +658,10 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
           store_row<T, EPL>(const_cast<T*>(vbase) + bo * a.vb + (int64_t)Tc * vt + piece * EPL, vnew);
         }
       }
+      DG_STAMP(2);  // wave 1: RoPE, QK-norm and the append done
       if constexpr (NS == 2) own_stream(qs, nsets);
       if constexpr (NS == 1) process(kr[0], vr[0], P, qs);
+      DG_STAMP(3);  // wave 1: own-key stream done
       if constexpr (FUSED) {  // the appended key, from registers (key lane 0 of each quad)
         const float dot = group_sum_dpp<LPK>(slice_dot<T, EPL>(qs, knew));
         const float sn = kk == 0 ? dot : kNegInf;
@@ -634,13 +669,18 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
         add_key(sn, vnew, mo * cl);
       }
       hand_over();
+      DG_STAMP(4);  // wave 1: new key and hand-over done
     };
     if (nsets >= 2) own_wave(IntConst<2>{});
     else if (nsets == 1) own_wave(IntConst<1>{});
     else own_wave(IntConst<0>{});
   }
   __syncthreads();
-  if (role == 1) return;
+  DG_STAMP(5);  // both: past the barrier
+  if (role == 1) {
+    DG_TIMELINE_FLUSH();
+    return;
+  }
 
   // --- merge (wave 0): lane (c, g) holds columns 16t + 4g + r of row c --------
   const float* pr = part + c * RS;
@@ -658,6 +698,7 @@ __global__ __launch_bounds__(128, 4) void attn_shared_kernel(const SharedArgs a)
     if (cvalid)
       store_vec<T, 4>(static_cast<T*>(a.y) + bc * a.yb + (int64_t)h * a.yh + 16 * t + 4 * g, out);
   }
+  DG_TIMELINE_FLUSH();
 }
 
 // ---------------------------------------------------------------------------
@@ -779,3 +820,18 @@ int shared_decode_step(int B, int H, int D, int dtype, const void* q, const dg_s
 }
 
 }  // namespace dg
+
+#ifdef DG_TIMELINE
+// Measurement build only: where the shared kernel's waves write their stamps
+// (NULL: nowhere), and an empty kernel of a given grid for the launch floor.
+namespace dg {
+__global__ void timeline_empty_kernel() {}
+}  // namespace dg
+extern "C" __attribute__((visibility("default"))) int dg_timeline_set(void* buffer) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(dg::g_timeline), &buffer, sizeof(buffer));
+}
+extern "C" __attribute__((visibility("default"))) int dg_timeline_empty(int blocks, int threads, void* stream) {
+  hipLaunchKernelGGL(dg::timeline_empty_kernel, dim3(blocks), dim3(threads), 0, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+#endif
