@@ -247,6 +247,243 @@ int res_pick(int npad, const AttnResArgs& a, hipStream_t s) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// One layer's work around its attention, in two launches (block.py:87-107 with
+// mha.py:39-42 and :84-85, feed_forward.py:10-14):
+//
+//   block_in_kernel   out = rms_norm(block_attn_res(sources, w)) @ W^T: the
+//                     sub-layer's mixture and norm, then the q/k/v/g
+//                     projection (one GEMM against the concatenated weights)
+//   block_out_kernel  after the attention: a = y * sigmoid(g); attn_out =
+//                     a @ W_proj^T; the partial sum (attn_out, or partial_in +
+//                     attn_out inside a block); the MLP's mixture over the
+//                     committed blocks and that partial, its norm; the FFN
+//                     (C -> 4C, clamped SwiGLU, 2C -> C); and the residual
+//
+// A workgroup of 4 waves takes 16 token rows.  The stages meet in LDS (rows
+// padded by 16 bytes, so the 16 rows of a matrix-core operand read fall on
+// different banks); every GEMM is a sequence of 16 x 16 output tiles on the
+// matrix cores (qk_mfma's lane mapping: lane (c, g) feeds weight row
+// 16t + c and token row c with the contiguous quarter g of the contraction,
+// and gets back token row c's outputs 16t + 4g .. 16t + 4g + 3), the tiles of a
+// stage dealt round-robin to the 4 waves.  Every intermediate is rounded to T
+// where the torch sequence rounds it -- the gate as gate_kernel, each GEMM's
+// fp32 sum once, the mixture as attn_res_norm_kernel, the SwiGLU as
+// swiglu_kernel, the residual adds -- so bf16 follows the same rounding steps;
+// only the GEMMs' summation order differs from hipBLASLt's.  C is 64 or 128.
+// ---------------------------------------------------------------------------
+constexpr int kLayerRows = 16;
+
+struct BlockInArgs {
+  const void* src[kMaxResSources];
+  int64_t ld[kMaxResSources];
+  const void* w_mix;  // (C,) pseudo-query
+  const void* w;      // (N, C) projection weights
+  void* out;          // (M, N)
+  int64_t w_ld, out_ld, M;
+  int nsrc, N;
+};
+
+struct BlockOutArgs {
+  const void* y;        // (M, C) attention output (before the gate)
+  const void* g;        // (M, C) gate logits
+  const void* w_proj;   // (C, C)
+  const void* pin;      // (M, C) partial sum entering the layer; null when the layer commits it
+  const void* blk[kMaxResSources];  // committed blocks (the MLP mixture's first sources)
+  int64_t blk_ld[kMaxResSources];
+  const void* w_mix;    // (C,)
+  const void* w_up;     // (4C, C)
+  const void* w_down;   // (C, 2C)
+  void* out;            // (M, C) partial sum leaving the layer
+  int64_t y_ld, g_ld, wp_ld, pin_ld, wu_ld, wd_ld, out_ld, M;
+  int nblk;
+  float alpha, limit;
+};
+
+// LDS row stride (elements) of a K-wide operand matrix: 16 bytes of padding
+template <typename T, int K>
+constexpr int lds_ld() {
+  return K + 16 / (int)sizeof(T);
+}
+
+// One 16 x 16 output tile over a K-long contraction: weight rows
+// w + (16t + c) * w_ld from global memory, token rows of the LDS matrix x.
+template <typename T, int K>
+__device__ __forceinline__ f32x4_t layer_tile(const T* __restrict__ w, int64_t w_ld, int t, const T* x, int lane) {
+  constexpr int CQ = K / 4;  // contraction elements of a lane's quarter
+  constexpr int KCH = 16;
+  static_assert(CQ % KCH == 0, "contraction chunking");
+  const int c = lane & 15, g = lane >> 4;
+  const T* wr = w + (int64_t)(16 * t + c) * w_ld + g * CQ;
+  const T* xr = x + c * lds_ld<T, K>() + g * CQ;
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k0 = 0; k0 < CQ; k0 += KCH) {
+    RowRegs<T, KCH> wo, xo;
+    load_row<T, KCH>(wo, wr + k0);
+    load_row<T, KCH>(xo, xr + k0);
+    acc = qk_mfma<T, KCH>(wo, xo, acc);
+  }
+  return acc;
+}
+
+// rms_norm(block_attn_res(V, w)) of the 16 rows into LDS xn, with
+// attn_res_norm_kernel's arithmetic; 16 lanes per row (CH = C / 16 elements
+// each).  Sources 0 .. nmem-1 are rows of global tensors; with lds_last the
+// last source is the LDS matrix last.
+template <typename T, int C>
+__device__ __forceinline__ void layer_mixture(const void* const* src, const int64_t* ld, int nmem, const T* last,
+                                              const void* w_mix, int64_t row0, int64_t M, T* xn) {
+#pragma clang fp contract(off)
+  constexpr int CH = C / 16;
+  constexpr int G = 16;
+  const int r = threadIdx.x / G, sub = threadIdx.x % G, c0 = sub * CH;
+  const int64_t row = min(row0 + r, M - 1);  // rows past M: a finite copy, never stored
+  const int nsrc = nmem + (last != nullptr ? 1 : 0);
+  auto load = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
+    if (n < nmem) load_vec<T, CH>(static_cast<const T*>(src[n]) + row * ld[n] + c0, x);
+    else load_vec<T, CH>(last + r * lds_ld<T, C>() + c0, x);
+  };
+  float w[CH];
+  load_vec<T, CH>(static_cast<const T*>(w_mix) + c0, w);
+  float score[kMaxResSources];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n) {
+    score[n] = -INFINITY;
+    if (n >= nsrc) continue;  // uniform
+    float x[CH];
+    load(n, x);
+    row_rms<CH, G>(x, C);
+    float prod[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) prod[i] = rt<T>(x[i]) * w[i];
+    float dot = tree_sum<CH>(prod);
+    dot = group_sum<G>(dot);
+    score[n] = rt<T>(dot);
+    mx = fmaxf(mx, score[n]);
+  }
+  float e[kMaxResSources];
+  float sum = 0.f;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n) {
+    e[n] = 0.f;
+    if (n >= nsrc) continue;
+    e[n] = expf(score[n] - mx);
+    sum += e[n];
+  }
+  float h[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) h[i] = 0.f;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n) {
+    if (n >= nsrc) continue;
+    const float p = rt<T>(e[n] / sum);
+    float x[CH];
+    load(n, x);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) h[i] = h[i] + rt<T>(p * x[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < CH; ++i) h[i] = rt<T>(h[i]);
+  row_rms<CH, G>(h, C);
+  store_vec<T, CH>(xn + r * lds_ld<T, C>() + c0, h);
+}
+
+template <typename T, int C>
+__global__ __launch_bounds__(256) void block_in_kernel(const BlockInArgs a) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) T xn[kLayerRows * lds_ld<T, C>()];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row0 = (int64_t)blockIdx.x * kLayerRows;
+  layer_mixture<T, C>(a.src, a.ld, a.nsrc, nullptr, a.w_mix, row0, a.M, xn);
+  __syncthreads();
+  const int c = lane & 15, g = lane >> 4;
+  const bool store = row0 + c < a.M;
+  T* orow = static_cast<T*>(a.out) + (row0 + c) * a.out_ld + 4 * g;
+  for (int t = wv; t < a.N / 16; t += 4) {
+    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w), a.w_ld, t, xn, lane);
+    float o[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (store) store_vec<T, 4>(orow + 16 * t, o);
+  }
+}
+
+template <typename T, int C>
+__global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
+#pragma clang fp contract(off)
+  constexpr int LDC = lds_ld<T, C>(), LDH = lds_ld<T, 2 * C>();
+  constexpr int CH = C / 16;
+  __shared__ __attribute__((aligned(16))) T ga[kLayerRows * LDC];  // gated attention output, then xn
+  __shared__ __attribute__((aligned(16))) T pm[kLayerRows * LDC];  // the partial sum after the attention
+  __shared__ __attribute__((aligned(16))) T hh[kLayerRows * LDH];  // SwiGLU output
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int64_t row0 = (int64_t)blockIdx.x * kLayerRows;
+  // 1) gate (gate_kernel's arithmetic): 16 lanes per row
+  {
+    const int r = threadIdx.x / 16, c0 = (threadIdx.x % 16) * CH;
+    const int64_t row = min(row0 + r, a.M - 1);
+    float y[CH], gl[CH];
+    load_vec<T, CH>(static_cast<const T*>(a.y) + row * a.y_ld + c0, y);
+    load_vec<T, CH>(static_cast<const T*>(a.g) + row * a.g_ld + c0, gl);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) y[i] = y[i] * rt<T>(sigmoid_f32(gl[i]));
+    store_vec<T, CH>(ga + r * LDC + c0, y);
+  }
+  __syncthreads();
+  // 2) c_proj, then the partial sum
+  const int64_t crow = min(row0 + c, a.M - 1);
+  for (int t = wv; t < C / 16; t += 4) {
+    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w_proj), a.wp_ld, t, ga, lane);
+    const int f = 16 * t + 4 * g;
+    float p[4];
+    if (a.pin != nullptr) {
+      float pi[4];
+      load_vec<T, 4>(static_cast<const T*>(a.pin) + crow * a.pin_ld + f, pi);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = pi[i] + rt<T>(acc[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = acc[i];
+    }
+    store_vec<T, 4>(pm + c * LDC + f, p);
+  }
+  __syncthreads();
+  // 3) the MLP's mixture over the committed blocks and the new partial; its
+  //    norm overwrites the gated rows (no longer read)
+  layer_mixture<T, C>(a.blk, a.blk_ld, a.nblk, pm, a.w_mix, row0, a.M, ga);
+  __syncthreads();
+  // 4) FFN up + SwiGLU (swiglu_kernel's arithmetic on the interleaved
+  //    (gate, linear) pairs: features 2j, 2j + 1 -> hidden j)
+  for (int t = wv; t < 4 * C / 16; t += 4) {
+    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w_up), a.wu_ld, t, ga, lane);
+    float hv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float gate = fminf(rt<T>(acc[2 * q]), a.limit);
+      const float lin = fminf(fmaxf(rt<T>(acc[2 * q + 1]), -a.limit), a.limit);
+      const float s = rt<T>(sigmoid_f32(rt<T>(a.alpha * gate)));
+      hv[q] = rt<T>(gate * s) * rt<T>(lin + 1.0f);
+    }
+    store_vec<T, 2>(hh + c * LDH + 8 * t + 2 * g, hv);
+  }
+  __syncthreads();
+  // 5) FFN down + residual
+  const bool store = row0 + c < a.M;
+  T* orow = static_cast<T*>(a.out) + (row0 + c) * a.out_ld;
+  for (int t = wv; t < C / 16; t += 4) {
+    const f32x4_t acc = layer_tile<T, 2 * C>(static_cast<const T*>(a.w_down), a.wd_ld, t, hh, lane);
+    const int f = 16 * t + 4 * g;
+    float pmv[4], o[4];
+    load_vec<T, 4>(pm + c * LDC + f, pmv);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = pmv[i] + rt<T>(acc[i]);
+    if (store) store_vec<T, 4>(orow + f, o);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // lm_head + softcap + greedy argmax.  Block = 4 waves = 16 rows of x; wave w
 // takes the vocabulary entries [w V/4, (w+1) V/4) in NTW tiles of 16.  Per
 // tile, logits^T (16 entries x 16 rows) = W_tile x^T on the matrix cores with
@@ -489,4 +726,95 @@ extern "C" int dg_lm_head(int64_t M, int C, int V, int dtype, const void* x, int
   if (dtype == DG_F32) return launch_lm_head<float>(a, s);
   if (dtype == DG_BF16) return launch_lm_head<bf16_t>(a, s);
   return launch_lm_head<f16_t>(a, s);
+}
+
+namespace {
+bool rows16(const void* p, int64_t ld, int64_t es) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld * es) % 16 == 0;
+}
+}  // namespace
+
+extern "C" int dg_block_in(int64_t M, int C, int N, int dtype, int nsrc, const void* const* src,
+                           const int64_t* src_ld, const void* w_mix, const void* w, int64_t w_ld, void* out,
+                           int64_t out_ld, void* stream) {
+  DG_REQUIRE(M >= 0 && C >= 1 && N >= 1, DG_EINVAL, "block_in: bad sizes M=%lld C=%d N=%d", (long long)M, C, N);
+  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "block_in: dtype %d unsupported", dtype);
+  DG_REQUIRE(C == 64 || C == 128, DG_EUNSUPPORTED, "block_in: n_embd %d unsupported (64 or 128)", C);
+  DG_REQUIRE(N % 16 == 0, DG_EUNSUPPORTED, "block_in: %d outputs per row unsupported (a multiple of 16)", N);
+  DG_REQUIRE(nsrc >= 1 && nsrc <= kMaxResSources, DG_EINVAL, "block_in: %d sources (1..%d)", nsrc, kMaxResSources);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(src && src_ld && w_mix && w && out, DG_EINVAL, "block_in: NULL pointer");
+  DG_REQUIRE(M <= (int64_t)kLayerRows * 0x7fffffffLL, DG_EINVAL, "block_in: too many rows (%lld)", (long long)M);
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  BlockInArgs a{};
+  bool ok = rows16(w_mix, 0, es) && rows16(w, w_ld, es) && rows16(out, out_ld, es) && w_ld >= C && out_ld >= N;
+  for (int n = 0; n < nsrc; ++n) {
+    DG_REQUIRE(src[n] != nullptr && src_ld[n] >= C, DG_EINVAL, "block_in: source %d is NULL or narrower than C", n);
+    ok = ok && rows16(src[n], src_ld[n], es);
+    a.src[n] = src[n];
+    a.ld[n] = src_ld[n];
+  }
+  DG_REQUIRE(ok, DG_EUNSUPPORTED, "block_in: rows must be 16-byte aligned");
+  a.w_mix = w_mix; a.w = w; a.out = out;
+  a.w_ld = w_ld; a.out_ld = out_ld; a.M = M; a.nsrc = nsrc; a.N = N;
+  const dim3 grid((unsigned)((M + kLayerRows - 1) / kLayerRows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define DG_BLOCK_IN(T)                                                                              \
+  do {                                                                                            \
+    if (C == 64) hipLaunchKernelGGL((block_in_kernel<T, 64>), grid, dim3(256), 0, s, a);          \
+    else hipLaunchKernelGGL((block_in_kernel<T, 128>), grid, dim3(256), 0, s, a);                 \
+  } while (0)
+  if (dtype == DG_F32) DG_BLOCK_IN(float);
+  else if (dtype == DG_BF16) DG_BLOCK_IN(bf16_t);
+  else DG_BLOCK_IN(f16_t);
+#undef DG_BLOCK_IN
+  return check_launch("block_in_kernel");
+}
+
+extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
+                            const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,
+                            const void* const* blocks, const int64_t* blocks_ld, const void* w_mix,
+                            const void* w_up, int64_t wu_ld, const void* w_down, int64_t wd_ld, float alpha,
+                            float limit, void* out, int64_t out_ld, void* stream) {
+  DG_REQUIRE(M >= 0 && C >= 1, DG_EINVAL, "block_out: bad sizes M=%lld C=%d", (long long)M, C);
+  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "block_out: dtype %d unsupported", dtype);
+  DG_REQUIRE(C == 64 || C == 128, DG_EUNSUPPORTED, "block_out: n_embd %d unsupported (64 or 128)", C);
+  DG_REQUIRE(nblk >= 0 && nblk + 1 <= kMaxResSources, DG_EINVAL, "block_out: %d blocks (0..%d)", nblk,
+             kMaxResSources - 1);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(y && g && w_proj && w_mix && w_up && w_down && out && (nblk == 0 || (blocks && blocks_ld)), DG_EINVAL,
+             "block_out: NULL pointer");
+  DG_REQUIRE(M <= (int64_t)kLayerRows * 0x7fffffffLL, DG_EINVAL, "block_out: too many rows (%lld)", (long long)M);
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  BlockOutArgs a{};
+  bool ok = rows16(y, y_ld, es) && rows16(g, g_ld, es) && rows16(w_proj, wp_ld, es) && rows16(w_mix, 0, es) &&
+            rows16(w_up, wu_ld, es) && rows16(w_down, wd_ld, es) && rows16(out, out_ld, es) &&
+            (partial_in == nullptr || rows16(partial_in, pin_ld, es));
+  DG_REQUIRE(y_ld >= C && g_ld >= C && wp_ld >= C && wu_ld >= C && wd_ld >= 2 * C && out_ld >= C &&
+                 (partial_in == nullptr || pin_ld >= C),
+             DG_EINVAL, "block_out: a row stride is narrower than its row");
+  for (int n = 0; n < nblk; ++n) {
+    DG_REQUIRE(blocks[n] != nullptr && blocks_ld[n] >= C, DG_EINVAL, "block_out: block %d is NULL or narrower than C",
+               n);
+    ok = ok && rows16(blocks[n], blocks_ld[n], es);
+    a.blk[n] = blocks[n];
+    a.blk_ld[n] = blocks_ld[n];
+  }
+  DG_REQUIRE(ok, DG_EUNSUPPORTED, "block_out: rows must be 16-byte aligned");
+  a.y = y; a.g = g; a.w_proj = w_proj; a.pin = partial_in; a.w_mix = w_mix; a.w_up = w_up; a.w_down = w_down;
+  a.out = out;
+  a.y_ld = y_ld; a.g_ld = g_ld; a.wp_ld = wp_ld; a.pin_ld = pin_ld; a.wu_ld = wu_ld; a.wd_ld = wd_ld;
+  a.out_ld = out_ld; a.M = M; a.nblk = nblk; a.alpha = alpha; a.limit = limit;
+  const dim3 grid((unsigned)((M + kLayerRows - 1) / kLayerRows));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define DG_BLOCK_OUT(T)                                                                             \
+  do {                                                                                            \
+    if (C == 64) hipLaunchKernelGGL((block_out_kernel<T, 64>), grid, dim3(256), 0, s, a);         \
+    else hipLaunchKernelGGL((block_out_kernel<T, 128>), grid, dim3(256), 0, s, a);                \
+  } while (0)
+  if (dtype == DG_F32) DG_BLOCK_OUT(float);
+  else if (dtype == DG_BF16) DG_BLOCK_OUT(bf16_t);
+  else DG_BLOCK_OUT(f16_t);
+#undef DG_BLOCK_OUT
+  return check_launch("block_out_kernel");
 }

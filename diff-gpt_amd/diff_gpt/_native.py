@@ -175,6 +175,20 @@ _SIGNATURES = {
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
          ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
     ),
+    "dg_block_in": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p],
+    ),
+    "dg_block_out": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+         ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p],
+    ),
 }
 
 ABI_VERSION = 2
@@ -615,6 +629,61 @@ def attn_res_norm_(sources: list[torch.Tensor], w: torch.Tensor, out: torch.Tens
         o2.size(0), C, _dtype_code(o2), n, ptrs, lds, _ptr(w1), _ptr(o2), o2.stride(0), _stream(o2)
     )
     _check(rc, "attn_res_norm")
+
+
+def _row_list(tensors: list[torch.Tensor], what: str):
+    rows = [_rows(t, what) for t in tensors]
+    ptrs = (ctypes.c_void_p * max(1, len(rows)))(*[t.data_ptr() for t in rows])
+    lds = (ctypes.c_int64 * max(1, len(rows)))(*[t.stride(0) for t in rows])
+    return rows, ptrs, lds
+
+
+def block_in_(sources: list[torch.Tensor], w_mix: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> bool:
+    """dg_block_in: out (..., N) = rms_norm(block_attn_res(sources[:-1],
+    sources[-1], w_mix)) @ w^T for w (N, C).  Returns False, having done
+    nothing, for shapes the fused kernel does not take (n_embd other than 64
+    or 128, unaligned rows); raises on any other error."""
+    C = w.size(1)
+    rows, ptrs, lds = _row_list(sources, "block_in")
+    for t in rows:
+        if t.shape != rows[0].shape or t.dtype != out.dtype or t.size(1) != C:
+            raise ValueError("block_in: sources must share shape and dtype with the output")
+    o2, w1 = out.view(-1, out.size(-1)), w_mix.reshape(-1).contiguous()
+    if w.stride(1) != 1 or o2.stride(1) != 1 or w.dtype != out.dtype:
+        return False
+    rc = lib().dg_block_in(o2.size(0), C, w.size(0), _dtype_code(o2), len(rows), ptrs, lds, _ptr(w1), _ptr(w),
+                           w.stride(0), _ptr(o2), o2.stride(0), _stream(o2))
+    if rc == DG_EUNSUPPORTED:
+        return False
+    _check(rc, "block_in")
+    return True
+
+
+def block_out_(y: torch.Tensor, g: torch.Tensor, w_proj: torch.Tensor, partial_in: torch.Tensor | None,
+               blocks: list[torch.Tensor], w_mix: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+               alpha: float, limit: float, out: torch.Tensor) -> bool:
+    """dg_block_out: from the attention output y (..., C) and the gate logits
+    g, the layer's new partial sum into out: c_proj(y * sigmoid(g)), added to
+    partial_in unless that is None (the layer commits its input), then plus
+    the FFN of the MLP mixture over blocks and that partial.  Returns False,
+    having done nothing, for shapes the fused kernel does not take."""
+    C = out.size(-1)
+    y2, g2, o2 = _rows(y, "block_out"), _rows(g, "block_out"), out.view(-1, C)
+    p2 = None if partial_in is None else _rows(partial_in, "block_out")
+    _, ptrs, lds = _row_list(blocks, "block_out")
+    ws = (w_proj, w_up, w_down)
+    if any(t.stride(1) != 1 or t.dtype != out.dtype for t in ws) or o2.stride(1) != 1:
+        return False
+    rc = lib().dg_block_out(
+        o2.size(0), C, _dtype_code(o2), _ptr(y2), y2.stride(0), _ptr(g2), g2.stride(0), _ptr(w_proj),
+        w_proj.stride(0), _ptr(p2), 0 if p2 is None else p2.stride(0), len(blocks), ptrs, lds,
+        _ptr(w_mix.reshape(-1).contiguous()), _ptr(w_up), w_up.stride(0), _ptr(w_down), w_down.stride(0),
+        float(alpha), float(limit), _ptr(o2), o2.stride(0), _stream(o2),
+    )
+    if rc == DG_EUNSUPPORTED:
+        return False
+    _check(rc, "block_out")
+    return True
 
 
 def gate_(y: torch.Tensor, g: torch.Tensor) -> None:

@@ -23,6 +23,10 @@ A decode step over a KV cache (one new token per row) makes one
 dg_decode_step call instead: the same RoPE, QK-norm and append, and the
 attention over the cache including the new token, in one launch where the
 rows share a broadcast prefix (two launches otherwise).
+
+Block.forward may run the projection itself (dg_block_in, fused with the
+mixture before it) and the gate and c_proj too (dg_block_out, fused with the
+MLP after them); it then calls _attend, the part between, directly.
 """
 
 import math
@@ -126,19 +130,30 @@ class MultiHeadAttention(nn.Module):
     ) -> torch.Tensor:
         _native.require_device("MultiHeadAttention", x)
         _native.require_inference("MultiHeadAttention", x, self.c_q.weight)
-        B, T, _ = x.size()
+        qkvg = F.linear(x, self._projection_weight())  # (B, T, 3*inner + C)
+        y = self._attend(qkvg, freqs_cis, kv_cache)
+        ops = _native.ops()
+        ops.gate_(y, self._gate_logits(qkvg))  # y * sigmoid(g)
+        return self.c_proj(y)
+
+    def _gate_logits(self, qkvg: torch.Tensor) -> torch.Tensor:
+        return qkvg[..., 3 * self.n_head * self.head_dim :]
+
+    def _attend(self, qkvg: torch.Tensor, freqs_cis: torch.Tensor, kv_cache: KVCache | None) -> torch.Tensor:
+        """mha.py:44-83 on the projections qkvg (B, T, 3*inner + C), whose
+        column slices are q, k, v and the gate logits: RoPE, QK-norm, the
+        cache append and the attention; returns y (B, T, inner) before the
+        gate."""
+        B, T, _ = qkvg.size()
         H, D = self.n_head, self.head_dim
         ops = _native.ops()
-
         inner = H * D
-        qkvg = F.linear(x, self._projection_weight())  # (B, T, 3*inner + C)
         q = qkvg[..., :inner].view(B, T, H, D)
         k = qkvg[..., inner : 2 * inner].view(B, T, H, D)
         v = qkvg[..., 2 * inner : 3 * inner].view(B, T, H, D)
-        g = qkvg[..., 3 * inner :]
 
         if kv_cache is not None and T == 1:
-            return self._decode_step(q, k, v, g, freqs_cis, kv_cache)
+            return self._decode_step(q, k, v, freqs_cis, kv_cache)
         assert kv_cache is None or kv_cache.pos_dev is None, "a captured decode step takes one token per row"
         # Prefills the MFMA kernel takes rotate and normalise q as they load it
         # (dg_prefill_rope); the first launch then handles k and v only.
@@ -184,17 +199,15 @@ class MultiHeadAttention(nn.Module):
                 y = None
         if y is None:
             y = ops.attention(q_rot, keys, values, scale, prefix_len, group)
-        y = y.view(B, T, H * D)
-        ops.gate_(y, g)  # y * sigmoid(g)
-        return self.c_proj(y)
+        return y.view(B, T, H * D)
 
-    def _decode_step(self, q, k, v, g, freqs, kv_cache: KVCache) -> torch.Tensor:
+    def _decode_step(self, q, k, v, freqs, kv_cache: KVCache) -> torch.Tensor:
         """One new token per row over the KV cache (mha.py:44-68 with T = 1):
         dg_decode_step appends k, v at the cache position and attends over it.
         With kv_cache.pos_dev set the position is read on the device (the
         launch form a HIP graph replays at every position) and freqs is the
         model's whole (Tmax, D/2, 2) table; otherwise freqs is the row of the
-        current position."""
+        current position.  Returns y (B, 1, inner) before the gate."""
         B, T, H, D = q.shape
         cap = kv_cache.kv_shape[4]
         t0, t1 = kv_cache.ensure_window(1, k.dtype, k.device)
@@ -211,6 +224,4 @@ class MultiHeadAttention(nn.Module):
         y = torch.empty_like(q)
         _native.decode_step_(q, k, v, freqs, k_cache, v_cache, y, 1.0 / math.sqrt(D), pos, prefix=prefix)
         kv_cache.advance(self.layer_idx, t1)
-        y = y.view(B, T, H * D)
-        _native.ops().gate_(y, g)  # y * sigmoid(g)
-        return self.c_proj(y)
+        return y.view(B, T, H * D)

@@ -297,3 +297,185 @@ def test_gpt_greedy_generate_uses_fused_argmax(dev, monkeypatch):
         plain = model.generate(idx, 12, TemperatureSampler(0))
     monkeypatch.setattr(_native, "lm_head_", real)
     assert torch.equal(fused, plain)
+
+
+# ------------------------------------------------------------------ a layer in three launches
+
+LAYER = [  # (rows, C, committed blocks, commits its input)
+    (6400, 64, 2, True),    # cfg1 decode step, layer 0: blocks (x, x)
+    (6400, 64, 3, True),    # layer 1
+    (37, 64, 5, False),     # ragged rows; a layer inside a block: partial_in + attention output
+    (100, 128, 3, True),    # n_embd 128
+    (17, 128, 1, False),
+    (1, 64, 30, True),      # one row; 31 mixture sources
+]
+ALPHA, LIMIT = 1.702, 7.0
+
+
+def _layer_case(M, C, nblk, dtype, seed):
+    """Blocks, partial_in, the attention output y, the gate logits g (a column
+    slice of a wider projection row, as in the model) and the layer's weights,
+    with a scale that keeps every stage O(1)."""
+    blocks = [_randn((M, C), seed + i, dtype, 1.0 + 0.3 * i) for i in range(nblk)]
+    pin = _randn((M, C), seed + 50, dtype)
+    y = _randn((M, C), seed + 51, dtype)
+    qkvg = _randn((M, 4 * C), seed + 52, dtype, 2.0)
+    w = {
+        "proj": _randn((C, C), seed + 53, dtype, C ** -0.5),
+        "mix_attn": _randn((1, C), seed + 54, dtype, 0.5),
+        "mix_mlp": _randn((1, C), seed + 55, dtype, 0.5),
+        "qkvg": _randn((4 * C, C), seed + 56, dtype, C ** -0.5),
+        "up": _randn((4 * C, C), seed + 57, dtype, 3.0 * C ** -0.5),
+        "down": _randn((C, 2 * C), seed + 58, dtype, (2 * C) ** -0.5),
+    }
+    return blocks, pin, y, qkvg, w
+
+
+def _swiglu64(h):
+    gl = h[..., ::2].clamp(max=LIMIT)
+    ln = h[..., 1::2].clamp(min=-LIMIT, max=LIMIT)
+    return gl * torch.sigmoid(ALPHA * gl) * (ln + 1)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", LAYER, ids=lambda s: "x".join(map(str, s)))
+def test_block_out_matches_reference(dev, dtype, shape):
+    """dg_block_out (gate, c_proj, the partial sum, the MLP's mixture and norm,
+    FFN up, SwiGLU, FFN down, residual) against the oracle's functions
+    evaluated in float64 on the same inputs (fp32 at 1e-5; bf16 / fp16 at
+    2e-2, or 1.5x the reference's own evaluation in that dtype where its
+    rounding alone exceeds it), and against the separate launches it replaces
+    on the device at the dtype's bar."""
+    from diff_gpt import _native
+    from diff_gpt.model.block import attn_res_norm
+
+    M, C, nblk, committed = shape
+    blocks, pin, y, qkvg, w = _layer_case(M, C, nblk, dtype, 300 + C + nblk)
+    g = qkvg[:, 3 * C:]
+    d = lambda t: t.to(dev)  # noqa: E731
+    out = torch.empty((M, C), dtype=TDT[dtype], device=dev)
+    assert _native.block_out_(d(y), d(qkvg)[:, 3 * C:], d(w["proj"]), None if committed else d(pin),
+                              [d(b) for b in blocks], d(w["mix_mlp"]), d(w["up"]), d(w["down"]), ALPHA, LIMIT, out)
+    # the oracle, float64
+    f = {k: v.double() for k, v in w.items()}
+    a = (y.double() * torch.sigmoid(g.double())) @ f["proj"].T
+    pm = a if committed else pin.double() + a
+    xn = tr.rms(tr.attn_res(tuple(b.double() for b in blocks), pm, f["mix_mlp"]))
+    ref = pm + _swiglu64(xn @ f["up"].T) @ f["down"].T
+    err = _rel(out, ref)
+    # the separate launches on the device (the unfused path)
+    with torch.inference_mode():
+        ya = d(y).clone()
+        _native.ops().gate_(ya, d(qkvg)[:, 3 * C:])
+        a2 = torch.nn.functional.linear(ya, d(w["proj"]))
+        pm2 = a2 if committed else d(pin) + a2
+        xn2 = attn_res_norm(tuple(d(b) for b in blocks), pm2, _Proj(d(w["mix_mlp"])))
+        h2 = _native.ops().swiglu(torch.nn.functional.linear(xn2, d(w["up"])), ALPHA, LIMIT)
+        sep = pm2 + torch.nn.functional.linear(h2, d(w["down"]))
+    # the reference's own evaluation in the dtype (torch on the CPU, each op
+    # rounding as it returns): through seven stages bf16 / fp16 rounding alone
+    # can move the result by about the north-star bar, so the bar against
+    # float64 is that deviation x 1.5 where it exceeds the bar
+    a3 = (y * torch.sigmoid(g)) @ w["proj"].T
+    pm3 = a3 if committed else pin + a3
+    xn3 = tr.rms(tr.attn_res(tuple(blocks), pm3, w["mix_mlp"]))
+    own = _rel(pm3 + _swiglu64(xn3 @ w["up"].T) @ w["down"].T, ref)
+    print(f"block_out {shape} {dtype}: |fused - f64| {err:.3g}, |unfused - f64| {_rel(sep, ref):.3g}, "
+          f"|reference {dtype} - f64| {own:.3g}, |fused - unfused| {_rel(out, sep.double().cpu()):.3g} "
+          f"(x max|ref|)", flush=True)
+    assert err <= max(TOL[dtype], 1.5 * own), (err, own)
+    assert _rel(out, sep.double().cpu()) <= TOL[dtype]
+
+
+class _Proj:
+    """The .weight holder block.attn_res_norm reads its pseudo-query from."""
+
+    def __init__(self, w):
+        self.weight = w
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", LAYER, ids=lambda s: "x".join(map(str, s)))
+def test_block_in_matches_reference(dev, dtype, shape):
+    """dg_block_in (the mixture, its norm, the q/k/v/g projection) against
+    the oracle in float64; with one source it is block.py's short cut (the
+    source's RMSNorm)."""
+    from diff_gpt import _native
+
+    M, C, nblk, _ = shape
+    blocks, pin, _, _, w = _layer_case(M, C, nblk, dtype, 400 + C + nblk)
+    d = lambda t: t.to(dev)  # noqa: E731
+    for sources in (blocks + [pin], [pin]):
+        out = torch.empty((M, 4 * C), dtype=TDT[dtype], device=dev)
+        assert _native.block_in_([d(s) for s in sources], d(w["mix_attn"]), d(w["qkvg"]), out)
+        src64 = [s.double() for s in sources]
+        h = src64[0] if len(src64) == 1 else tr.attn_res(tuple(src64[:-1]), src64[-1], w["mix_attn"].double())
+        ref = tr.rms(h) @ w["qkvg"].double().T
+        assert _rel(out, ref) <= TOL[dtype], len(sources)
+
+
+@pytest.mark.parametrize("C", [32, 96, 256])
+def test_block_kernels_decline_other_widths(dev, C):
+    """n_embd other than 64 or 128: both entry points return False and write
+    nothing (the model then makes the separate launches)."""
+    from diff_gpt import _native
+
+    M = 20
+    blocks, pin, y, qkvg, w = _layer_case(M, C, 2, "f32", 7)
+    d = lambda t: t.to(dev)  # noqa: E731
+    out = torch.full((M, 4 * C), 5.0, device=dev)
+    assert not _native.block_in_([d(pin)], d(w["mix_attn"]), d(w["qkvg"]), out)
+    out2 = torch.full((M, C), 5.0, device=dev)
+    assert not _native.block_out_(d(y), d(qkvg)[:, 3 * C:], d(w["proj"]), None, [d(b) for b in blocks],
+                                  d(w["mix_mlp"]), d(w["up"]), d(w["down"]), ALPHA, LIMIT, out2)
+    torch.cuda.synchronize()
+    assert bool((out == 5.0).all()) and bool((out2 == 5.0).all())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("layers_per_block", [1, 2])
+def test_gpt_layers_in_three_launches_match_separate_launches(dev, dtype, layers_per_block, monkeypatch):
+    """GPT.forward at n_embd 64 runs each layer as dg_block_in, the attention
+    and dg_block_out; with both declined it makes the separate launches.  The
+    logits of a prefill and a decode step agree within the dtype's bar, and
+    the fp32 ones with the oracle forward within 1e-5."""
+    from diff_gpt import _native
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.model.kv_cache import KVCache
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=64, n_head=4, n_layer=4, use_checkpoint=False,
+                attn_res_layers_per_block=layers_per_block).eval()
+    p = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=256, n_embd=64, block_size=64, n_head=4, n_layer=4,
+                         attn_res_layers_per_block=layers_per_block)
+    model = model.to(dev).to(TDT[dtype])
+    idx = torch.randint(0, 256, (3, 20), generator=torch.Generator().manual_seed(2))
+    calls = {"in": 0, "out": 0}
+    real_in, real_out = _native.block_in_, _native.block_out_
+
+    def count(name, fn):
+        def wrapped(*a, **k):
+            calls[name] += 1
+            return fn(*a, **k)
+        return wrapped
+
+    def run():
+        kv = KVCache(batch_size=3, num_heads=4, seq_len=21, head_dim=16, num_layers=4)
+        with torch.inference_mode():
+            first = model(idx.to(dev), kv_cache=kv)[0][:, -1]
+            step = model(first.argmax(-1, keepdim=True), kv_cache=kv)[0][:, -1]
+        return first.float().cpu(), step.float().cpu()
+
+    monkeypatch.setattr(_native, "block_in_", count("in", real_in))
+    monkeypatch.setattr(_native, "block_out_", count("out", real_out))
+    fused = run()
+    assert calls == {"in": 8, "out": 8}  # 4 layers x (prefill, step)
+    monkeypatch.setattr(_native, "block_in_", lambda *a, **k: False)
+    separate = run()
+    for f_, s_ in zip(fused, separate):
+        assert _rel(f_, s_.double()) <= TOL[dtype]
+    if dtype == "f32":
+        with torch.no_grad():
+            ref = tr.forward(p, cfg, idx)[:, -1]
+        assert _rel(fused[0], ref) <= 1e-5
