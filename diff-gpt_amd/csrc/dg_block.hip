@@ -70,16 +70,40 @@ __device__ __forceinline__ void load_slice(const T* p, int c0, int N, bool vec, 
   }
 }
 
+// Sources a lane loads into registers together, up front, to serve both
+// passes of the mixture (one round trip to memory for them, instead of one
+// per source and pass): about 32 registers of slices.
+template <int CH>
+constexpr int res_held() {
+  return CH <= 4 ? 8 : CH <= 8 ? 4 : CH <= 16 ? 2 : 1;
+}
+
 template <typename T, int NPAD, int CH>
 __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a, const int vec) {
 #pragma clang fp contract(off)
   constexpr int G = NPAD / CH;
+  constexpr int HELD = res_held<CH>();
   static_assert(G >= 1 && G <= 64, "row mapping");
   constexpr int ROWS_PER_BLOCK = 256 / G;
   const int sub = threadIdx.x % G;
   const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / G;
   if (row >= a.M) return;  // whole lane groups leave together; no barriers
   const int c0 = sub * CH;
+  auto load = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
+    load_slice<T, CH>(static_cast<const T*>(a.src[n]) + row * a.ld[n] + c0, c0, a.N, vec, x);
+  };
+  float held[HELD][CH];
+#pragma unroll
+  for (int n = 0; n < HELD; ++n)
+    if (n < a.nsrc) load(n, held[n]);  // uniform; no use before all are issued
+  auto get = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
+    if (n < HELD) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) x[i] = held[n][i];
+    } else {
+      load(n, x);
+    }
+  };
   float w[CH];
   load_slice<T, CH>(static_cast<const T*>(a.w) + c0, c0, a.N, vec, w);
 
@@ -91,7 +115,7 @@ __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a,
     score[n] = -INFINITY;
     if (n >= a.nsrc) continue;  // uniform
     float x[CH];
-    load_slice<T, CH>(static_cast<const T*>(a.src[n]) + row * a.ld[n] + c0, c0, a.N, vec, x);
+    get(n, x);
     row_rms<CH, G>(x, a.N);
     float prod[CH];
 #pragma unroll
@@ -120,7 +144,7 @@ __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a,
     if (n >= a.nsrc) continue;
     const float p = rt<T>(e[n] / sum);
     float x[CH];
-    load_slice<T, CH>(static_cast<const T*>(a.src[n]) + row * a.ld[n] + c0, c0, a.N, vec, x);
+    get(n, x);
 #pragma unroll
     for (int i = 0; i < CH; ++i) h[i] = h[i] + rt<T>(p * x[i]);
   }
@@ -247,17 +271,14 @@ int res_pick(int npad, const AttnResArgs& a, hipStream_t s) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// One layer's work around its attention, in two launches (block.py:87-107 with
-// mha.py:39-42 and :84-85, feed_forward.py:10-14):
+// A layer's work after its attention, in one launch (mha.py:84-85,
+// block.py:98-106, feed_forward.py:10-14):
 //
-//   block_in_kernel   out = rms_norm(block_attn_res(sources, w)) @ W^T: the
-//                     sub-layer's mixture and norm, then the q/k/v/g
-//                     projection (one GEMM against the concatenated weights)
-//   block_out_kernel  after the attention: a = y * sigmoid(g); attn_out =
-//                     a @ W_proj^T; the partial sum (attn_out, or partial_in +
-//                     attn_out inside a block); the MLP's mixture over the
-//                     committed blocks and that partial, its norm; the FFN
-//                     (C -> 4C, clamped SwiGLU, 2C -> C); and the residual
+//   block_out_kernel  a = y * sigmoid(g); attn_out = a @ W_proj^T; the
+//                     partial sum (attn_out, or partial_in + attn_out inside
+//                     a block); the MLP's mixture over the committed blocks
+//                     and that partial, its norm; the FFN (C -> 4C, clamped
+//                     SwiGLU, 2C -> C); and the residual
 //
 // A workgroup of 4 waves takes 16 token rows.  The stages meet in LDS (rows
 // padded by 16 bytes, so the 16 rows of a matrix-core operand read fall on
@@ -265,23 +286,18 @@ int res_pick(int npad, const AttnResArgs& a, hipStream_t s) {
 // matrix cores (qk_mfma's lane mapping: lane (c, g) feeds weight row
 // 16t + c and token row c with the contiguous quarter g of the contraction,
 // and gets back token row c's outputs 16t + 4g .. 16t + 4g + 3), the tiles of a
-// stage dealt round-robin to the 4 waves.  Every intermediate is rounded to T
-// where the torch sequence rounds it -- the gate as gate_kernel, each GEMM's
-// fp32 sum once, the mixture as attn_res_norm_kernel, the SwiGLU as
-// swiglu_kernel, the residual adds -- so bf16 follows the same rounding steps;
-// only the GEMMs' summation order differs from hipBLASLt's.  C is 64 or 128.
+// stage dealt round-robin to the 4 waves, each wave's weight fragments
+// fetched a stage or a tile ahead.  Every intermediate is rounded to T where
+// the torch sequence rounds it -- the gate as gate_kernel, each GEMM's fp32
+// sum once, the mixture as attn_res_norm_kernel, the SwiGLU as swiglu_kernel,
+// the residual adds -- so bf16 follows the same rounding steps; only the
+// GEMMs' summation order differs from hipBLASLt's.  C is 64 or 128.
+// (The same fusion before the attention -- the mixture, its norm and the
+// q/k/v/g projection in one launch -- measured no faster than the two
+// launches at 6400 rows and slower beyond: the mixture's dependent chain at
+// the occupancy its registers allow costs what the saved launch gains.)
 // ---------------------------------------------------------------------------
 constexpr int kLayerRows = 16;
-
-struct BlockInArgs {
-  const void* src[kMaxResSources];
-  int64_t ld[kMaxResSources];
-  const void* w_mix;  // (C,) pseudo-query
-  const void* w;      // (N, C) projection weights
-  void* out;          // (M, N)
-  int64_t w_ld, out_ld, M;
-  int nsrc, N;
-};
 
 struct BlockOutArgs {
   const void* y;        // (M, C) attention output (before the gate)
@@ -305,31 +321,49 @@ constexpr int lds_ld() {
   return K + 16 / (int)sizeof(T);
 }
 
-// One 16 x 16 output tile over a K-long contraction: weight rows
-// w + (16t + c) * w_ld from global memory, token rows of the LDS matrix x.
+// A lane's weight fragment of one 16 x 16 output tile over a K-long
+// contraction: weight row 16t + c (c = lane & 15), the contiguous quarter
+// g = lane >> 4 of the contraction, in chunks of 16 elements.  Loaded apart
+// from the product so that a wave can fetch it before the stage that
+// produces the tile's other operand, or one tile ahead.
 template <typename T, int K>
-__device__ __forceinline__ f32x4_t layer_tile(const T* __restrict__ w, int64_t w_ld, int t, const T* x, int lane) {
-  constexpr int CQ = K / 4;  // contraction elements of a lane's quarter
-  constexpr int KCH = 16;
+struct TileW {
+  static constexpr int CQ = K / 4;  // contraction elements of a lane's quarter
+  static constexpr int KCH = 16;
   static_assert(CQ % KCH == 0, "contraction chunking");
+  RowRegs<T, KCH> r[CQ / KCH];
+};
+
+template <typename T, int K>
+__device__ __forceinline__ void load_tile_w(TileW<T, K>& f, const T* __restrict__ w, int64_t w_ld, int t, int lane) {
   const int c = lane & 15, g = lane >> 4;
-  const T* wr = w + (int64_t)(16 * t + c) * w_ld + g * CQ;
+  const T* wr = w + (int64_t)(16 * t + c) * w_ld + g * TileW<T, K>::CQ;
+#pragma unroll
+  for (int i = 0; i < TileW<T, K>::CQ / 16; ++i) load_row<T, 16>(f.r[i], wr + 16 * i);
+}
+
+// The tile's product against the token rows of the LDS matrix x.
+template <typename T, int K>
+__device__ __forceinline__ f32x4_t layer_tile(const TileW<T, K>& f, const T* x, int lane) {
+  constexpr int CQ = TileW<T, K>::CQ;
+  const int c = lane & 15, g = lane >> 4;
   const T* xr = x + c * lds_ld<T, K>() + g * CQ;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k0 = 0; k0 < CQ; k0 += KCH) {
-    RowRegs<T, KCH> wo, xo;
-    load_row<T, KCH>(wo, wr + k0);
-    load_row<T, KCH>(xo, xr + k0);
-    acc = qk_mfma<T, KCH>(wo, xo, acc);
+  for (int i = 0; i < CQ / 16; ++i) {
+    RowRegs<T, 16> xo;
+    load_row<T, 16>(xo, xr + 16 * i);
+    acc = qk_mfma<T, 16>(f.r[i], xo, acc);
   }
   return acc;
 }
 
 // rms_norm(block_attn_res(V, w)) of the 16 rows into LDS xn, with
 // attn_res_norm_kernel's arithmetic; 16 lanes per row (CH = C / 16 elements
-// each).  Sources 0 .. nmem-1 are rows of global tensors; with lds_last the
-// last source is the LDS matrix last.
+// each).  Sources 0 .. nmem-1 are rows of global tensors; with last != null
+// the last source is that LDS matrix.  The first res_held<CH>() sources are
+// loaded into registers together, up front, and serve both passes.
+
 template <typename T, int C>
 __device__ __forceinline__ void layer_mixture(const void* const* src, const int64_t* ld, int nmem, const T* last,
                                               const void* w_mix, int64_t row0, int64_t M, T* xn) {
@@ -343,6 +377,19 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
     if (n < nmem) load_vec<T, CH>(static_cast<const T*>(src[n]) + row * ld[n] + c0, x);
     else load_vec<T, CH>(last + r * lds_ld<T, C>() + c0, x);
   };
+  constexpr int HELD = res_held<CH>();
+  float held[HELD][CH];
+#pragma unroll
+  for (int n = 0; n < HELD; ++n)
+    if (n < nsrc) load(n, held[n]);  // uniform; no use before all are issued
+  auto get = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
+    if (n < HELD) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) x[i] = held[n][i];
+    } else {
+      load(n, x);
+    }
+  };
   float w[CH];
   load_vec<T, CH>(static_cast<const T*>(w_mix) + c0, w);
   float score[kMaxResSources];
@@ -352,7 +399,7 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
     score[n] = -INFINITY;
     if (n >= nsrc) continue;  // uniform
     float x[CH];
-    load(n, x);
+    get(n, x);
     row_rms<CH, G>(x, C);
     float prod[CH];
 #pragma unroll
@@ -379,7 +426,7 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
     if (n >= nsrc) continue;
     const float p = rt<T>(e[n] / sum);
     float x[CH];
-    load(n, x);
+    get(n, x);
 #pragma unroll
     for (int i = 0; i < CH; ++i) h[i] = h[i] + rt<T>(p * x[i]);
   }
@@ -387,25 +434,6 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
   for (int i = 0; i < CH; ++i) h[i] = rt<T>(h[i]);
   row_rms<CH, G>(h, C);
   store_vec<T, CH>(xn + r * lds_ld<T, C>() + c0, h);
-}
-
-template <typename T, int C>
-__global__ __launch_bounds__(256) void block_in_kernel(const BlockInArgs a) {
-#pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) T xn[kLayerRows * lds_ld<T, C>()];
-  const int lane = threadIdx.x & 63;
-  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t row0 = (int64_t)blockIdx.x * kLayerRows;
-  layer_mixture<T, C>(a.src, a.ld, a.nsrc, nullptr, a.w_mix, row0, a.M, xn);
-  __syncthreads();
-  const int c = lane & 15, g = lane >> 4;
-  const bool store = row0 + c < a.M;
-  T* orow = static_cast<T*>(a.out) + (row0 + c) * a.out_ld + 4 * g;
-  for (int t = wv; t < a.N / 16; t += 4) {
-    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w), a.w_ld, t, xn, lane);
-    float o[4] = {acc[0], acc[1], acc[2], acc[3]};
-    if (store) store_vec<T, 4>(orow + 16 * t, o);
-  }
 }
 
 template <typename T, int C>
@@ -420,6 +448,14 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = lane & 15, g = lane >> 4;
   const int64_t row0 = (int64_t)blockIdx.x * kLayerRows;
+  const T* w_proj = static_cast<const T*>(a.w_proj);
+  const T* w_up = static_cast<const T*>(a.w_up);
+  const T* w_down = static_cast<const T*>(a.w_down);
+  // the wave's first c_proj and FFN-up weight fragments go out before the
+  // gate's loads
+  TileW<T, C> wp, wu;
+  load_tile_w<T, C>(wp, w_proj, a.wp_ld, wv, lane);  // C / 16 >= 4 tiles: every wave has one
+  load_tile_w<T, C>(wu, w_up, a.wu_ld, wv, lane);
   // 1) gate (gate_kernel's arithmetic): 16 lanes per row
   {
     const int r = threadIdx.x / 16, c0 = (threadIdx.x % 16) * CH;
@@ -435,7 +471,10 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   // 2) c_proj, then the partial sum
   const int64_t crow = min(row0 + c, a.M - 1);
   for (int t = wv; t < C / 16; t += 4) {
-    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w_proj), a.wp_ld, t, ga, lane);
+    TileW<T, C> next;
+    if (t + 4 < C / 16) load_tile_w<T, C>(next, w_proj, a.wp_ld, t + 4, lane);
+    const f32x4_t acc = layer_tile<T, C>(wp, ga, lane);
+    wp = next;
     const int f = 16 * t + 4 * g;
     float p[4];
     if (a.pin != nullptr) {
@@ -455,9 +494,15 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   layer_mixture<T, C>(a.blk, a.blk_ld, a.nblk, pm, a.w_mix, row0, a.M, ga);
   __syncthreads();
   // 4) FFN up + SwiGLU (swiglu_kernel's arithmetic on the interleaved
-  //    (gate, linear) pairs: features 2j, 2j + 1 -> hidden j)
+  //    (gate, linear) pairs: features 2j, 2j + 1 -> hidden j); the first
+  //    FFN-down fragment goes out with the last up tile
+  TileW<T, 2 * C> wd;
   for (int t = wv; t < 4 * C / 16; t += 4) {
-    const f32x4_t acc = layer_tile<T, C>(static_cast<const T*>(a.w_up), a.wu_ld, t, ga, lane);
+    TileW<T, C> next;
+    if (t + 4 < 4 * C / 16) load_tile_w<T, C>(next, w_up, a.wu_ld, t + 4, lane);
+    else load_tile_w<T, 2 * C>(wd, w_down, a.wd_ld, wv, lane);
+    const f32x4_t acc = layer_tile<T, C>(wu, ga, lane);
+    wu = next;
     float hv[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -473,7 +518,10 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   const bool store = row0 + c < a.M;
   T* orow = static_cast<T*>(a.out) + (row0 + c) * a.out_ld;
   for (int t = wv; t < C / 16; t += 4) {
-    const f32x4_t acc = layer_tile<T, 2 * C>(static_cast<const T*>(a.w_down), a.wd_ld, t, hh, lane);
+    TileW<T, 2 * C> next;
+    if (t + 4 < C / 16) load_tile_w<T, 2 * C>(next, w_down, a.wd_ld, t + 4, lane);
+    const f32x4_t acc = layer_tile<T, 2 * C>(wd, hh, lane);
+    wd = next;
     const int f = 16 * t + 4 * g;
     float pmv[4], o[4];
     load_vec<T, 4>(pm + c * LDC + f, pmv);
@@ -733,43 +781,6 @@ bool rows16(const void* p, int64_t ld, int64_t es) {
   return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && (ld * es) % 16 == 0;
 }
 }  // namespace
-
-extern "C" int dg_block_in(int64_t M, int C, int N, int dtype, int nsrc, const void* const* src,
-                           const int64_t* src_ld, const void* w_mix, const void* w, int64_t w_ld, void* out,
-                           int64_t out_ld, void* stream) {
-  DG_REQUIRE(M >= 0 && C >= 1 && N >= 1, DG_EINVAL, "block_in: bad sizes M=%lld C=%d N=%d", (long long)M, C, N);
-  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "block_in: dtype %d unsupported", dtype);
-  DG_REQUIRE(C == 64 || C == 128, DG_EUNSUPPORTED, "block_in: n_embd %d unsupported (64 or 128)", C);
-  DG_REQUIRE(N % 16 == 0, DG_EUNSUPPORTED, "block_in: %d outputs per row unsupported (a multiple of 16)", N);
-  DG_REQUIRE(nsrc >= 1 && nsrc <= kMaxResSources, DG_EINVAL, "block_in: %d sources (1..%d)", nsrc, kMaxResSources);
-  if (M == 0) return DG_OK;
-  DG_REQUIRE(src && src_ld && w_mix && w && out, DG_EINVAL, "block_in: NULL pointer");
-  DG_REQUIRE(M <= (int64_t)kLayerRows * 0x7fffffffLL, DG_EINVAL, "block_in: too many rows (%lld)", (long long)M);
-  const int64_t es = dtype == DG_F32 ? 4 : 2;
-  BlockInArgs a{};
-  bool ok = rows16(w_mix, 0, es) && rows16(w, w_ld, es) && rows16(out, out_ld, es) && w_ld >= C && out_ld >= N;
-  for (int n = 0; n < nsrc; ++n) {
-    DG_REQUIRE(src[n] != nullptr && src_ld[n] >= C, DG_EINVAL, "block_in: source %d is NULL or narrower than C", n);
-    ok = ok && rows16(src[n], src_ld[n], es);
-    a.src[n] = src[n];
-    a.ld[n] = src_ld[n];
-  }
-  DG_REQUIRE(ok, DG_EUNSUPPORTED, "block_in: rows must be 16-byte aligned");
-  a.w_mix = w_mix; a.w = w; a.out = out;
-  a.w_ld = w_ld; a.out_ld = out_ld; a.M = M; a.nsrc = nsrc; a.N = N;
-  const dim3 grid((unsigned)((M + kLayerRows - 1) / kLayerRows));
-  hipStream_t s = static_cast<hipStream_t>(stream);
-#define DG_BLOCK_IN(T)                                                                              \
-  do {                                                                                            \
-    if (C == 64) hipLaunchKernelGGL((block_in_kernel<T, 64>), grid, dim3(256), 0, s, a);          \
-    else hipLaunchKernelGGL((block_in_kernel<T, 128>), grid, dim3(256), 0, s, a);                 \
-  } while (0)
-  if (dtype == DG_F32) DG_BLOCK_IN(float);
-  else if (dtype == DG_BF16) DG_BLOCK_IN(bf16_t);
-  else DG_BLOCK_IN(f16_t);
-#undef DG_BLOCK_IN
-  return check_launch("block_in_kernel");
-}
 
 extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
                             const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,

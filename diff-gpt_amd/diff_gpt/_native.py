@@ -175,12 +175,6 @@ _SIGNATURES = {
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
          ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
     ),
-    "dg_block_in": (
-        ctypes.c_int,
-        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
-         ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-         ctypes.c_int64, ctypes.c_void_p],
-    ),
     "dg_block_out": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
@@ -636,27 +630,6 @@ def _row_list(tensors: list[torch.Tensor], what: str):
     ptrs = (ctypes.c_void_p * max(1, len(rows)))(*[t.data_ptr() for t in rows])
     lds = (ctypes.c_int64 * max(1, len(rows)))(*[t.stride(0) for t in rows])
     return rows, ptrs, lds
-
-
-def block_in_(sources: list[torch.Tensor], w_mix: torch.Tensor, w: torch.Tensor, out: torch.Tensor) -> bool:
-    """dg_block_in: out (..., N) = rms_norm(block_attn_res(sources[:-1],
-    sources[-1], w_mix)) @ w^T for w (N, C).  Returns False, having done
-    nothing, for shapes the fused kernel does not take (n_embd other than 64
-    or 128, unaligned rows); raises on any other error."""
-    C = w.size(1)
-    rows, ptrs, lds = _row_list(sources, "block_in")
-    for t in rows:
-        if t.shape != rows[0].shape or t.dtype != out.dtype or t.size(1) != C:
-            raise ValueError("block_in: sources must share shape and dtype with the output")
-    o2, w1 = out.view(-1, out.size(-1)), w_mix.reshape(-1).contiguous()
-    if w.stride(1) != 1 or o2.stride(1) != 1 or w.dtype != out.dtype:
-        return False
-    rc = lib().dg_block_in(o2.size(0), C, w.size(0), _dtype_code(o2), len(rows), ptrs, lds, _ptr(w1), _ptr(w),
-                           w.stride(0), _ptr(o2), o2.stride(0), _stream(o2))
-    if rc == DG_EUNSUPPORTED:
-        return False
-    _check(rc, "block_in")
-    return True
 
 
 def block_out_(y: torch.Tensor, g: torch.Tensor, w_proj: torch.Tensor, partial_in: torch.Tensor | None,

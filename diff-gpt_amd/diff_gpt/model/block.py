@@ -6,10 +6,9 @@ pseudo-query; a block boundary every ``layers_per_block`` layers commits the
 partial sum.  In Block.forward the mixture and the RMSNorm after it are one
 dg_attn_res_norm launch, the clamped SwiGLU of the MLP one dg_swiglu launch,
 and the attention sub-layer is the HIP path of MultiHeadAttention.  At
-n_embd 64 or 128 the whole layer is three launches instead: dg_block_in (the
-attention's mixture, its norm and the q/k/v/g projection), the attention, and
-dg_block_out (gate, c_proj, the partial sum, the MLP's mixture and norm, the
-FFN and the residual).
+n_embd 64 or 128 everything after the attention -- gate, c_proj, the partial
+sum, the MLP's mixture and norm, the FFN and the residual -- is one
+dg_block_out launch instead of six.
 ``block_attn_res`` keeps the reference's torch formulation for direct callers.
 """
 
@@ -92,15 +91,27 @@ class Block(nn.Module):
         kv_cache: KVCache | None,
     ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
         _native.require_device("Block", partial_block)
-        fused = self._forward_fused(blocks, partial_block, freqs_cis, kv_cache)
-        if fused is not None:
-            return fused
         xn = attn_res_norm(blocks, partial_block, self.attn_res_proj)
         committed = self._at_boundary()
+        partial_in = partial_block
         if committed:
             blocks = (*blocks, partial_block)
-        attn_out = self.sa(xn, freqs_cis=freqs_cis, kv_cache=kv_cache)
-        partial_block = attn_out if committed else partial_block + attn_out
+        sa = self.sa
+        qkvg = F.linear(xn, sa._projection_weight())
+        y = sa._attend(qkvg, freqs_cis, kv_cache)
+        g = sa._gate_logits(qkvg)
+        up, swiglu, down = self.ffwd.net
+        if len(blocks) + 1 <= ATTN_RES_MAX_SOURCES:
+            # gate, c_proj, the partial sum, the MLP's mixture and norm, the FFN
+            # and the residual in one launch (n_embd 64 or 128)
+            out = torch.empty_like(partial_in)
+            if _native.block_out_(y, g, sa.c_proj.weight, None if committed else partial_in, list(blocks),
+                                  self.mlp_res_proj.weight, up.weight, down.weight, swiglu.alpha, swiglu.limit,
+                                  out):
+                return blocks, out
+        _native.ops().gate_(y, g)  # y * sigmoid(g), mha.py:84
+        attn_out = sa.c_proj(y)
+        partial_block = attn_out if committed else partial_in + attn_out
         return blocks, self._mlp(blocks, partial_block)
 
     def _mlp(self, blocks: tuple[torch.Tensor, ...], partial_block: torch.Tensor) -> torch.Tensor:
@@ -108,37 +119,3 @@ class Block(nn.Module):
         up, swiglu, down = self.ffwd.net
         hidden = _native.ops().swiglu(F.linear(xn, up.weight), swiglu.alpha, swiglu.limit)
         return partial_block + F.linear(hidden, down.weight)
-
-    def _forward_fused(self, blocks, partial_block, freqs_cis, kv_cache):
-        """The layer in three launches where the kernels take it (n_embd 64 or
-        128, 16-byte aligned rows): dg_block_in (the attention's mixture and
-        norm, and the q/k/v/g projection), the attention itself
-        (MultiHeadAttention._attend), and dg_block_out (gate, c_proj, the
-        partial sum, the MLP's mixture and norm, the FFN and the residual).
-        Returns None, having launched nothing, when the first kernel does not
-        take the shape."""
-        if len(blocks) + 1 > ATTN_RES_MAX_SOURCES:
-            return None
-        sa = self.sa
-        w = sa._projection_weight()
-        sources = [partial_block] if len(blocks) == 1 and partial_block is blocks[0] else [*blocks, partial_block]
-        qkvg = torch.empty((*partial_block.shape[:-1], w.size(0)), dtype=partial_block.dtype,
-                           device=partial_block.device)
-        if not _native.block_in_(sources, self.attn_res_proj.weight, w, qkvg):
-            return None
-        partial_in = partial_block
-        committed = self._at_boundary()
-        if committed:
-            blocks = (*blocks, partial_block)
-        y = sa._attend(qkvg, freqs_cis, kv_cache)
-        g = sa._gate_logits(qkvg)
-        up, swiglu, down = self.ffwd.net
-        out = torch.empty_like(partial_block)
-        if _native.block_out_(y, g, sa.c_proj.weight, None if committed else partial_in, list(blocks),
-                              self.mlp_res_proj.weight, up.weight, down.weight, swiglu.alpha, swiglu.limit, out):
-            return blocks, out
-        # the second kernel does not take the layout: the separate launches
-        _native.ops().gate_(y, g)
-        attn_out = sa.c_proj(y)
-        partial_block = attn_out if committed else partial_in + attn_out
-        return blocks, self._mlp(blocks, partial_block)

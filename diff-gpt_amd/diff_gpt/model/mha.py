@@ -24,9 +24,9 @@ dg_decode_step call instead: the same RoPE, QK-norm and append, and the
 attention over the cache including the new token, in one launch where the
 rows share a broadcast prefix (two launches otherwise).
 
-Block.forward may run the projection itself (dg_block_in, fused with the
-mixture before it) and the gate and c_proj too (dg_block_out, fused with the
-MLP after them); it then calls _attend, the part between, directly.
+Block.forward runs the projection itself and may run the gate and c_proj
+too (dg_block_out, fused with the MLP after them); it then calls _attend, the
+part between, directly.
 """
 
 import math

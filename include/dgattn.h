@@ -392,24 +392,6 @@ DG_API int dg_lm_head(int64_t M, int C, int V, int dtype, const void* x, int64_t
                       int64_t w_ld, float cap, void* logits, int64_t logits_ld, int64_t* ids, void* stream);
 
 /*
- * A layer's work before its attention in one launch: block.py:94 (the
- * sub-layer's Block-AttnRes mixture and RMSNorm, dg_attn_res_norm) then
- * mha.py:39-42 (the q, k, v and gate projections as one product against their
- * concatenated weights).  out (M, N) = rms_norm(block_attn_res(src[0 ..
- * nsrc-2], src[nsrc-1], w_mix)) @ w^T for w (N, C); a single source is
- * block.py's short cut (its RMSNorm).  Intermediates are rounded where the
- * torch sequence rounds them (the mixture as dg_attn_res_norm, the product's
- * fp32 sum once); the product runs on the matrix cores, so the result agrees
- * with dg_attn_res_norm + F.linear within the north-star bars, not bit for
- * bit.  Supported: C = 64 or 128, N a multiple of 16, at most 32 sources,
- * 16-byte aligned rows; anything else returns DG_EUNSUPPORTED and does
- * nothing.
- */
-DG_API int dg_block_in(int64_t M, int C, int N, int dtype, int nsrc, const void* const* src,
-                       const int64_t* src_ld, const void* w_mix, const void* w, int64_t w_ld, void* out,
-                       int64_t out_ld, void* stream);
-
-/*
  * A layer's work after its attention in one launch: mha.py:84-85 (the gate
  * y * sigmoid(g) and c_proj), block.py:98-106 (the partial sum: the
  * attention output itself when the layer commits its input block, else
@@ -419,8 +401,13 @@ DG_API int dg_block_in(int64_t M, int C, int N, int dtype, int nsrc, const void*
  * the interleaved pairs, 2C -> C).  y, g (M, C): the attention output and
  * the gate logits; w_proj (C, C), w_up (4C, C), w_down (C, 2C); partial_in
  * NULL when the layer commits; blocks[0 .. nblk-1] the committed blocks; out
- * (M, C) the partial sum leaving the layer.  Rounding and supported shapes
- * as dg_block_in (C = 64 or 128, nblk + 1 <= 32).
+ * (M, C) the partial sum leaving the layer.  Intermediates are rounded where
+ * the torch sequence rounds them (the gate as dg_gate, each product's fp32
+ * sum once, the mixture as dg_attn_res_norm, the SwiGLU as dg_swiglu, the
+ * residual adds); the products run on the matrix cores, so the result agrees
+ * with the separate launches within the north-star bars, not bit for bit.
+ * Supported: C = 64 or 128, nblk + 1 <= 32, 16-byte aligned rows; anything
+ * else returns DG_EUNSUPPORTED and does nothing.
  */
 DG_API int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
                         const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,

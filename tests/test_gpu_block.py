@@ -322,9 +322,7 @@ def _layer_case(M, C, nblk, dtype, seed):
     qkvg = _randn((M, 4 * C), seed + 52, dtype, 2.0)
     w = {
         "proj": _randn((C, C), seed + 53, dtype, C ** -0.5),
-        "mix_attn": _randn((1, C), seed + 54, dtype, 0.5),
         "mix_mlp": _randn((1, C), seed + 55, dtype, 0.5),
-        "qkvg": _randn((4 * C, C), seed + 56, dtype, C ** -0.5),
         "up": _randn((4 * C, C), seed + 57, dtype, 3.0 * C ** -0.5),
         "down": _randn((C, 2 * C), seed + 58, dtype, (2 * C) ** -0.5),
     }
@@ -394,51 +392,30 @@ class _Proj:
         self.weight = w
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", LAYER, ids=lambda s: "x".join(map(str, s)))
-def test_block_in_matches_reference(dev, dtype, shape):
-    """dg_block_in (the mixture, its norm, the q/k/v/g projection) against
-    the oracle in float64; with one source it is block.py's short cut (the
-    source's RMSNorm)."""
-    from diff_gpt import _native
-
-    M, C, nblk, _ = shape
-    blocks, pin, _, _, w = _layer_case(M, C, nblk, dtype, 400 + C + nblk)
-    d = lambda t: t.to(dev)  # noqa: E731
-    for sources in (blocks + [pin], [pin]):
-        out = torch.empty((M, 4 * C), dtype=TDT[dtype], device=dev)
-        assert _native.block_in_([d(s) for s in sources], d(w["mix_attn"]), d(w["qkvg"]), out)
-        src64 = [s.double() for s in sources]
-        h = src64[0] if len(src64) == 1 else tr.attn_res(tuple(src64[:-1]), src64[-1], w["mix_attn"].double())
-        ref = tr.rms(h) @ w["qkvg"].double().T
-        assert _rel(out, ref) <= TOL[dtype], len(sources)
-
-
 @pytest.mark.parametrize("C", [32, 96, 256])
-def test_block_kernels_decline_other_widths(dev, C):
-    """n_embd other than 64 or 128: both entry points return False and write
+def test_block_out_declines_other_widths(dev, C):
+    """n_embd other than 64 or 128: dg_block_out returns False and writes
     nothing (the model then makes the separate launches)."""
     from diff_gpt import _native
 
     M = 20
     blocks, pin, y, qkvg, w = _layer_case(M, C, 2, "f32", 7)
     d = lambda t: t.to(dev)  # noqa: E731
-    out = torch.full((M, 4 * C), 5.0, device=dev)
-    assert not _native.block_in_([d(pin)], d(w["mix_attn"]), d(w["qkvg"]), out)
-    out2 = torch.full((M, C), 5.0, device=dev)
+    out = torch.full((M, C), 5.0, device=dev)
     assert not _native.block_out_(d(y), d(qkvg)[:, 3 * C:], d(w["proj"]), None, [d(b) for b in blocks],
-                                  d(w["mix_mlp"]), d(w["up"]), d(w["down"]), ALPHA, LIMIT, out2)
+                                  d(w["mix_mlp"]), d(w["up"]), d(w["down"]), ALPHA, LIMIT, out)
     torch.cuda.synchronize()
-    assert bool((out == 5.0).all()) and bool((out2 == 5.0).all())
+    assert bool((out == 5.0).all())
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("layers_per_block", [1, 2])
-def test_gpt_layers_in_three_launches_match_separate_launches(dev, dtype, layers_per_block, monkeypatch):
-    """GPT.forward at n_embd 64 runs each layer as dg_block_in, the attention
-    and dg_block_out; with both declined it makes the separate launches.  The
-    logits of a prefill and a decode step agree within the dtype's bar, and
-    the fp32 ones with the oracle forward within 1e-5."""
+def test_gpt_layers_with_fused_block_out_match_separate_launches(dev, dtype, layers_per_block, monkeypatch):
+    """GPT.forward at n_embd 64 ends each layer with one dg_block_out launch;
+    with it declined it makes the separate launches.  The logits of a prefill
+    and a decode step agree within the dtype's bar, and the fp32 ones with the
+    oracle forward within 1e-5 (layers_per_block 2: half the layers add their
+    attention output to the partial sum they were given)."""
     from diff_gpt import _native
     from diff_gpt.model.gpt import GPT
     from diff_gpt.model.kv_cache import KVCache
@@ -451,14 +428,12 @@ def test_gpt_layers_in_three_launches_match_separate_launches(dev, dtype, layers
                          attn_res_layers_per_block=layers_per_block)
     model = model.to(dev).to(TDT[dtype])
     idx = torch.randint(0, 256, (3, 20), generator=torch.Generator().manual_seed(2))
-    calls = {"in": 0, "out": 0}
-    real_in, real_out = _native.block_in_, _native.block_out_
+    calls = [0]
+    real_out = _native.block_out_
 
-    def count(name, fn):
-        def wrapped(*a, **k):
-            calls[name] += 1
-            return fn(*a, **k)
-        return wrapped
+    def counted(*a, **k):
+        calls[0] += 1
+        return real_out(*a, **k)
 
     def run():
         kv = KVCache(batch_size=3, num_heads=4, seq_len=21, head_dim=16, num_layers=4)
@@ -467,11 +442,10 @@ def test_gpt_layers_in_three_launches_match_separate_launches(dev, dtype, layers
             step = model(first.argmax(-1, keepdim=True), kv_cache=kv)[0][:, -1]
         return first.float().cpu(), step.float().cpu()
 
-    monkeypatch.setattr(_native, "block_in_", count("in", real_in))
-    monkeypatch.setattr(_native, "block_out_", count("out", real_out))
+    monkeypatch.setattr(_native, "block_out_", counted)
     fused = run()
-    assert calls == {"in": 8, "out": 8}  # 4 layers x (prefill, step)
-    monkeypatch.setattr(_native, "block_in_", lambda *a, **k: False)
+    assert calls[0] == 8  # 4 layers x (prefill, step)
+    monkeypatch.setattr(_native, "block_out_", lambda *a, **k: False)
     separate = run()
     for f_, s_ in zip(fused, separate):
         assert _rel(f_, s_.double()) <= TOL[dtype]

@@ -213,20 +213,19 @@ def test_decode_step_at_config_geometry(dev, shape):
 
 class _AttentionTap:
     """Records, for chosen layers, what the HIP path feeds the attention and
-    what it returns: the layer input x (a forward pre-hook on the attention
-    module), and the arguments and output of the prefill (dg_prefill_rope)
-    and decode-step (dg_decode_step) calls made while that layer runs."""
+    what it returns: the layer's q/k/v/g projections (the argument of the
+    attention module's _attend, which Block.forward calls on them), and the
+    arguments and output of the prefill (dg_prefill_rope) and decode-step
+    (dg_decode_step) calls made while that layer attends."""
 
     def __init__(self, model, layers, monkeypatch):
         from diff_gpt import _native
 
         self.records = {l: [] for l in layers}
         self._cur = None
-        self._hooks = []
         for l in layers:
             sa = model.blocks[l].sa
-            self._hooks.append(sa.register_forward_pre_hook(self._pre(l)))
-            self._hooks.append(sa.register_forward_hook(self._post()))
+            monkeypatch.setattr(sa, "_attend", self._wrap(l, sa._attend))
         orig_prefill, orig_step = _native.prefill_rope_, _native.decode_step_
 
         def prefill(q, freqs, k, v, y, scale, qknorm, keys_normed=False):
@@ -245,32 +244,26 @@ class _AttentionTap:
         monkeypatch.setattr(_native, "prefill_rope_", prefill)
         monkeypatch.setattr(_native, "decode_step_", step)
 
-    def _pre(self, layer):
-        def hook(module, args):
-            self._cur = {"x": args[0].detach().clone()}
+    def _wrap(self, layer, attend):
+        def wrapped(qkvg, freqs_cis, kv_cache):
+            self._cur = {"qkvg": qkvg.detach().clone()}
             self.records[layer].append(self._cur)
-        return hook
-
-    def _post(self):
-        def hook(module, args, out):
-            self._cur = None
-        return hook
+            try:
+                return attend(qkvg, freqs_cis, kv_cache)
+            finally:
+                self._cur = None
+        return wrapped
 
     def close(self):
-        for h in self._hooks:
-            h.remove()
+        pass
 
 
-def _projections(model, layer, x):
-    """q, k, v (B,T,H,D) of the layer's input, from the same fused GEMM the
-    model runs."""
-    import torch.nn.functional as F
-
+def _projections(model, layer, qkvg):
+    """q, k, v (B,T,H,D): the column slices of the layer's projections."""
     sa = model.blocks[layer].sa
     H, D = sa.n_head, sa.head_dim
     inner = H * D
-    B, T, _ = x.shape
-    qkvg = F.linear(x, sa._projection_weight())
+    B, T, _ = qkvg.shape
     return tuple(qkvg[..., i * inner:(i + 1) * inner].reshape(B, T, H, D) for i in range(3))
 
 
@@ -282,7 +275,7 @@ def _check_layer_attention(model, layer, recs, D, what):
     pre, step = recs[0], recs[1]
     assert pre["kind"] == "prefill" and pre["fused"] and pre["keys_normed"], what
     assert step["kind"] == "step", what
-    q, k, v = _projections(model, layer, pre["x"])
+    q, k, v = _projections(model, layer, pre["qkvg"])
     assert torch.equal(q, pre["q"]), what  # the projections the kernel was fed
     B, T, H, _ = q.shape
     cs = pre["freqs"].float().cpu().numpy().reshape(T, D // 2, 2)
@@ -299,7 +292,7 @@ def _check_layer_attention(model, layer, recs, D, what):
             worst = max(worst, err)
             assert err <= 2e-2, (what, "prefill", b, h, err)
     # decode step at position T: keys 0 .. T-1 from the prefill, key T new
-    qs, ks, vs = _projections(model, layer, step["x"])
+    qs, ks, vs = _projections(model, layer, step["qkvg"])
     assert torch.equal(qs, step["q"]) and torch.equal(ks, step["k"]), what
     cs1 = step["freqs"].float().cpu().numpy().reshape(1, D // 2, 2)
     sq = on.rope_qknorm(qs.float().cpu().numpy(), cs1[None, :, None], "bf16")
