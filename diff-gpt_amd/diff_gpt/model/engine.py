@@ -266,13 +266,15 @@ class Engine:
             masks.append(mask)
         T, steps = len(prompts[0]), len(columns)
         # the token columns reach the host in one copy; the mask of a step that
-        # samples or forces every row is known on the host already
-        mask_np = np.empty((rows, steps), dtype=np.int64)
+        # samples or forces every row is known on the host already, and when
+        # every step is such a step all rows share one mask list
         on_device = [s for s, m in enumerate(masks) if isinstance(m, torch.Tensor)]
-        for s, m in enumerate(masks):
-            if not isinstance(m, torch.Tensor):
-                mask_np[:, s] = m
+        mask_np = None
         if on_device:
+            mask_np = np.empty((rows, steps), dtype=np.int64)
+            for s, m in enumerate(masks):
+                if not isinstance(m, torch.Tensor):
+                    mask_np[:, s] = m
             mask_np[:, on_device] = torch.stack([masks[s] for s in on_device], dim=1).cpu().numpy()
         gen_np = torch.stack(columns, dim=1).cpu().numpy() if columns else np.empty((rows, 0), dtype=np.int64)
         # about 2 * rows lists of Python ints are built here: with the garbage
@@ -282,10 +284,14 @@ class Engine:
         gc.disable()
         try:
             generated = gen_np.tolist()
-            mask_rows = mask_np.tolist()
             results = [prompts[r // num_samples] + generated[r] for r in range(rows)]
-            zeros = [0] * T
-            out_masks = [zeros + mask_rows[r] for r in range(rows)]
+            if mask_np is None:
+                shared = [0] * T + [int(m) for m in masks]
+                out_masks = [shared.copy() for _ in range(rows)]
+            else:
+                mask_rows = mask_np.tolist()
+                zeros = [0] * T
+                out_masks = [zeros + mask_rows[r] for r in range(rows)]
         finally:
             if gc_enabled:
                 gc.enable()
