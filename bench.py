@@ -53,6 +53,7 @@ for p in (REPO / "diff-gpt_amd", REPO):
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
 METRIC = "decode attn tokens/s + % HBM roofline; prefill attn TFLOP/s, 1×MI355X"
 
 # configs[1] geometry
@@ -362,7 +363,9 @@ def shapes_leg(reps: int = 20):
     prefill T=3584).  The cache is (2, B, H, capacity, D), the layout the
     model's KV cache uses.  Each case is `reps` launches captured in one graph,
     timed with events over 5 replays (median); decode bytes per launch =
-    B*H*es*(2*L_kv*D + 2*D), prefill FLOP = 2*B*H*D*T*(T+1).  The D = 16 fp32
+    B*H*es*(2*L_kv*D + 2*D), prefill FLOP = 2*B*H*D*T*(T+1).  The same two
+    prefills in fp32 (an fp32 model of that geometry) run on the fp32 matrix
+    cores and are priced against their 157.3 TFLOP/s peak.  The D = 16 fp32
     prefills of configs[0] (B=32) and configs[1] (one series, B=1), T=96,
     H=4, are launch-bound and report latency only."""
     import torch
@@ -431,6 +434,21 @@ def shapes_leg(reps: int = 20):
                     "general_kernel_tflops": flop / t_gen / 1e12})
         log(f"shapes: {out[-1]}")
         del q, k, v, y, k_rot
+    # an fp32 model of the same geometry: dg_attention on rotated q and k runs
+    # the fp32 MFMA kernel (v_mfma_f32_32x32x2_f32, dense fp32 matrix peak
+    # 157.3 TFLOP/s)
+    for name, B, H, D, T in (("configs[3]", 512, 8, 64, 1024), ("configs[4]", 64, 8, 128, 3584)):
+        q, k, v = (torch.randn((B, T, H, D), generator=g, device=dev) for _ in range(3))
+        y = torch.empty_like(q)
+        flop = 2.0 * B * H * D * T * (T + 1)
+        t = timed(lambda: _native.attention_(q, k, v, y, D ** -0.5))
+        tf = flop / t / 1e12
+        out.append({"workload": f"{name} geometry causal prefill attention B={B} H={H} T={T} D={D} fp32 "
+                                "(an fp32 model's prefill kernel, on the matrix cores)",
+                    "ms": t * 1e3, "tflops": tf, "frac": tf / FP32_MFMA_PEAK_TFLOPS,
+                    "peak_tflops": FP32_MFMA_PEAK_TFLOPS})
+        log(f"shapes: {out[-1]}")
+        del q, k, v, y
     # configs[0] and configs[1] prefill (D = 16, fp32): launch-bound, so the
     # figure is latency per launch, with no roofline
     for name, B in (("configs[0]", 32), ("configs[1] per series", 1)):

@@ -25,9 +25,9 @@ REPO = PKG.parent
 BUILD = HERE / "_build"
 LIB = PKG / "lib" / "libdgattn.so"
 TIMELINE_LIB = PKG / "lib" / "libdgattn_timeline.so"
-SOURCES = ["dg_abi.hip", "dg_rope.hip", "dg_attn_vec.hip", "dg_attn_mfma.hip", "dg_attn_shared.hip",
-           "dg_block.hip", "dg_noalloc.hip"]
-HEADERS = ["dg_common.h", "dg_rope_math.h", str(REPO / "include" / "dgattn.h")]
+SOURCES = ["dg_abi.hip", "dg_rope.hip", "dg_attn_vec.hip", "dg_attn_mfma.hip", "dg_attn_mfma_f32.hip",
+           "dg_attn_shared.hip", "dg_block.hip", "dg_noalloc.hip"]
+HEADERS = ["dg_common.h", "dg_rope_math.h", "dg_prefill.h", str(REPO / "include" / "dgattn.h")]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

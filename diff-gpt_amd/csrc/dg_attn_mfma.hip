@@ -49,6 +49,7 @@
 // (b, h) run on the same XCD (blockIdx round-robins over the 8 XCDs), keeping
 // that head's K/V resident in one L2, and the longest (last) query blocks of a
 // head start first.
+#include "dg_prefill.h"
 #include "dg_rope_math.h"
 
 namespace dg {
@@ -57,31 +58,9 @@ typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
 typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
 typedef _Float16 __attribute__((ext_vector_type(2))) f16x2_t;
-typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16_t;
 // plain clang vector (not HIP's uint4 wrapper class) so staging arrays stay in registers
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
-struct PrefillArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  void* y;
-  int64_t qb, qt, qh;
-  int64_t kb, kt, kh;
-  int64_t vb, vt, vh;
-  int64_t yb, yt, yh;
-  int H, Tq, Tk, q_offset;
-  int nqb;     // query blocks per (b, h)
-  int nbh;     // B*H
-  int win;     // (b, h) pairs per scheduling window
-  float scale_log2;  // SDPA scale * log2(e)
-  float lazy_raw;    // kLazyLog2 / scale_log2: allowed growth of a row max in raw score units
-  // ROPE instances: (cos, sin) pairs of query row (b, i, h) at
-  // freqs + b*fb + i*ft + h*fh (D/2 pairs, contiguous), and the QK-norm flag
-  const void* freqs;
-  int64_t fb, ft, fh;
-  int qknorm;
-};
 
 template <typename T>
 struct MfmaOps;
@@ -130,8 +109,6 @@ template <int D>
 constexpr int prefill_bn() {
   return D == 64 ? 64 : 32;
 }
-constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
-constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 // Schedule of the bounded form's 32-key blocks, per head_dim (measured at
 // configs[2] / [4]: D = 64 gains 3-4 % from the prefetch, while the
 // prefetched V^T fragments do not fit D = 128's register budget and halve
@@ -147,21 +124,6 @@ constexpr bool prefill_pipe() {
 template <int D>
 constexpr bool prefill_prefetch() {
   return D == 64;
-}
-
-// max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
-// value in both operands leaves every lane holding its own value in one
-// result and lane l^32's in the other (which one depends on the half), so a
-// commutative op over the pair gives both halves the same bits.
-__device__ __forceinline__ float half_pair_max(float x) {
-  const uint32_t u = __float_as_uint(x);
-  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float half_pair_sum(float x) {
-  const uint32_t u = __float_as_uint(x);
-  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 template <typename T, int D, int QW>
@@ -190,14 +152,6 @@ template <int D>
 __device__ __forceinline__ int piece_swz(int r) {
   if constexpr (D == 64) return ((r & 2) << 1) | ((r >> 2) & 3);
   else return ((r & 3) << 2) | ((r >> 2) & 3);
-}
-
-// Global -> LDS copy through a buffer resource: 16 bytes per lane from byte
-// offset voff + soff of the resource (zeros past its range) into lds + 16*l
-// (buffer_load_dwordx4 ... lds).  The address-space cast stays inside this
-// device function.
-__device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, void* lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
 }
 
 // Resident workgroups per CU the register allocation must allow: D = 64 fits
@@ -759,7 +713,11 @@ void prefill_mfma_kernel(const PrefillArgs a) {
 namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-bool strides8(const dg_stride3* s) { return s->b % 8 == 0 && s->t % 8 == 0 && s->h % 8 == 0; }
+// every (b, t, h) row start 16-byte aligned
+bool strides16b(const dg_stride3* s, int64_t es) {
+  const int64_t n = 16 / es;
+  return s->b % n == 0 && s->t % n == 0 && s->h % n == 0;
+}
 
 // query blocks of 32 per wave (64 per wave spills at D = 64, and halves the
 // resident workgroups at D = 128)
@@ -787,20 +745,21 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
                              const dg_stride3* q_st, const void* k, const dg_stride3* k_st,
                              const void* v, const dg_stride3* v_st, const void* y,
                              const dg_stride3* y_st, float scale) {
-  (void)Tk;
   if (!(scale > 0.f)) return false;  // the tile max of raw scores needs a positive scale
-  if (dtype != DG_BF16 && dtype != DG_F16) return false;
+  // bf16 / fp16 here, fp32 in dg_attn_mfma_f32.hip
+  if (dtype != DG_BF16 && dtype != DG_F16 && dtype != DG_F32) return false;
   if (D != 64 && D != 128) return false;
   if (Tq < 16) return false;  // decode and tiny chunks: vector kernel
   // grid (window, query blocks, windows): at most 65535 query blocks of 128
   // and 65535 windows of kPrefillWindow pairs
   const int64_t nbh = (int64_t)B * H;
   if (nbh <= 0 || (Tq + 127) / 128 > 65535 || (nbh + kPrefillWindow - 1) / kPrefillWindow > 65535) return false;
-  // per-head byte offsets (buffer ranges) are 32-bit signed inside the kernel
+  // per-head byte offsets (buffer ranges) are 32-bit signed inside the kernels
+  const int64_t es = dtype == DG_F32 ? 4 : 2;
   const int64_t span = (int64_t)Tk * (k_st->t > v_st->t ? k_st->t : v_st->t);
-  if (span >= (int64_t)1 << 30 || k_st->t < 0 || v_st->t < 0) return false;
-  return aligned16(q) && aligned16(k) && aligned16(v) && aligned16(y) && strides8(q_st) &&
-         strides8(k_st) && strides8(v_st) && strides8(y_st);
+  if (span * es >= (int64_t)1 << 31 || k_st->t < 0 || v_st->t < 0) return false;
+  return aligned16(q) && aligned16(k) && aligned16(v) && aligned16(y) && strides16b(q_st, es) &&
+         strides16b(k_st, es) && strides16b(v_st, es) && strides16b(y_st, es);
 }
 
 namespace {
@@ -830,6 +789,7 @@ int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                  hipStream_t s) {
   const PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
+  if (dtype == DG_F32) return launch_prefill_f32(a, D, s);
   if (dtype == DG_BF16) return D == 64 ? launch_prefill<bf16_t, 64>(a, s) : launch_prefill<bf16_t, 128>(a, s);
   return D == 64 ? launch_prefill<f16_t, 64>(a, s) : launch_prefill<f16_t, 128>(a, s);
 }
@@ -841,6 +801,7 @@ bool mfma_prefill_rope_applicable(int B, int H, int Tq, int Tk, int D, int dtype
                                   int fdtype, const void* k, const dg_stride3* k_st, const void* v,
                                   const dg_stride3* v_st, const void* y, const dg_stride3* y_st,
                                   float scale) {
+  if (dtype != DG_BF16 && dtype != DG_F16) return false;  // no fp32 form
   if (!mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale)) return false;
   if (fdtype != dtype && fdtype != DG_F32) return false;
   const int64_t fes = fdtype == DG_F32 ? 4 : 2;

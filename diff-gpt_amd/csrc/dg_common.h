@@ -379,6 +379,33 @@ __device__ __forceinline__ f32x4_t qk_mfma(const RowRegs<T, DQ>& kop, const RowR
 // 32-bit data format, no swizzle, no stride.
 constexpr int kBufferWord3 = 0x00020000;
 
+// Global -> LDS copy through a buffer resource: 16 bytes per lane from byte
+// offset voff + soff of the resource (zeros past its range) into lds + 16*l
+// (buffer_load_dwordx4 ... lds).  The address-space cast stays inside this
+// device function.
+__device__ __forceinline__ void lds_copy16_buf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, void* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
+// The 16 accumulators of a 32 x 32 MFMA block: lane l, register r holds row
+// 8*(r/4) + 4*(l/32) + r%4 of column l%32.
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float floatx16_t;
+
+// max / sum of x over lanes l and l^32.  v_permlane32_swap with the same
+// value in both operands leaves every lane holding its own value in one
+// result and lane l^32's in the other (which one depends on the half), so a
+// commutative op over the pair gives both halves the same bits.
+__device__ __forceinline__ float half_pair_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_pair_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ds_read_b64_tr_b16: within each 16 lanes, lane t receives element t & 3 of
 // the 8-byte chunks addressed by lanes t/4, 4 + t/4, 8 + t/4, 12 + t/4
 __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {

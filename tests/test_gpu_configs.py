@@ -101,6 +101,60 @@ def test_prefill_at_config_shape(dev, name, path):
         assert err <= 2e-2, (name, path, bh, err)
 
 
+F32_PREFILL = {  # name: (B, H, Tq, Tk, D): fp32 prefill on the matrix cores (v_mfma_f32_32x32x2_f32)
+    "cfg3_geometry": (64, 8, 1024, 1024, 64),    # 8 windows of 64 pairs
+    "cfg4_geometry": (8, 8, 3584, 3584, 128),
+    "ragged_d64": (26, 5, 512, 512, 64),         # windows of 64, 64 and 2 pairs
+    "ragged_d128": (65, 2, 300, 300, 128),
+    "chunked_d64": (3, 7, 200, 1100, 64),        # bottom-right mask, ragged tiles
+    "chunked_d128": (5, 3, 77, 333, 128),
+}
+
+
+@pytest.mark.parametrize("name", list(F32_PREFILL))
+def test_fp32_prefill_at_config_shape(dev, name):
+    """An fp32 model's prefill attention (mha.py:61-81) at head_dim 64 / 128:
+    rotated, normalised q and k through dg_rope_qknorm_append (keys into a
+    cache page, as the model stores them), then dg_attention, which runs the
+    fp32 MFMA kernel.  Keys bit-exact against the oracle; the output of the
+    checked pairs (first and last of the first, a middle and the last window),
+    every query row, within 1e-5 * max|ref| of float64 attention on the
+    oracle's rotated q and k."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, Tq, Tk, D = F32_PREFILL[name]
+    print(f"fp32 prefill {name}: B={B} H={H} Tq={Tq} Tk={Tk} D={D}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(1)
+    q = torch.randn((B, Tq, H, D), generator=g, device=dev)
+    k, v = (torch.randn((B, Tk, H, D), generator=g, device=dev) for _ in range(2))
+    table = precompute_freqs_cis(D, 2 * Tk, 10000)
+    cap = Tk + 3
+    cache = torch.empty((2, B, H, cap, D), device=dev)
+    keys, values = cache[0, :, :, :Tk].transpose(1, 2), cache[1, :, :, :Tk].transpose(1, 2)
+    ops = _native.ops()
+    ops.rope_qknorm_append(None, k, v, table[:Tk].view(1, Tk, 1, D // 2, 2).to(dev), None, keys, values, True)
+    q_rot = torch.empty_like(q)
+    fq = table[Tk - Tq:Tk].view(1, Tq, 1, D // 2, 2).to(dev)
+    ops.rope_qknorm_append(q, None, None, fq, q_rot, None, None, True)
+    y = ops.attention(q_rot, keys, values, 1.0 / D**0.5)
+    torch.cuda.synchronize()
+    cs_k, cs_q = table[:Tk].numpy(), table[Tk - Tq:Tk].numpy()
+    worst = 0.0
+    for bh in _checked_pairs(B * H):
+        b, h = divmod(bh, H)
+        exp_q = on.rope_qknorm(q[b, :, h].cpu().numpy(), cs_q, "f32")
+        exp_k = on.rope_qknorm(k[b, :, h].cpu().numpy(), cs_k, "f32")
+        got_k = cache[0, b, h, :Tk].cpu().numpy()
+        assert np.array_equal(got_k.view(np.uint32), exp_k.view(np.uint32)), (name, bh)
+        assert np.array_equal(q_rot[b, :, h].cpu().numpy().view(np.uint32), exp_q.view(np.uint32)), (name, bh)
+        ref = on.attention_head_f64(exp_q, exp_k, v[b, :, h].cpu().numpy())
+        err = np.abs(y[b, :, h].cpu().numpy() - ref).max() / np.abs(ref).max()
+        worst = max(worst, err)
+        assert err <= 1e-5, (name, bh, err)
+    print(f"fp32 prefill {name}: worst {worst:.3g} x max|ref| (bar 1e-5)", flush=True)
+
+
 # ------------------------------------------------------------------ models at configs[3] / [4] geometry
 
 
