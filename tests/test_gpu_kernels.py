@@ -194,6 +194,32 @@ def test_prefill_attention_parity(dev, dtype, shape):
     assert err <= TOL[dtype], err
 
 
+def _random_prefills(seed, n):
+    """Seeded (B, H, Tq, Tk, D) for the MFMA prefill kernels: D 64 or 128,
+    causal (Tq = Tk) or chunked (Tq < Tk), Tq >= 16, ragged query blocks and
+    key tiles."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = int(rng.choice([64, 128]))
+        B, H = int(rng.integers(1, 5)), int(rng.integers(1, 5))
+        Tk = int(rng.integers(16, 900))
+        Tq = Tk if rng.random() < 0.5 else int(rng.integers(16, Tk + 1))
+        out.append((B, H, Tq, Tk, D))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", _random_prefills(2024, 12), ids=lambda s: "x".join(map(str, s)))
+def test_prefill_attention_random_shapes(dev, dtype, shape):
+    """dg_attention at seeded random prefill shapes (the fp32 and the bf16 /
+    fp16 MFMA kernels), k and v as strided views of a cache page, against
+    float64 attention: fp32 within 1e-5, bf16 / fp16 within 2e-2."""
+    B, H, Tq, Tk, D = shape
+    err = _attention_case(dev, dtype, B, H, Tq, Tk, D, cache_layout=True, seed=Tq * 7 + Tk + D)
+    assert err <= TOL[dtype], err
+
+
 PREFILL_ROPE = [  # (B, H, Tq, Tk, D)
     (2, 3, 200, 200, 64),   # causal, ragged last query block
     (1, 2, 130, 330, 128),  # chunked (bottom-right mask), D = 128
