@@ -45,7 +45,9 @@ __device__ __forceinline__ float rt(float x) {
 }
 
 // RMSNorm of one row slice with rms_norm_kernel's arithmetic (squares summed
-// by tree_sum inside the lane, then the butterfly over the G lanes of the row)
+// by tree_sum inside the lane, then the butterfly over the G lanes of the row,
+// here in registers: group_sum_dpp pairs the lanes as group_sum does, so the
+// bits are the same)
 template <int CH, int G>
 __device__ __forceinline__ void row_rms(float (&x)[CH], int N) {
 #pragma clang fp contract(off)
@@ -53,7 +55,7 @@ __device__ __forceinline__ void row_rms(float (&x)[CH], int N) {
 #pragma unroll
   for (int i = 0; i < CH; ++i) sq[i] = x[i] * x[i];
   float ss = tree_sum<CH>(sq);
-  ss = group_sum<G>(ss);
+  ss = group_sum_dpp<G>(ss);
   const float mean = ss / (float)N;
   const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
 #pragma unroll
@@ -72,17 +74,23 @@ __device__ __forceinline__ void load_slice(const T* p, int c0, int N, bool vec, 
 
 // Sources a lane loads into registers together, up front, to serve both
 // passes of the mixture (one round trip to memory for them, instead of one
-// per source and pass): about 32 registers of slices.
+// per source and pass): about 32 registers of slices inside dg_block_out,
+// whose GEMM stages need the rest, and about 64 in attn_res_norm_kernel (at
+// n_embd 512, bf16, 10 sources took 21 us with 4 held).
 template <int CH>
 constexpr int res_held() {
   return CH <= 4 ? 8 : CH <= 8 ? 4 : CH <= 16 ? 2 : 1;
+}
+template <int CH>
+constexpr int res_held_norm() {
+  return CH <= 4 ? 16 : CH <= 8 ? 8 : CH <= 16 ? 4 : CH <= 32 ? 2 : 1;
 }
 
 template <typename T, int NPAD, int CH>
 __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a, const int vec) {
 #pragma clang fp contract(off)
   constexpr int G = NPAD / CH;
-  constexpr int HELD = res_held<CH>();
+  constexpr int HELD = res_held_norm<CH>();
   static_assert(G >= 1 && G <= 64, "row mapping");
   constexpr int ROWS_PER_BLOCK = 256 / G;
   const int sub = threadIdx.x % G;
@@ -121,7 +129,7 @@ __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a,
 #pragma unroll
     for (int i = 0; i < CH; ++i) prod[i] = rt<T>(x[i]) * w[i];
     float dot = tree_sum<CH>(prod);
-    dot = group_sum<G>(dot);
+    dot = group_sum_dpp<G>(dot);
     score[n] = rt<T>(dot);
     mx = fmaxf(mx, score[n]);
   }
@@ -405,7 +413,7 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
 #pragma unroll
     for (int i = 0; i < CH; ++i) prod[i] = rt<T>(x[i]) * w[i];
     float dot = tree_sum<CH>(prod);
-    dot = group_sum<G>(dot);
+    dot = group_sum_dpp<G>(dot);
     score[n] = rt<T>(dot);
     mx = fmaxf(mx, score[n]);
   }
