@@ -115,6 +115,24 @@ def test_swiglu_matches_reference(dev, dtype, rows):
     assert _rel(got, ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("pair,alpha,limit,expected", [
+    # the reference's known answers (tests/diff_gpt/model/test_swi_glu.py:21-102),
+    # the sigmoid written out: y = g * 1 / (1 + exp(-alpha * g)) * (l + 1)
+    ((1.0, 2.0), 2.0, 100.0, 1.0 / (1.0 + np.exp(-2.0)) * 3.0),      # no clamp
+    ((10.0, 10.0), 1.0, 5.0, 5.0 / (1.0 + np.exp(-5.0)) * 6.0),      # both halves clamped above
+    ((1.0, -10.0), 1.0, 5.0, 1.0 / (1.0 + np.exp(-1.0)) * -4.0),     # linear half clamped below
+    ((-10.0, 0.0), 1.0, 5.0, -10.0 / (1.0 + np.exp(10.0)) * 1.0),    # gate half has no lower clamp
+])
+def test_swiglu_kernel_known_answers(dev, pair, alpha, limit, expected):
+    """dg_swiglu on one (gate, linear) pair, fp32, at the reference's known
+    answers: within fp32 rounding of the closed form."""
+    from diff_gpt import _native
+
+    got = _native.ops().swiglu(torch.tensor([list(pair)], device=dev), alpha, limit)
+    assert got.shape == (1, 1)
+    assert abs(got.item() - expected) <= 1e-6 * max(1.0, abs(expected))
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
 def test_softcap_matches_reference(dev, dtype):
     from diff_gpt import _native
