@@ -220,6 +220,40 @@ def test_prefill_attention_random_shapes(dev, dtype, shape):
     assert err <= TOL[dtype], err
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("amp", [3.0, 20.0])
+@pytest.mark.parametrize("shape", [(2, 3, 300, 300, 64), (1, 2, 200, 700, 128)], ids=lambda s: "x".join(map(str, s)))
+def test_prefill_attention_large_scores(dev, dtype, amp, shape):
+    """Unnormalised q and k scaled by `amp`: scores spread over tens (amp 3)
+    or thousands (amp 20) of units, so the MFMA prefill kernels' running
+    maximum is raised many times along a row.  Against float64 attention:
+    bf16 within 2e-2; fp32 within 1e-5 at amp 3.  At amp 20 a score carries
+    fp32 rounding of order 0.1 (64 products of size ~1e5), which moves the
+    probabilities of near-tied keys by percents in any fp32 evaluation: there
+    the bar is 1.5x the deviation of the reference's own fp32 evaluation (torch
+    SDPA on the CPU) from float64, and both are printed."""
+    from diff_gpt import _native
+    from oracle import torch_ref as tr
+
+    B, H, Tq, Tk, D = shape
+    q = _randn((B, Tq, H, D), 7 + D, dtype, amp)
+    k = _randn((B, Tk, H, D), 8 + D, dtype, amp)
+    v = _randn((B, Tk, H, D), 9 + D, dtype)
+    ref = on.attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    y = _native.ops().attention(q.to(dev), k.to(dev), v.to(dev), 1.0 / np.sqrt(D))
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    bar = TOL[dtype]
+    if dtype == "f32" and amp > 3.0:
+        with torch.no_grad():
+            own = tr.sdpa(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)).transpose(1, 2)
+        own_err = np.abs(own.double().numpy() - ref).max() / np.abs(ref).max()
+        print(f"{shape} amp {amp}: ours {err:.3g}, reference fp32 {own_err:.3g} (x max|ref|)", flush=True)
+        bar = max(bar, 1.5 * own_err)
+    assert err <= bar, (err, bar)
+
+
 PREFILL_ROPE = [  # (B, H, Tq, Tk, D)
     (2, 3, 200, 200, 64),   # causal, ragged last query block
     (1, 2, 130, 330, 128),  # chunked (bottom-right mask), D = 128
