@@ -254,6 +254,28 @@ def test_prefill_attention_large_scores(dev, dtype, amp, shape):
     assert err <= bar, (err, bar)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(64, 4, 1, 144, 16), (4, 8, 1, 3000, 64), (2, 2, 1, 5000, 128)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_decode_attention_large_scores(dev, dtype, shape):
+    """Single-token decode (the vector kernel, with key splits merged in the
+    workgroup or through the workspace) on unnormalised q and k scaled by 3:
+    the wave-shared exponent offset is raised several times along the keys;
+    fp32 within 1e-5, bf16 within 2e-2 of float64."""
+    from diff_gpt import _native
+
+    B, H, Tq, Tk, D = shape
+    q = _randn((B, Tq, H, D), 17 + D, dtype, 3.0)
+    k = _randn((B, Tk, H, D), 18 + D, dtype, 3.0)
+    v = _randn((B, Tk, H, D), 19 + D, dtype)
+    ref = on.attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    y = _native.ops().attention(q.to(dev), k.to(dev), v.to(dev), 1.0 / np.sqrt(D))
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= TOL[dtype], err
+
+
 PREFILL_ROPE = [  # (B, H, Tq, Tk, D)
     (2, 3, 200, 200, 64),   # causal, ragged last query block
     (1, 2, 130, 330, 128),  # chunked (bottom-right mask), D = 128
