@@ -113,6 +113,9 @@ DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
  * (mha.py:64), the unmasked single-query decode when Tq == 1 (mha.py:68) and
  * the bottom-right chunk mask otherwise (mha.py:69-81).  Softmax in fp32.
  * scale is the SDPA scale (the reference uses the default 1/sqrt(D)).
+ * Prefills (Tq >= 16) at D = 64 or 128 with 16-byte aligned rows run on the
+ * matrix cores: bf16 / fp16 products with fp32 accumulation, fp32 inputs on
+ * fp32 products and accumulation; other shapes on the vector kernel.
  *
  * workspace: split-KV partials; dg_attention_workspace_size() gives the bytes
  * needed for these sizes: 0 unless a single-token decode splits the keys of
