@@ -789,6 +789,9 @@ def main():
     ap.add_argument("--engine-only", action="store_true",
                     help="run only the engine leg's one-call configs[1] job (twice: capture, then timed) "
                          "and print its JSON")
+    ap.add_argument("--jobs-only", action="store_true",
+                    help="run only the configs[3] / configs[4] decode-job legs (captured dg_decode_step launches) "
+                         "and print their JSON list")
     ap.add_argument("--e2e-only", choices=["configs[3]", "configs[4]"],
                     help="run only that configuration end to end through Engine.generate_multi_batch "
                          "(warm-up call, then the timed call) and print its JSON")
@@ -810,6 +813,9 @@ def main():
         return
     if args.engine_only:
         print(json.dumps(engine_leg(args.dtype, per_series=False)), flush=True)
+        return
+    if args.jobs_only:
+        print(json.dumps([decode_job_leg(name) for name in DECODE_JOBS]), flush=True)
         return
     if args.e2e_only:
         print(json.dumps(engine_multi_leg(args.e2e_only)), flush=True)

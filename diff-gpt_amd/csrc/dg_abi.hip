@@ -33,6 +33,12 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                   const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                   const PrefixRef& pre, const int* pos_dev, void* workspace,
                   size_t workspace_bytes, int size_keys, hipStream_t s);
+int vec_decode_step(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, const void* k,
+                    const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
+                    const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
+                    int fdtype, int pos, const int* pos_dev, int max_pos, void* y, const dg_stride3* y_st,
+                    float scale, const PrefixRef& pre, int qknorm, void* workspace, size_t workspace_bytes,
+                    bool* declined, hipStream_t s);
 // dg_attn_shared.hip
 bool shared_attention_applicable(int B, int H, int Tq, int Tk, int D, int dtype, const PrefixRef& pre,
                                  const void* q, const dg_stride3* q_st, const void* k,
@@ -315,6 +321,19 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
     return shared_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, kw, kc_st, vw, vc_st, freqs,
                               freqs_pos_stride, freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, pre, qknorm,
                               s);
+  // Where the attention runs on the vector kernel: one launch of its fused
+  // form, with the two launches' bits (below), unless the projections or the
+  // table are not aligned to its lane slices.
+  const bool vector_attention =
+      !(vec_attention_splits(B, H, 1, max_pos, D) == 1 &&
+        shared_attention_applicable(B, H, 1, max_pos, D, dtype, pre, y, y_st, kw, kc_st, vw, vc_st, y, y_st));
+  if (vector_attention && (freqs_dtype == DG_F32 || freqs_dtype == dtype)) {
+    bool declined = false;
+    rc = vec_decode_step(B, H, D, dtype, q, q_st, k, k_st, v, v_st, kw, kc_st, vw, vc_st, freqs, freqs_pos_stride,
+                         freqs_dtype, pos, pos_dev, max_pos, y, y_st, scale, pre, qknorm, workspace,
+                         workspace_bytes, &declined, s);
+    if (!declined) return rc;
+  }
   // Two launches: RoPE/QK-norm/append with the rotated q staged in y, then the
   // attention reading q from y (every attention kernel reads a query row
   // before it writes the output row at the same place).  Both index the

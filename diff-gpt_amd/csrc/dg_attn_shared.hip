@@ -158,30 +158,6 @@ __device__ __forceinline__ uint32_t lane_get_u(uint32_t x, int src) {
   return (uint32_t)__builtin_amdgcn_ds_bpermute(src << 2, (int)x);
 }
 
-// EPL fp32 values rounded to T and packed as the raw words of a row slice.
-template <typename T, int EPL>
-__device__ __forceinline__ void pack_row(RowRegs<T, EPL>& r, const float (&x)[EPL]) {
-  if constexpr (sizeof(T) == 4) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) r.w[e] = __float_as_uint(x[e]);
-  } else {
-#pragma unroll
-    for (int w = 0; w < EPL / 2; ++w) r.w[w] = pack_pair<T>(x[2 * w], x[2 * w + 1]);
-  }
-}
-
-template <typename T, int EPL>
-__device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
-  constexpr int W = RowRegs<T, EPL>::WORDS;
-  static_assert(W % 4 == 0 || W == 2, "row slice width");
-  if constexpr (W % 4 == 0) {
-#pragma unroll
-    for (int c4 = 0; c4 < W / 4; ++c4)
-      reinterpret_cast<u32x4_t*>(p)[c4] = u32x4_t{r.w[4 * c4], r.w[4 * c4 + 1], r.w[4 * c4 + 2], r.w[4 * c4 + 3]};
-  } else {
-    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{r.w[0], r.w[1]};
-  }
-}
 
 // O^T += V^T P^T over one 16-key tile on the 16-bit matrix cores
 // (v_mfma_f32_16x16x16_{bf16,f16}): lane (c, g) feeds va[t] = V[4g + i][16t + c]

@@ -25,7 +25,7 @@
 // splits, up to 16 splits of one (b, h, i) are the waves of one workgroup
 // and merge their unnormalised partials (acc, m, l) in LDS; more go to the
 // caller's workspace and attn_combine_kernel merges them.
-#include "dg_common.h"
+#include "dg_rope_math.h"
 
 namespace dg {
 
@@ -50,6 +50,17 @@ struct AttnArgs {
   // keys are positions 0 .. *pos_dev (the token of this step was appended at
   // *pos_dev), at most Tk of them; split_len follows from that count.
   const int* pos_dev;
+  // Fused decode step (FUSED instances, Tq == 1, mha.py:44-68 for one new
+  // token): q is the new token's query projection, kn / vn its key and value
+  // projections ((b, h) strides); the (cos, sin) row of position p is at
+  // freqs + p * fpos (fp32 when f32freqs, else T).  The position is pos_dev's
+  // value when set, else pos.  k and v (the cache pages) are written at it.
+  const void* kn;
+  const void* vn;
+  int64_t knb, knh, vnb, vnh;
+  const void* freqs;
+  int64_t fpos;
+  int f32freqs, qknorm, pos;
 };
 
 constexpr float kVecLazyLog2 = 8.0f;
@@ -60,7 +71,12 @@ constexpr int kMaxBlockSplits = 16;
 
 // MERGE: the workgroup's nsplit waves are the key splits of one (b, h, i)
 // (blockDim = 64 * nsplit); otherwise a workgroup holds 4 independent units.
-template <typename T, int DPAD, int EPL, int U, bool MERGE>
+// FUSED: the decode step of one new token in the same launch -- q and the new
+// key rotated (and normalised) with rope_qknorm_kernel's arithmetic, the key
+// and value appended by the wave whose split holds the position, and the new
+// key taken from registers in the trip slot where the two-call form reads it
+// back from the cache, so y has the two calls' bits.
+template <typename T, int DPAD, int EPL, int U, bool MERGE, bool FUSED>
 __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_kernel(const AttnArgs a) {
   constexpr int LPK = DPAD / EPL;
   constexpr int KPI = 64 / LPK;
@@ -93,8 +109,16 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
   const bool active = d0 < a.D;
   const int dl = active ? d0 : 0;  // inactive lanes (D not a power of two) read a valid slice
   int Tk = a.Tk, q_offset = a.q_offset, split_len = a.split_len;
-  if (a.pos_dev != nullptr) {  // uniform over the grid
-    Tk = min(*a.pos_dev + 1, a.Tk);
+  int pos = -1;         // fused: the new token's position
+  bool pos_ok = false;  // fused: the position lies in the rows' own pages (a.Tk = max_pos)
+  if (FUSED || a.pos_dev != nullptr) {  // uniform over the grid
+    if constexpr (FUSED) {
+      pos = a.pos_dev != nullptr ? *a.pos_dev : a.pos;
+      pos_ok = pos >= a.pre.own_start && pos < a.Tk;
+      Tk = min(pos + 1, a.Tk);
+    } else {
+      Tk = min(*a.pos_dev + 1, a.Tk);
+    }
     q_offset = Tk - 1;
     split_len = a.nsplit == 1 ? Tk : (((Tk + a.nsplit - 1) / a.nsplit + 15) / 16) * 16;
   }
@@ -104,10 +128,23 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
   const float c = a.scale_log2;
 
   Row qr;
-  load_row<T, EPL>(qr, static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + dl);
-  if (!active) {
+  Row knew, vnew;              // fused: the appended key and value
+  float xq[EPL], xk[EPL], cs[EPL];  // fused: q and k before RoPE, the (cos, sin) pairs
+  if constexpr (FUSED) {
+    load_vec<T, EPL>(static_cast<const T*>(a.q) + b * a.qb + (int64_t)h * a.qh + dl, xq);
+    load_vec<T, EPL>(static_cast<const T*>(a.kn) + b * a.knb + (int64_t)h * a.knh + dl, xk);
+    load_row<T, EPL>(vnew, static_cast<const T*>(a.vn) + b * a.vnb + (int64_t)h * a.vnh + dl);
+    // a position outside the pages writes nothing and reads table row 0
+    // (its y is undefined, as in the two-launch form)
+    const int64_t frow = pos_ok ? pos : 0;
+    if (a.f32freqs) load_vec<float, EPL>(static_cast<const float*>(a.freqs) + frow * a.fpos + dl, cs);
+    else load_vec<T, EPL>(static_cast<const T*>(a.freqs) + frow * a.fpos + dl, cs);
+  } else {
+    load_row<T, EPL>(qr, static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + dl);
+    if (!active) {
 #pragma unroll
-    for (int w = 0; w < Row::WORDS; ++w) qr.w[w] = 0u;  // contributes 0 to every dot
+      for (int w = 0; w < Row::WORDS; ++w) qr.w[w] = 0u;  // contributes 0 to every dot
+    }
   }
 
   // wave-uniform page bases; per-lane offsets of slot u inside a trip
@@ -159,7 +196,25 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
       }
     }
   };
-  auto process = [&](const Row (&kr)[U], const Row (&vr)[U], int t0) __attribute__((always_inline)) {
+  auto process = [&](Row (&kr)[U], Row (&vr)[U], int t0) __attribute__((always_inline)) {
+    if constexpr (FUSED) {
+      // the trip holding the new position takes its key and value from
+      // registers in every lane the cache read would fill from that row: the
+      // position's own slot and the slots past the last key, which re-read
+      // the last row (kend - 1 = pos) and are masked -- the row's old
+      // contents, read before the append, could be any bits
+      if (pos_ok && pos >= t0 && pos < t0 + STEP) {  // wave-uniform
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool mine = t0 + u * KPI + grp >= pos;
+#pragma unroll
+          for (int w = 0; w < Row::WORDS; ++w) {
+            kr[u].w[w] = mine ? knew.w[w] : kr[u].w[w];
+            vr[u].w[w] = mine ? vnew.w[w] : vr[u].w[w];
+          }
+        }
+      }
+    }
     float s[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -192,8 +247,31 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
   };
 
   int t0 = kbeg;
+  if (t0 < kend) load_trip(kA, vA, t0);
+  if constexpr (FUSED) {
+    // rope_qknorm_kernel's arithmetic on the lane's EPL elements (lanes past
+    // D hold zeros, which leave the row norm unchanged), while the first
+    // trip's keys are in flight; then the append (kv_cache.py:108-109) by the
+    // split that holds the position, after those loads in program order (the
+    // slot they read at the position is replaced from registers anyway)
+    if (!active) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) xq[e] = xk[e] = 0.f;
+    }
+    rope_rotate<T, EPL>(xq, cs);
+    rope_rotate<T, EPL>(xk, cs);
+    if (a.qknorm) {
+      qk_rms_norm<EPL, LPK, true>(xq, a.D);
+      qk_rms_norm<EPL, LPK, true>(xk, a.D);
+    }
+    pack_row<T, EPL>(qr, xq);
+    pack_row<T, EPL>(knew, xk);
+    if (pos_ok && pos >= kbeg && pos < kend && grp == 0 && active) {
+      store_row<T, EPL>(const_cast<T*>(kbase) + (int64_t)pos * kt + d0, knew);
+      store_row<T, EPL>(const_cast<T*>(vbase) + (int64_t)pos * vt + d0, vnew);
+    }
+  }
   if (t0 < kend) {
-    load_trip(kA, vA, t0);
     while (true) {
       if (t0 + STEP < kend) load_trip(kB, vB, t0 + STEP);
       process(kA, vA, t0);
@@ -399,19 +477,19 @@ constexpr int slots_for() {
   return EPL * (int)sizeof(T) >= 16 ? 2 : 4;
 }
 
-template <typename T, int DPAD, int EPL>
+template <typename T, int DPAD, int EPL, bool FUSED>
 int launch_attn(AttnArgs a, hipStream_t s) {
   if (a.nsplit > 1 && a.nsplit <= kMaxBlockSplits) {
     // one workgroup per (b, h, i), one wave per key split, merged in LDS
     const int64_t blocks = a.units / a.nsplit;
     DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), true>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), true, FUSED>), dim3((unsigned)blocks),
                        dim3(64 * a.nsplit), 0, s, a);
     return check_launch("attn_vec_kernel");
   }
   const int64_t blocks = (a.units + 3) / 4;
   DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), false>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), false, FUSED>), dim3((unsigned)blocks),
                      dim3(256), 0, s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
@@ -426,30 +504,30 @@ int launch_attn(AttnArgs a, hipStream_t s) {
   return check_launch("attn_combine_kernel");
 }
 
-template <typename T, int DPAD>
+template <typename T, int DPAD, bool FUSED>
 int attn_pick_epl(int epl, const AttnArgs& a, hipStream_t s) {
   constexpr int PREF = (16 / (int)sizeof(T)) < DPAD ? (16 / (int)sizeof(T)) : DPAD;
   if constexpr (PREF != 2) {
-    if (epl == PREF) return launch_attn<T, DPAD, PREF>(a, s);
+    if (epl == PREF) return launch_attn<T, DPAD, PREF, FUSED>(a, s);
   }
   if constexpr (DPAD / 2 <= 64) {
-    if (epl == 2) return launch_attn<T, DPAD, 2>(a, s);
+    if (epl == 2) return launch_attn<T, DPAD, 2, FUSED>(a, s);
   }
   set_error("attention: no kernel for D pad %d with %d elements per lane", DPAD, epl);
   return DG_EUNSUPPORTED;
 }
 
-template <typename T>
+template <typename T, bool FUSED = false>
 int attn_pick_d(int dpad, int epl, const AttnArgs& a, hipStream_t s) {
   switch (dpad) {
-    case 2: return attn_pick_epl<T, 2>(epl, a, s);
-    case 4: return attn_pick_epl<T, 4>(epl, a, s);
-    case 8: return attn_pick_epl<T, 8>(epl, a, s);
-    case 16: return attn_pick_epl<T, 16>(epl, a, s);
-    case 32: return attn_pick_epl<T, 32>(epl, a, s);
-    case 64: return attn_pick_epl<T, 64>(epl, a, s);
-    case 128: return attn_pick_epl<T, 128>(epl, a, s);
-    case 256: return attn_pick_epl<T, 256>(epl, a, s);
+    case 2: return attn_pick_epl<T, 2, FUSED>(epl, a, s);
+    case 4: return attn_pick_epl<T, 4, FUSED>(epl, a, s);
+    case 8: return attn_pick_epl<T, 8, FUSED>(epl, a, s);
+    case 16: return attn_pick_epl<T, 16, FUSED>(epl, a, s);
+    case 32: return attn_pick_epl<T, 32, FUSED>(epl, a, s);
+    case 64: return attn_pick_epl<T, 64, FUSED>(epl, a, s);
+    case 128: return attn_pick_epl<T, 128, FUSED>(epl, a, s);
+    case 256: return attn_pick_epl<T, 256, FUSED>(epl, a, s);
   }
   set_error("attention: head_dim %d unsupported", a.D);
   return DG_EUNSUPPORTED;
@@ -470,11 +548,27 @@ size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
   return (size_t)B * H * Tq * ns * (size_t)(next_pow2(D) + 2) * sizeof(float);
 }
 
-int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
-                  const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
-                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
-                  const PrefixRef& pre, const int* pos_dev, void* workspace,
-                  size_t workspace_bytes, int size_keys, hipStream_t s) {
+// The fused decode step's extra inputs (dg_decode_step): the new token's key
+// and value projections and the (cos, sin) table.
+struct VecStep {
+  const void* kn;
+  const dg_stride3* kn_st;
+  const void* vn;
+  const dg_stride3* vn_st;
+  const void* freqs;
+  int64_t fpos;
+  int fdtype, qknorm, pos;
+};
+
+namespace {
+
+// The vector kernel's launch.  With step != nullptr (Tq == 1, Tk = max_pos)
+// it is the fused decode step; when the projections or the table are not
+// aligned to the kernel's lane slices it launches nothing and sets *declined.
+int vec_launch(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, const dg_stride3* q_st,
+               const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
+               const dg_stride3* y_st, float scale, const PrefixRef& pre, const int* pos_dev, void* workspace,
+               size_t workspace_bytes, int size_keys, const VecStep* step, bool* declined, hipStream_t s) {
   // size_keys (>= Tk) sizes the key splits and the workspace: a decode step
   // passes its max_pos, so that the host- and device-position forms split
   // the same way and give the same bits
@@ -495,13 +589,26 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
     const int64_t bytes = (int64_t)epl * es;
     const bool pre_ok = pre.len == 0 || (aligned(pre.k, bytes) && aligned(pre.v, bytes) && pre.kb % epl == 0 &&
                                          pre.kh % epl == 0 && pre.vb % epl == 0 && pre.vh % epl == 0);
+    bool step_ok = true;
+    if (step != nullptr) {
+      // the table row's slice of a lane: epl elements of the table's dtype
+      const int64_t fes = step->fdtype == DG_F32 ? 4 : 2;
+      const int64_t fbytes = epl * fes < 16 ? epl * fes : 16;
+      step_ok = aligned(step->kn, bytes) && aligned(step->vn, bytes) && step->kn_st->b % epl == 0 &&
+                step->kn_st->h % epl == 0 && step->vn_st->b % epl == 0 && step->vn_st->h % epl == 0 &&
+                aligned(step->freqs, fbytes) && (step->fpos * fes) % fbytes == 0;
+    }
     return aligned(q, bytes) && aligned(k, bytes) && aligned(v, bytes) && aligned(y, bytes) &&
            strides_multiple(q_st, epl) && strides_multiple(k_st, epl) &&
-           strides_multiple(v_st, epl) && strides_multiple(y_st, epl) && pre_ok;
+           strides_multiple(v_st, epl) && strides_multiple(y_st, epl) && pre_ok && step_ok;
   };
   int epl = 0;
   if (fits(pref)) epl = pref;
   else if (fits(2)) epl = 2;
+  if (epl == 0 && step != nullptr) {
+    *declined = true;
+    return DG_OK;
+  }
   DG_REQUIRE(epl != 0, DG_EINVAL,
              "attention: pointers/strides not aligned to an element pair (D=%d); pass contiguous rows", D);
 
@@ -517,6 +624,14 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.lazy_raw = kVecLazyLog2 / a.scale_log2;
   a.pre = pre;
   a.pos_dev = pos_dev;
+  if (step != nullptr) {
+    a.kn = step->kn; a.vn = step->vn;
+    a.knb = step->kn_st->b; a.knh = step->kn_st->h; a.vnb = step->vn_st->b; a.vnh = step->vn_st->h;
+    a.freqs = step->freqs; a.fpos = step->fpos;
+    a.f32freqs = step->fdtype == DG_F32 ? 1 : 0;
+    a.qknorm = step->qknorm;
+    a.pos = step->pos;
+  }
 
   DG_REQUIRE(size_keys >= Tk, DG_EINVAL, "attention: split sizing for %d keys below Tk = %d", size_keys, Tk);
   int ns = vec_attention_splits(B, H, Tq, size_keys, D);
@@ -534,9 +649,44 @@ int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
   a.units = (int64_t)B * H * Tq * ns;
   DG_REQUIRE(a.units < ((int64_t)1 << 31), DG_EINVAL, "attention: B*H*Tq*splits must be below 2^31");
 
+  if (step != nullptr) {
+    if (dtype == DG_F32) return attn_pick_d<float, true>(dpad, epl, a, s);
+    if (dtype == DG_BF16) return attn_pick_d<bf16_t, true>(dpad, epl, a, s);
+    return attn_pick_d<f16_t, true>(dpad, epl, a, s);
+  }
   if (dtype == DG_F32) return attn_pick_d<float>(dpad, epl, a, s);
   if (dtype == DG_BF16) return attn_pick_d<bf16_t>(dpad, epl, a, s);
   return attn_pick_d<f16_t>(dpad, epl, a, s);
+}
+
+}  // namespace
+
+int vec_attention(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
+                  const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
+                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
+                  const PrefixRef& pre, const int* pos_dev, void* workspace,
+                  size_t workspace_bytes, int size_keys, hipStream_t s) {
+  return vec_launch(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale, pre, pos_dev, workspace,
+                    workspace_bytes, size_keys, nullptr, nullptr, s);
+}
+
+// The decode step of one new token in one launch of the vector kernel
+// (dg_decode_step where the attention runs on it): q, k, v are the token's
+// projections, kc / vc the cache pages (written at the position: pos_dev's
+// value when set, else pos), keys 0 .. position attended.  The kernel, its
+// key splits and the workspace follow max_pos, as in the two-launch form,
+// whose y it reproduces bit for bit.  *declined: the projections or the
+// table are not aligned to the kernel's lane slices; nothing was launched.
+int vec_decode_step(int B, int H, int D, int dtype, const void* q, const dg_stride3* q_st, const void* k,
+                    const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* kc,
+                    const dg_stride3* kc_st, void* vc, const dg_stride3* vc_st, const void* freqs, int64_t fpos,
+                    int fdtype, int pos, const int* pos_dev, int max_pos, void* y, const dg_stride3* y_st,
+                    float scale, const PrefixRef& pre, int qknorm, void* workspace, size_t workspace_bytes,
+                    bool* declined, hipStream_t s) {
+  *declined = false;
+  const VecStep step{k, k_st, v, v_st, freqs, fpos, fdtype, qknorm, pos};
+  return vec_launch(B, H, 1, max_pos, D, dtype, q, q_st, kc, kc_st, vc, vc_st, y, y_st, scale, pre, pos_dev,
+                    workspace, workspace_bytes, max_pos, &step, declined, s);
 }
 
 }  // namespace dg

@@ -303,6 +303,34 @@ __device__ __forceinline__ void load_row(RowRegs<T, EPL>& r, const T* p) {
   }
 }
 
+// EPL fp32 values rounded to T and packed as the raw words of a row slice.
+template <typename T, int EPL>
+__device__ __forceinline__ void pack_row(RowRegs<T, EPL>& r, const float (&x)[EPL]) {
+  if constexpr (sizeof(T) == 4) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) r.w[e] = __float_as_uint(x[e]);
+  } else {
+#pragma unroll
+    for (int w = 0; w < EPL / 2; ++w) r.w[w] = pack_pair<T>(x[2 * w], x[2 * w + 1]);
+  }
+}
+
+// The row slice's raw words to memory (naturally aligned by the host checks).
+template <typename T, int EPL>
+__device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
+  constexpr int W = RowRegs<T, EPL>::WORDS;
+  if constexpr (W % 4 == 0) {
+#pragma unroll
+    for (int c4 = 0; c4 < W / 4; ++c4)
+      reinterpret_cast<u32x4_t*>(p)[c4] = u32x4_t{r.w[4 * c4], r.w[4 * c4 + 1], r.w[4 * c4 + 2], r.w[4 * c4 + 3]};
+  } else if constexpr (W == 2) {
+    *reinterpret_cast<u32x2_t*>(p) = u32x2_t{r.w[0], r.w[1]};
+  } else {
+    static_assert(W == 1, "row slice width");
+    *reinterpret_cast<uint32_t*>(p) = r.w[0];
+  }
+}
+
 // Element e of the slice as fp32.
 template <typename T, int EPL>
 __device__ __forceinline__ float elem(const RowRegs<T, EPL>& r, int e) {

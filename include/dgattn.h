@@ -271,10 +271,16 @@ DG_API int dg_decode_attention_at(int B, int H, int D, int dtype,
  * key and value are appended and also used from registers.  The cache
  * contents are those of dg_rope_qknorm_append bit for bit; y equals the
  * two-call result within fp32 rounding (the new key is accumulated last).
- * Other shapes run two launches, with the rotated q staged in y:
- * dg_rope_qknorm_append at p, then the decode attention over 0 .. p with its
- * kernel and key splits chosen for max_pos -- in both position forms, since
- * the device form must fix them for every p a captured graph replays.  So y
+ * Where the attention runs on the vector kernel (every other shape whose
+ * rows, projections and table are aligned to its lane slices) it is one
+ * launch too: each (row, head) wave rotates q and k itself, the wave whose
+ * key split holds p appends them, and the new key enters the softmax from
+ * registers in the slot where the two-launch form reads it back, so y has
+ * the two-launch form's bits.  Any other shape runs those two launches, with
+ * the rotated q staged in y: dg_rope_qknorm_append at p, then the decode
+ * attention over 0 .. p.  Both choose the kernel and key splits for max_pos
+ * -- in both position forms, since the device form must fix them for every
+ * p a captured graph replays.  So y
  * equals dg_decode_attention_at's (max_keys = max_pos) bit for bit, host and
  * device position alike; it equals the two calls dg_rope_qknorm_append +
  * dg_attention_grouped over p + 1 keys bit for bit when both choose the same

@@ -573,11 +573,11 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     # capacity, so they still agree bit for bit (ragged last group)
     (155, 100, 2, 188, 243, 32, 261),
     (200, 100, 2, 188, 243, 16, 261),
-    (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: two launches
+    (6, 1, 4, 0, 23, 16, 40),         # no shared prefix: the vector kernel's fused step
     # no shared prefix, pos + 1 = 201 keys (one split) but max_pos = 300 (two):
     # y is dg_decode_attention_at's over max_pos, not the two calls' bits
     (1, 1, 1, 0, 200, 16, 300),
-    (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): two launches
+    (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): the vector kernel's fused step
 ]
 
 
@@ -585,11 +585,12 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
 @pytest.mark.parametrize("shape", DECODE_STEP, ids=lambda s: "x".join(map(str, s)))
 def test_decode_step_matches_two_calls(dev, dtype, shape):
     """dg_decode_step == dg_rope_qknorm_append at pos + dg_attention_grouped over
-    0 .. pos: the cache bit for bit.  Where it makes two launches, y bit for
-    bit dg_decode_attention_at's over max_pos = cap (kernel and key splits
-    chosen for the capacity), and the two calls' wherever those choose the
-    same number of key splits; within the north-star bars of them and of fp64
-    where it fuses the step or the split counts differ.  The device-position
+    0 .. pos: the cache bit for bit.  Where the attention runs on the vector
+    kernel (its fused one-launch step), y bit for bit dg_decode_attention_at's
+    over max_pos = cap (kernel and key splits chosen for the capacity), and
+    the two calls' wherever those choose the same number of key splits;
+    within the north-star bars of them and of fp64 where the shared-prefix
+    kernel fuses the step or the split counts differ.  The device-position
     form equal to the host-position form; an out-of-range device position
     leaves the cache untouched."""
     from diff_gpt import _native
@@ -645,6 +646,42 @@ def test_decode_step_matches_two_calls(dev, dtype, shape):
                          torch.tensor([cap], dtype=torch.int32, device=dev), prefix, group)
     torch.cuda.synchronize()
     assert torch.equal(c4.cpu(), cache)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(6, 1, 4, 0, 23, 16, 40), (3, 1, 2, 0, 70, 64, 100), (2, 1, 2, 0, 600, 128, 700)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_decode_step_ignores_old_contents_at_the_position(dev, dtype, shape):
+    """The fused decode step appends the new key and value while it streams
+    the keys: the cache rows at and past the position hold NaN before the
+    step (stale or uninitialised memory), yet y equals the two calls' (which
+    append first) bit for bit, with the host and the device position, and the
+    cache holds the new row."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, G, H, P, pos, D, cap = shape
+    cache = torch.full((2, B, H, cap, D), float("nan"), dtype=TDT[dtype])
+    cache[:, :, :, :pos] = _randn((B, 2, H, pos, D), 91 + D, dtype).transpose(0, 1)
+    q, k, v = (_randn((B, 1, H, D), 92 + D + i, dtype, 2.0).to(dev) for i in range(3))
+    table = precompute_freqs_cis(D, 2 * cap, 10000).to(TDT[dtype]).to(dev)
+    scale = 1.0 / np.sqrt(D)
+    ops = _native.ops()
+    c1 = cache.to(dev)
+    q_rot = torch.empty_like(q)
+    ops.rope_qknorm_append(q, k, v, table[pos:pos + 1].view(1, 1, 1, D // 2, 2), q_rot,
+                           c1[0, :, :, pos:pos + 1].transpose(1, 2), c1[1, :, :, pos:pos + 1].transpose(1, 2), True)
+    y_at = torch.empty_like(q)
+    _native.decode_attention_at_(q_rot, c1[0].transpose(1, 2), c1[1].transpose(1, 2), y_at, scale,
+                                 torch.tensor([pos], dtype=torch.int32, device=dev))
+    for p_arg in (pos, torch.tensor([pos], dtype=torch.int32, device=dev)):
+        c2, y2 = cache.to(dev), torch.empty_like(q)
+        _native.decode_step_(q, k, v, table if isinstance(p_arg, torch.Tensor) else table[pos],
+                             c2[0].transpose(1, 2), c2[1].transpose(1, 2), y2, scale, p_arg)
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(y2).all())
+        assert torch.equal(y2, y_at)
+        assert torch.equal(c2[:, :, :, :pos + 1], c1[:, :, :, :pos + 1])
 
 
 def _random_decode_steps(seed, n):
