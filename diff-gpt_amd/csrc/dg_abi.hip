@@ -234,7 +234,7 @@ extern "C" int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, c
   DG_REQUIRE(mfma_prefill_rope_applicable(B, H, Tq, Tk, D, dtype, q, q_st, freqs, f_st, freqs_dtype, k, k_st, v,
                                           v_st, y, y_st, scale),
              DG_EUNSUPPORTED,
-             "prefill_rope: not taken by the fused kernel (bf16/fp16, head_dim 64 or 128, Tq >= 16, "
+             "prefill_rope: not taken by the fused kernels (bf16/fp16/fp32, head_dim 64 or 128, Tq >= 16, "
              "16-byte aligned rows); use dg_rope_qknorm_append + dg_attention");
   return mfma_prefill_rope(B, H, Tq, Tk, D, dtype, q, q_st, freqs, f_st, freqs_dtype, (flags & DG_QKNORM) != 0,
                            (flags & DG_KEYS_NORMED) != 0, k, k_st, v, v_st, y, y_st, scale,

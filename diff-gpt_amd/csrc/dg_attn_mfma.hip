@@ -801,7 +801,6 @@ bool mfma_prefill_rope_applicable(int B, int H, int Tq, int Tk, int D, int dtype
                                   int fdtype, const void* k, const dg_stride3* k_st, const void* v,
                                   const dg_stride3* v_st, const void* y, const dg_stride3* y_st,
                                   float scale) {
-  if (dtype != DG_BF16 && dtype != DG_F16) return false;  // no fp32 form
   if (!mfma_prefill_applicable(B, H, Tq, Tk, D, dtype, q, q_st, k, k_st, v, v_st, y, y_st, scale)) return false;
   if (fdtype != dtype && fdtype != DG_F32) return false;
   const int64_t fes = fdtype == DG_F32 ? 4 : 2;
@@ -836,6 +835,7 @@ int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void
   // at D = 128; a scale above 0.68 / 0.34 there runs the running-maximum
   // form).  bf16 only: p reaches 2^16.5 at D = 128 with the SDPA scale, beyond
   // fp16's range, while bf16 has fp32's exponent range
+  if (dtype == DG_F32) return launch_prefill_f32(a, D, s);  // running maximum; fp32 table
   const bool small_scores = (double)scale * 1.4426950408889634 * D * (1.0 + 1.0 / 128.0) <= 64.0;
   const bool bounded = qknorm && keys_normed && dtype == DG_BF16 && small_scores;
   if (dtype == DG_BF16)

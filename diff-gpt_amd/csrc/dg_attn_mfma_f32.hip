@@ -37,7 +37,15 @@
 // piece ^ (r & 15): the K operand reads (16 rows, one piece each, per 16
 // lanes) and the V reads (one whole row per 32 lanes) are free of bank
 // conflicts.
+//
+// ROPE instances (dg_prefill_rope) rotate and normalise each query row as it
+// is loaded (mha.py:44-48) with rope_qknorm_kernel's arithmetic: a lane's
+// half row rotates with its (cos, sin) pairs (rope_rotate), its squares sum
+// by the pairwise tree (tree_sum) and meet the other half's in lane l^32 --
+// the top level of the same tree over the row -- so the operand has the bits
+// dg_rope_qknorm_append would store.
 #include "dg_prefill.h"
+#include "dg_rope_math.h"
 
 namespace dg {
 
@@ -72,7 +80,7 @@ constexpr int prefill_f32_wgs_per_cu() {
   return D == 64 ? 4 : 2;
 }
 
-template <int D>
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256, (prefill_f32_wgs_per_cu<D>()))
 void prefill_mfma_f32_kernel(const PrefillArgs a) {
   using C = PrefillF32Cfg<D>;
@@ -142,9 +150,9 @@ void prefill_mfma_f32_kernel(const PrefillArgs a) {
   // Q^T operands: lane (r32, hh) holds Q[qw + r32][(D/2)*hh + c], c < D/2.
   // Rows past Tq hold row Tq - 1 (finite) and are never stored.
   float qf[QC];
+  const int qi0 = min(qw + r32, a.Tq - 1);
   {
-    const int qi = min(qw + r32, a.Tq - 1);
-    const f32x4v_t* src = reinterpret_cast<const f32x4v_t*>(qp + (int64_t)qi * a.qt + QC * hh);
+    const f32x4v_t* src = reinterpret_cast<const f32x4v_t*>(qp + (int64_t)qi0 * a.qt + QC * hh);
 #pragma unroll
     for (int m = 0; m < QC / 4; ++m) {
       const f32x4v_t x = src[m];
@@ -154,7 +162,26 @@ void prefill_mfma_f32_kernel(const PrefillArgs a) {
       qf[4 * m + 3] = x[3];
     }
   }
+  float cs[ROPE ? QC : 1];
+  if constexpr (ROPE)
+    load_vec<float, QC>(static_cast<const float*>(a.freqs) + b * a.fb + (int64_t)qi0 * a.ft + (int64_t)head * a.fh +
+                            QC * hh,
+                        cs);
   dma_tile(ks0, vs0, 0);
+  if constexpr (ROPE) {
+#pragma clang fp contract(off)
+    rope_rotate<float, QC>(qf, cs);
+    if (a.qknorm) {
+      // lanes l and l^32 hold the same row, so both take this branch
+      float sq[QC];
+#pragma unroll
+      for (int c = 0; c < QC; ++c) sq[c] = qf[c] * qf[c];
+      const float mean = half_pair_sum(tree_sum<QC>(sq)) / (float)D;
+      const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+#pragma unroll
+      for (int c = 0; c < QC; ++c) qf[c] = qf[c] * r;
+    }
+  }
 
   const int kv_end = min(a.Tk, q0 + C::BM + qoff);
   const int ntiles = (kv_end + BN - 1) / BN;
@@ -283,13 +310,15 @@ int launch_prefill_f32(PrefillArgs a, int D, hipStream_t s) {
   DG_REQUIRE(a.nqb <= 65535 && nwin <= 65535, DG_EINVAL, "prefill: %d query blocks, %d windows, at most 65535 each",
              a.nqb, nwin);
   const dim3 grid((unsigned)a.win, (unsigned)a.nqb, (unsigned)nwin);
-  if (D == 64) {
-    static_assert(PrefillF32Cfg<64>::BM == BM, "query block size");
-    hipLaunchKernelGGL(prefill_mfma_f32_kernel<64>, grid, dim3(PrefillF32Cfg<64>::NT), 0, s, a);
+  static_assert(PrefillF32Cfg<64>::BM == BM && PrefillF32Cfg<128>::BM == BM, "query block size");
+  DG_REQUIRE(D == 64 || D == 128, DG_EINVAL, "prefill_f32: head_dim %d (64 or 128)", D);
+  const dim3 block(PrefillF32Cfg<64>::NT);
+  if (a.freqs != nullptr) {
+    if (D == 64) hipLaunchKernelGGL((prefill_mfma_f32_kernel<64, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma_f32_kernel<128, true>), grid, block, 0, s, a);
   } else {
-    DG_REQUIRE(D == 128, DG_EINVAL, "prefill_f32: head_dim %d (64 or 128)", D);
-    static_assert(PrefillF32Cfg<128>::BM == BM, "query block size");
-    hipLaunchKernelGGL(prefill_mfma_f32_kernel<128>, grid, dim3(PrefillF32Cfg<128>::NT), 0, s, a);
+    if (D == 64) hipLaunchKernelGGL((prefill_mfma_f32_kernel<64, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma_f32_kernel<128, false>), grid, block, 0, s, a);
   }
   return check_launch("prefill_mfma_f32_kernel");
 }

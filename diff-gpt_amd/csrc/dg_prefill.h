@@ -32,7 +32,8 @@ constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
 // fp32 prefill on v_mfma_f32_32x32x2_f32 (dg_attn_mfma_f32.hip): D is 64 or
-// 128; a.nqb is set by the launch.
+// 128; a.nqb is set by the launch.  With a.freqs set, q is rotated (and
+// normalised when a.qknorm) as it is loaded (fp32 table).
 int launch_prefill_f32(PrefillArgs a, int D, hipStream_t s);
 
 }  // namespace dg

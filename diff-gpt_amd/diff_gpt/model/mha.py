@@ -157,7 +157,7 @@ class MultiHeadAttention(nn.Module):
         assert kv_cache is None or kv_cache.pos_dev is None, "a captured decode step takes one token per row"
         # Prefills the MFMA kernel takes rotate and normalise q as they load it
         # (dg_prefill_rope); the first launch then handles k and v only.
-        fuse_q = T >= 16 and D in (64, 128) and q.dtype in (torch.bfloat16, torch.float16)
+        fuse_q = T >= 16 and D in (64, 128) and q.dtype in (torch.bfloat16, torch.float16, torch.float32)
         q_rot = None if fuse_q else torch.empty((B, T, H, D), dtype=q.dtype, device=q.device)
         q_in = None if fuse_q else q
         if kv_cache is None:

@@ -149,11 +149,11 @@ DG_API int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype,
  * bound on a score in log2 units that keeps exp2 of every score inside
  * fp32's normal range: scale up to about 0.68 at head_dim 64 and 0.34 at 128,
  * the SDPA scale 1/sqrt(D) well inside.  A larger scale, and fp16 data,
- * ignore the flag and give dg_attention's y bit for bit).
- * Only the MFMA prefill kernel's shapes are taken (bf16 or
- * fp16, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
+ * ignore the flag and give dg_attention's y bit for bit, as fp32 data always
+ * does).  Only the MFMA prefill kernels' shapes are taken (bf16, fp16 or
+ * fp32, head_dim 64 or 128, Tq >= 16, scale > 0, 16-byte aligned rows,
  * freqs in the data's dtype or fp32, Tq <= 65535 * 128 and B*H <= 65535 * 64,
- * one head's K and V rows within 2^30 elements): anything else returns
+ * one head's K and V rows within 2^31 bytes): anything else returns
  * DG_EUNSUPPORTED and does nothing, and the caller makes the two calls.
  */
 DG_API int dg_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype,

@@ -284,7 +284,7 @@ PREFILL_ROPE = [  # (B, H, Tq, Tk, D)
 ]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("fdt", ["f32", "data"])
 @pytest.mark.parametrize("qknorm", [True, False], ids=["qknorm", "rope"])
 @pytest.mark.parametrize("shape", PREFILL_ROPE, ids=lambda s: "x".join(map(str, s)))
@@ -328,7 +328,7 @@ def _random_rope_prefills(seed, n):
 
 
 @pytest.mark.parametrize("qknorm", [True, False])
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("shape", _random_rope_prefills(77, 10), ids=lambda s: "x".join(map(str, s)))
 def test_prefill_rope_random_shapes(dev, dtype, qknorm, shape):
     """Seeded random causal (Tq = Tk) and chunked (Tq < Tk) shapes: the fused
@@ -417,8 +417,8 @@ def test_prefill_rope_keys_normed_large_scale_keeps_running_max(dev, D):
     assert torch.equal(y[:, 0], v[:, 0])  # one visible key: its value
 
 
-@pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 64), "f32"),
-                                         ((1, 2, 8, 8, 64), "bf16")])
+@pytest.mark.parametrize("shape,dtype", [((1, 2, 40, 40, 32), "bf16"), ((1, 2, 40, 40, 32), "f32"),
+                                         ((1, 2, 8, 8, 64), "bf16"), ((1, 2, 8, 8, 128), "f32")])
 def test_prefill_rope_unsupported_shapes_do_nothing(dev, shape, dtype):
     """Shapes the MFMA kernel does not take return False and leave y alone."""
     from diff_gpt import _native
