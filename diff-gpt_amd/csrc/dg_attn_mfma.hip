@@ -751,9 +751,10 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
   if (D != 64 && D != 128) return false;
   if (Tq < 16) return false;  // decode and tiny chunks: vector kernel
   // grid (window, query blocks, windows): at most 65535 query blocks of 128
-  // and 65535 windows of kPrefillWindow pairs
+  // and 65535 windows (of kPrefillWindowLong pairs at the least)
   const int64_t nbh = (int64_t)B * H;
-  if (nbh <= 0 || (Tq + 127) / 128 > 65535 || (nbh + kPrefillWindow - 1) / kPrefillWindow > 65535) return false;
+  if (nbh <= 0 || (Tq + 127) / 128 > 65535 || (nbh + kPrefillWindowLong - 1) / kPrefillWindowLong > 65535)
+    return false;
   // per-head byte offsets (buffer ranges) are 32-bit signed inside the kernels
   const int64_t es = dtype == DG_F32 ? 4 : 2;
   const int64_t span = (int64_t)Tk * (k_st->t > v_st->t ? k_st->t : v_st->t);
@@ -763,7 +764,7 @@ bool mfma_prefill_applicable(int B, int H, int Tq, int Tk, int D, int dtype, con
 }
 
 namespace {
-PrefillArgs prefill_args(int B, int H, int Tq, int Tk, const void* q, const dg_stride3* q_st, const void* k,
+PrefillArgs prefill_args(int B, int H, int Tq, int Tk, int D, const void* q, const dg_stride3* q_st, const void* k,
                          const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
                          const dg_stride3* y_st, float scale) {
   PrefillArgs a{};
@@ -775,9 +776,15 @@ PrefillArgs prefill_args(int B, int H, int Tq, int Tk, const void* q, const dg_s
   a.H = H; a.Tq = Tq; a.Tk = Tk;
   a.q_offset = Tk - Tq;
   a.nbh = B * H;
-  // 64 (b, h) pairs per window: measured best or within 1 % of it from
-  // B*H = 64 to 2048 at T = 1024 and 3584, D = 64 and 128
-  a.win = B * H < kPrefillWindow ? B * H : kPrefillWindow;
+  // (b, h) pairs per scheduling window.  All query blocks of a pair share one
+  // XCD, so a window keeps win/8 heads' K and V in each XCD's 4 MB L2.  32
+  // for long rows (a head's K/V of 1 MB or more in bf16: at configs[4] the
+  // FETCH_SIZE traffic drops from 4.35 to 2.68 GB per launch and the time by
+  // 1 %) and for large batches (B*H >= 2048: +1 to +2 % at configs[2] /
+  // configs[3]); 64 otherwise (B*H = 256 and D = 64 at T = 3584 measured 0.5
+  // to 2.5 % slower with 32)
+  const int win = (B * H >= 2048 || (int64_t)Tk * D >= 262144) ? kPrefillWindowLong : kPrefillWindow;
+  a.win = B * H < win ? B * H : win;
   a.scale_log2 = scale * 1.44269504088896340736f;
   a.lazy_raw = kLazyLog2 / a.scale_log2;
   return a;
@@ -788,7 +795,7 @@ int mfma_prefill(int B, int H, int Tq, int Tk, int D, int dtype, const void* q,
                  const dg_stride3* q_st, const void* k, const dg_stride3* k_st, const void* v,
                  const dg_stride3* v_st, void* y, const dg_stride3* y_st, float scale,
                  hipStream_t s) {
-  const PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
+  const PrefillArgs a = prefill_args(B, H, Tq, Tk, D, q, q_st, k, k_st, v, v_st, y, y_st, scale);
   if (dtype == DG_F32) return launch_prefill_f32(a, D, s);
   if (dtype == DG_BF16) return D == 64 ? launch_prefill<bf16_t, 64>(a, s) : launch_prefill<bf16_t, 128>(a, s);
   return D == 64 ? launch_prefill<f16_t, 64>(a, s) : launch_prefill<f16_t, 128>(a, s);
@@ -822,7 +829,7 @@ int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void
                       const void* freqs, const dg_stride3* f_st, int fdtype, int qknorm, int keys_normed,
                       const void* k, const dg_stride3* k_st, const void* v, const dg_stride3* v_st, void* y,
                       const dg_stride3* y_st, float scale, hipStream_t s) {
-  PrefillArgs a = prefill_args(B, H, Tq, Tk, q, q_st, k, k_st, v, v_st, y, y_st, scale);
+  PrefillArgs a = prefill_args(B, H, Tq, Tk, D, q, q_st, k, k_st, v, v_st, y, y_st, scale);
   a.freqs = freqs;
   a.fb = f_st->b; a.ft = f_st->t; a.fh = f_st->h;
   a.qknorm = qknorm;

@@ -28,7 +28,8 @@ struct PrefillArgs {
   int qknorm;
 };
 
-constexpr int kPrefillWindow = 64;  // (b, h) pairs per scheduling window
+constexpr int kPrefillWindow = 64;      // (b, h) pairs per scheduling window
+constexpr int kPrefillWindowLong = 32;  // ... for long rows and large batches (prefill_args)
 constexpr float kLazyLog2 = 8.0f;   // probabilities stay <= 2^8 between rescales
 
 // fp32 prefill on v_mfma_f32_32x32x2_f32 (dg_attn_mfma_f32.hip): D is 64 or
