@@ -25,6 +25,13 @@
 // splits, up to 16 splits of one (b, h, i) are the waves of one workgroup
 // and merge their unnormalised partials (acc, m, l) in LDS; more go to the
 // caller's workspace and attn_combine_kernel merges them.
+//
+// FUSED instances are the whole decode step of one new token (dg_decode_step,
+// mha.py:44-68): every wave rotates and normalises its q and the new k from
+// the projections, the wave whose split holds the position appends k and v
+// to the cache, and the new key enters the softmax from registers in the
+// trip slot where the two-launch form reads it back, so y has that form's
+// bits.
 #include "dg_rope_math.h"
 
 namespace dg {
