@@ -578,6 +578,7 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     # y is dg_decode_attention_at's over max_pos, not the two calls' bits
     (1, 1, 1, 0, 200, 16, 300),
     (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): the vector kernel's fused step
+    (1, 1, 2, 0, 4000, 64, 4100),     # 32 key splits: the fused step's partials through the workspace
 ]
 
 
