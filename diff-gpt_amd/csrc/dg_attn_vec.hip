@@ -72,9 +72,11 @@ struct AttnArgs {
 
 constexpr float kVecLazyLog2 = 8.0f;
 // Key splits of one (b, h, i) run as the waves of one workgroup and merge in
-// LDS when there are at most this many; more go through the workspace and
-// attn_combine_kernel.
+// LDS when there are at most this many (16, or 8 for rows padded to 1024,
+// whose (acc, m, l) partials would not fit 32 KB of LDS); more go through
+// the workspace and attn_combine_kernel.
 constexpr int kMaxBlockSplits = 16;
+constexpr int block_splits(int dpad) { return dpad * kMaxBlockSplits * 4 <= 32768 ? kMaxBlockSplits : 32768 / (dpad * 4); }
 
 // MERGE: the workgroup's nsplit waves are the key splits of one (b, h, i)
 // (blockDim = 64 * nsplit); otherwise a workgroup holds 4 independent units.
@@ -83,8 +85,10 @@ constexpr int kMaxBlockSplits = 16;
 // and value appended by the wave whose split holds the position, and the new
 // key taken from registers in the trip slot where the two-call form reads it
 // back from the cache, so y has the two calls' bits.
-template <typename T, int DPAD, int EPL, int U, bool MERGE, bool FUSED>
-__global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_kernel(const AttnArgs a) {
+// PAIRS: the lanes' slices are read and written pair by pair (load_slice),
+// pairs past D skipped.
+template <typename T, int DPAD, int EPL, int U, bool MERGE, bool FUSED, bool PAIRS>
+__global__ __launch_bounds__(MERGE ? 64 * block_splits(DPAD) : 256) void attn_vec_kernel(const AttnArgs a) {
   constexpr int LPK = DPAD / EPL;
   constexpr int KPI = 64 / LPK;
   constexpr int STEP = KPI * U;  // keys per trip
@@ -115,6 +119,7 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
   const int dl = active ? d0 : 0;  // inactive lanes (D not a power of two) read a valid slice
+  const int np = slice_pairs<EPL>(d0, a.D);  // PAIRS: pairs of the slice inside D
   int Tk = a.Tk, q_offset = a.q_offset, split_len = a.split_len;
   int pos = -1;         // fused: the new token's position
   bool pos_ok = false;  // fused: the position lies in the rows' own pages (a.Tk = max_pos)
@@ -138,16 +143,19 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
   Row knew, vnew;              // fused: the appended key and value
   float xq[EPL], xk[EPL], cs[EPL];  // fused: q and k before RoPE, the (cos, sin) pairs
   if constexpr (FUSED) {
-    load_vec<T, EPL>(static_cast<const T*>(a.q) + b * a.qb + (int64_t)h * a.qh + dl, xq);
-    load_vec<T, EPL>(static_cast<const T*>(a.kn) + b * a.knb + (int64_t)h * a.knh + dl, xk);
-    load_row<T, EPL>(vnew, static_cast<const T*>(a.vn) + b * a.vnb + (int64_t)h * a.vnh + dl);
+    load_vec_slice<T, EPL, PAIRS>(static_cast<const T*>(a.q) + b * a.qb + (int64_t)h * a.qh + dl, xq, np);
+    load_vec_slice<T, EPL, PAIRS>(static_cast<const T*>(a.kn) + b * a.knb + (int64_t)h * a.knh + dl, xk, np);
+    load_slice<T, EPL, PAIRS>(vnew, static_cast<const T*>(a.vn) + b * a.vnb + (int64_t)h * a.vnh + dl, np);
     // a position outside the pages writes nothing and reads table row 0
     // (its y is undefined, as in the two-launch form)
     const int64_t frow = pos_ok ? pos : 0;
-    if (a.f32freqs) load_vec<float, EPL>(static_cast<const float*>(a.freqs) + frow * a.fpos + dl, cs);
-    else load_vec<T, EPL>(static_cast<const T*>(a.freqs) + frow * a.fpos + dl, cs);
+    if (a.f32freqs)
+      load_vec_slice<float, EPL, PAIRS>(static_cast<const float*>(a.freqs) + frow * a.fpos + dl, cs, np);
+    else
+      load_vec_slice<T, EPL, PAIRS>(static_cast<const T*>(a.freqs) + frow * a.fpos + dl, cs, np);
   } else {
-    load_row<T, EPL>(qr, static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + dl);
+    load_slice<T, EPL, PAIRS>(qr, static_cast<const T*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh + dl,
+                              np);
     if (!active) {
 #pragma unroll
       for (int w = 0; w < Row::WORDS; ++w) qr.w[w] = 0u;  // contributes 0 to every dot
@@ -185,8 +193,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
       const T* vb = (pre ? vpre : vbase) + (int64_t)t0 * vt;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        load_row<T, EPL>(kr[u], kb + koff[u]);
-        load_row<T, EPL>(vr[u], vb + voff[u]);
+        load_slice<T, EPL, PAIRS>(kr[u], kb + koff[u], np);
+        load_slice<T, EPL, PAIRS>(vr[u], vb + voff[u], np);
       }
     } else {
       // trip straddling the end of the prefix or the end of the keys: slots
@@ -198,8 +206,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
         if (t0 + u * KPI >= kend) break;
         const int t = min(t0 + u * KPI + grp, kend - 1);
         const bool pre = t < P;
-        load_row<T, EPL>(kr[u], (pre ? kpre : kbase) + t * kt + dl);
-        load_row<T, EPL>(vr[u], (pre ? vpre : vbase) + t * vt + dl);
+        load_slice<T, EPL, PAIRS>(kr[u], (pre ? kpre : kbase) + t * kt + dl, np);
+        load_slice<T, EPL, PAIRS>(vr[u], (pre ? vpre : vbase) + t * vt + dl, np);
       }
     }
   };
@@ -274,8 +282,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
     pack_row<T, EPL>(qr, xq);
     pack_row<T, EPL>(knew, xk);
     if (pos_ok && pos >= kbeg && pos < kend && grp == 0 && active) {
-      store_row<T, EPL>(const_cast<T*>(kbase) + (int64_t)pos * kt + d0, knew);
-      store_row<T, EPL>(const_cast<T*>(vbase) + (int64_t)pos * vt + d0, vnew);
+      store_slice<T, EPL, PAIRS>(const_cast<T*>(kbase) + (int64_t)pos * kt + d0, knew, np);
+      store_slice<T, EPL, PAIRS>(const_cast<T*>(vbase) + (int64_t)pos * vt + d0, vnew, np);
     }
   }
   if (t0 < kend) {
@@ -301,8 +309,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
     // workgroup's threads take the output dims in pairs and merge the splits:
     // weights exp2((m_j - M) c) against the largest offset M, as the combine
     // kernel does.  Every wave reaches the barrier (no early exit above).
-    __shared__ float lds_acc[kMaxBlockSplits][DPAD];
-    __shared__ float lds_ml[kMaxBlockSplits][2];
+    __shared__ float lds_acc[block_splits(DPAD)][DPAD];
+    __shared__ float lds_ml[block_splits(DPAD)][2];
     if (grp == 0 && active) {
 #pragma unroll
       for (int e = 0; e < EPL; ++e) lds_acc[split][d0 + e] = acc[e];
@@ -337,8 +345,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
     const float inv = 1.0f / l;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] *= inv;
-    store_vec<T, EPL>(static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh + d0,
-                      acc);
+    store_vec_slice<T, EPL, PAIRS>(static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh + d0,
+                                   acc, np);
   } else {
     // workspace: acc of every unit ([units][DPAD] fp32), then its (m, l)
     store_vec<float, EPL>(a.part + (int64_t)unit * DPAD + d0, acc);
@@ -355,7 +363,8 @@ __global__ __launch_bounds__(MERGE ? 64 * kMaxBlockSplits : 256) void attn_vec_k
 // folds splits j, j + SP, ... into a running (m, l, acc) -- all its loads are
 // independent of one another, so a row's partials arrive in about one memory
 // latency -- and the SP slot states meet in LDS, where slot 0 merges them.
-template <typename T, int DPAD, int EPL>
+// PAIRS (y aligned to a pair only, D any even size): stored pair by pair.
+template <typename T, int DPAD, int EPL, bool PAIRS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, const int sp_shift) {
   constexpr int CW = DPAD < 4 ? DPAD : 4;
   constexpr int C = DPAD / CW;
@@ -426,11 +435,11 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, con
   const int64_t b = r / a.H;
   T* yp = static_cast<T*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh;
   const int d0 = cidx * CW;
-  if constexpr (EPL >= CW) {
+  if constexpr (EPL >= CW && !PAIRS) {
     // EPL-element alignment of y (host check) covers a CW-element store
     if (d0 < a.D) store_vec<T, CW>(yp + d0, acc);
   } else {
-    static_assert(EPL == 2 && CW == 4, "combine store width");
+    static_assert(CW == 4, "combine store width");
     // D is even here (2-element alignment); store the pairs inside D
     const float lo[2] = {acc[0], acc[1]}, hi[2] = {acc[2], acc[3]};
     if (d0 < a.D) store_vec<T, 2>(yp + d0, lo);
@@ -479,24 +488,26 @@ int pick_splits(int64_t base_units, int Tk) {
 // Key slots per trip: 2 with 16-byte lane slices, 4 with narrower ones (the
 // same bytes in flight per wave).  Two register sets of two slots keep the
 // kernel at 72 VGPRs.
+// Slices of 32 bytes or more (head dims past 256) take one slot per trip.
 template <typename T, int EPL>
 constexpr int slots_for() {
-  return EPL * (int)sizeof(T) >= 16 ? 2 : 4;
+  return EPL * (int)sizeof(T) >= 32 ? 1 : EPL * (int)sizeof(T) >= 16 ? 2 : 4;
 }
 
-template <typename T, int DPAD, int EPL, bool FUSED>
+template <typename T, int DPAD, int EPL, bool FUSED, bool PAIRS>
 int launch_attn(AttnArgs a, hipStream_t s) {
-  if (a.nsplit > 1 && a.nsplit <= kMaxBlockSplits) {
+  constexpr int U = slots_for<T, EPL>();
+  if (a.nsplit > 1 && a.nsplit <= block_splits(DPAD)) {
     // one workgroup per (b, h, i), one wave per key split, merged in LDS
     const int64_t blocks = a.units / a.nsplit;
     DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), true, FUSED>), dim3((unsigned)blocks),
+    hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, U, true, FUSED, PAIRS>), dim3((unsigned)blocks),
                        dim3(64 * a.nsplit), 0, s, a);
     return check_launch("attn_vec_kernel");
   }
   const int64_t blocks = (a.units + 3) / 4;
   DG_REQUIRE(blocks <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
-  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, slots_for<T, EPL>(), false, FUSED>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((attn_vec_kernel<T, DPAD, EPL, U, false, FUSED, PAIRS>), dim3((unsigned)blocks),
                      dim3(256), 0, s, a);
   int rc = check_launch("attn_vec_kernel");
   if (rc != DG_OK || a.nsplit == 1) return rc;
@@ -506,35 +517,38 @@ int launch_attn(AttnArgs a, hipStream_t s) {
   while ((1 << sp_shift) < a.nsplit && (C << (sp_shift + 1)) <= 256) ++sp_shift;
   const int64_t rows = a.units / a.nsplit;
   const int64_t rpb = 256 / (C << sp_shift);
-  hipLaunchKernelGGL((attn_combine_kernel<T, DPAD, EPL>), dim3((unsigned)((rows + rpb - 1) / rpb)),
+  hipLaunchKernelGGL((attn_combine_kernel<T, DPAD, EPL, PAIRS>), dim3((unsigned)((rows + rpb - 1) / rpb)),
                      dim3(256), 0, s, a, sp_shift);
   return check_launch("attn_combine_kernel");
 }
 
+// The kernel for a slice choice: vector slices (vec_slice_epl) or pair
+// slices (pair_slice_epl; read pair by pair past one pair per lane).
 template <typename T, int DPAD, bool FUSED>
-int attn_pick_epl(int epl, const AttnArgs& a, hipStream_t s) {
-  constexpr int PREF = (16 / (int)sizeof(T)) < DPAD ? (16 / (int)sizeof(T)) : DPAD;
-  if constexpr (PREF != 2) {
-    if (epl == PREF) return launch_attn<T, DPAD, PREF, FUSED>(a, s);
-  }
-  if constexpr (DPAD / 2 <= 64) {
-    if (epl == 2) return launch_attn<T, DPAD, 2, FUSED>(a, s);
-  }
+int attn_pick_epl(int epl, bool pairs, const AttnArgs& a, hipStream_t s) {
+  constexpr int es = (int)sizeof(T);
+  constexpr int VEC = ((16 / es) < DPAD ? (16 / es) : DPAD) > DPAD / 64 ? ((16 / es) < DPAD ? (16 / es) : DPAD)
+                                                                        : DPAD / 64;
+  constexpr int PAIR = DPAD / 64 > 2 ? DPAD / 64 : 2;
+  if (!pairs && epl == VEC) return launch_attn<T, DPAD, VEC, FUSED, false>(a, s);
+  if (pairs && epl == PAIR) return launch_attn<T, DPAD, PAIR, FUSED, (PAIR > 2)>(a, s);
   set_error("attention: no kernel for D pad %d with %d elements per lane", DPAD, epl);
   return DG_EUNSUPPORTED;
 }
 
 template <typename T, bool FUSED = false>
-int attn_pick_d(int dpad, int epl, const AttnArgs& a, hipStream_t s) {
+int attn_pick_d(int dpad, int epl, bool pairs, const AttnArgs& a, hipStream_t s) {
   switch (dpad) {
-    case 2: return attn_pick_epl<T, 2, FUSED>(epl, a, s);
-    case 4: return attn_pick_epl<T, 4, FUSED>(epl, a, s);
-    case 8: return attn_pick_epl<T, 8, FUSED>(epl, a, s);
-    case 16: return attn_pick_epl<T, 16, FUSED>(epl, a, s);
-    case 32: return attn_pick_epl<T, 32, FUSED>(epl, a, s);
-    case 64: return attn_pick_epl<T, 64, FUSED>(epl, a, s);
-    case 128: return attn_pick_epl<T, 128, FUSED>(epl, a, s);
-    case 256: return attn_pick_epl<T, 256, FUSED>(epl, a, s);
+    case 2: return attn_pick_epl<T, 2, FUSED>(epl, pairs, a, s);
+    case 4: return attn_pick_epl<T, 4, FUSED>(epl, pairs, a, s);
+    case 8: return attn_pick_epl<T, 8, FUSED>(epl, pairs, a, s);
+    case 16: return attn_pick_epl<T, 16, FUSED>(epl, pairs, a, s);
+    case 32: return attn_pick_epl<T, 32, FUSED>(epl, pairs, a, s);
+    case 64: return attn_pick_epl<T, 64, FUSED>(epl, pairs, a, s);
+    case 128: return attn_pick_epl<T, 128, FUSED>(epl, pairs, a, s);
+    case 256: return attn_pick_epl<T, 256, FUSED>(epl, pairs, a, s);
+    case 512: return attn_pick_epl<T, 512, FUSED>(epl, pairs, a, s);
+    case 1024: return attn_pick_epl<T, 1024, FUSED>(epl, pairs, a, s);
   }
   set_error("attention: head_dim %d unsupported", a.D);
   return DG_EUNSUPPORTED;
@@ -551,7 +565,7 @@ int vec_attention_splits(int B, int H, int Tq, int Tk, int D) {
 
 size_t vec_attention_workspace(int B, int H, int Tq, int Tk, int D) {
   const int ns = vec_attention_splits(B, H, Tq, Tk, D);
-  if (ns <= kMaxBlockSplits) return 0;  // merged inside the workgroup
+  if (ns <= block_splits(next_pow2(D))) return 0;  // merged inside the workgroup
   return (size_t)B * H * Tq * ns * (size_t)(next_pow2(D) + 2) * sizeof(float);
 }
 
@@ -581,37 +595,42 @@ int vec_launch(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, co
   // the same way and give the same bits
   const int es = dtype == DG_F32 ? 4 : 2;
   const int dpad = next_pow2(D);
-  DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "attention: head_dim %d > 256", D);
+  DG_REQUIRE(D <= kMaxHeadDim, DG_EUNSUPPORTED, "attention: head_dim %d > %d", D, kMaxHeadDim);
   DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
   // row offsets inside one (b, h) page are 32-bit in the kernel
   const int64_t span_k = (int64_t)Tk * (k_st->t < 0 ? -k_st->t : k_st->t);
   const int64_t span_v = (int64_t)Tk * (v_st->t < 0 ? -v_st->t : v_st->t);
   DG_REQUIRE(span_k < ((int64_t)1 << 31) && span_v < ((int64_t)1 << 31) && k_st->t >= 0 && v_st->t >= 0,
              DG_EINVAL, "attention: Tk * key/value row stride must be below 2^31 elements");
-  int pref = 16 / es;
-  if (pref > dpad) pref = dpad;
-  auto fits = [&](int epl) {
-    if (epl != 2 && dpad != D) return false;
-    if (dpad / epl > 64) return false;
-    const int64_t bytes = (int64_t)epl * es;
-    const bool pre_ok = pre.len == 0 || (aligned(pre.k, bytes) && aligned(pre.v, bytes) && pre.kb % epl == 0 &&
-                                         pre.kh % epl == 0 && pre.vb % epl == 0 && pre.vh % epl == 0);
+  // vector slices where D is a multiple of them and every operand is aligned
+  // to a load; else pair slices (each operand aligned to a pair)
+  auto fits = [&](int epl, bool pairs) {
+    if (!pairs && D % epl != 0) return false;
+    const int w = pairs ? 2 : slice_load_elems(epl, es);  // elements per access
+    const int64_t bytes = (int64_t)w * es;
+    const bool pre_ok = pre.len == 0 || (aligned(pre.k, bytes) && aligned(pre.v, bytes) && pre.kb % w == 0 &&
+                                         pre.kh % w == 0 && pre.vb % w == 0 && pre.vh % w == 0);
     bool step_ok = true;
     if (step != nullptr) {
       // the table row's slice of a lane: epl elements of the table's dtype
       const int64_t fes = step->fdtype == DG_F32 ? 4 : 2;
-      const int64_t fbytes = epl * fes < 16 ? epl * fes : 16;
-      step_ok = aligned(step->kn, bytes) && aligned(step->vn, bytes) && step->kn_st->b % epl == 0 &&
-                step->kn_st->h % epl == 0 && step->vn_st->b % epl == 0 && step->vn_st->h % epl == 0 &&
+      const int64_t fbytes = pairs ? 2 * fes : (epl * fes < 16 ? epl * fes : 16);
+      step_ok = aligned(step->kn, bytes) && aligned(step->vn, bytes) && step->kn_st->b % w == 0 &&
+                step->kn_st->h % w == 0 && step->vn_st->b % w == 0 && step->vn_st->h % w == 0 &&
                 aligned(step->freqs, fbytes) && (step->fpos * fes) % fbytes == 0;
     }
     return aligned(q, bytes) && aligned(k, bytes) && aligned(v, bytes) && aligned(y, bytes) &&
-           strides_multiple(q_st, epl) && strides_multiple(k_st, epl) &&
-           strides_multiple(v_st, epl) && strides_multiple(y_st, epl) && pre_ok && step_ok;
+           strides_multiple(q_st, w) && strides_multiple(k_st, w) &&
+           strides_multiple(v_st, w) && strides_multiple(y_st, w) && pre_ok && step_ok;
   };
   int epl = 0;
-  if (fits(pref)) epl = pref;
-  else if (fits(2)) epl = 2;
+  bool pairs = false;
+  if (fits(vec_slice_epl(dpad, es), false)) {
+    epl = vec_slice_epl(dpad, es);
+  } else if (fits(pair_slice_epl(dpad), true)) {
+    epl = pair_slice_epl(dpad);
+    pairs = true;
+  }
   if (epl == 0 && step != nullptr) {
     *declined = true;
     return DG_OK;
@@ -643,27 +662,28 @@ int vec_launch(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, co
   DG_REQUIRE(size_keys >= Tk, DG_EINVAL, "attention: split sizing for %d keys below Tk = %d", size_keys, Tk);
   int ns = vec_attention_splits(B, H, Tq, size_keys, D);
   const size_t need = vec_attention_workspace(B, H, Tq, size_keys, D);
-  if (ns > kMaxBlockSplits && (workspace == nullptr || workspace_bytes < need)) {
+  const int in_block = block_splits(dpad);
+  if (ns > in_block && (workspace == nullptr || workspace_bytes < need)) {
     DG_REQUIRE(workspace == nullptr, DG_EWORKSPACE,
                "attention: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
-    ns = kMaxBlockSplits;  // no workspace: as many splits as one workgroup merges
+    ns = in_block;  // no workspace: as many splits as one workgroup merges
   }
   a.nsplit = ns;
   a.split_len = ns == 1 ? Tk : (((Tk + ns - 1) / ns + 15) / 16) * 16;
-  const bool global_splits = ns > kMaxBlockSplits;
+  const bool global_splits = ns > in_block;
   a.part = global_splits ? static_cast<float*>(workspace) : nullptr;
   DG_REQUIRE(!global_splits || aligned(workspace, 16), DG_EINVAL, "attention: workspace must be 16-byte aligned");
   a.units = (int64_t)B * H * Tq * ns;
   DG_REQUIRE(a.units < ((int64_t)1 << 31), DG_EINVAL, "attention: B*H*Tq*splits must be below 2^31");
 
   if (step != nullptr) {
-    if (dtype == DG_F32) return attn_pick_d<float, true>(dpad, epl, a, s);
-    if (dtype == DG_BF16) return attn_pick_d<bf16_t, true>(dpad, epl, a, s);
-    return attn_pick_d<f16_t, true>(dpad, epl, a, s);
+    if (dtype == DG_F32) return attn_pick_d<float, true>(dpad, epl, pairs, a, s);
+    if (dtype == DG_BF16) return attn_pick_d<bf16_t, true>(dpad, epl, pairs, a, s);
+    return attn_pick_d<f16_t, true>(dpad, epl, pairs, a, s);
   }
-  if (dtype == DG_F32) return attn_pick_d<float>(dpad, epl, a, s);
-  if (dtype == DG_BF16) return attn_pick_d<bf16_t>(dpad, epl, a, s);
-  return attn_pick_d<f16_t>(dpad, epl, a, s);
+  if (dtype == DG_F32) return attn_pick_d<float>(dpad, epl, pairs, a, s);
+  if (dtype == DG_BF16) return attn_pick_d<bf16_t>(dpad, epl, pairs, a, s);
+  return attn_pick_d<f16_t>(dpad, epl, pairs, a, s);
 }
 
 }  // namespace

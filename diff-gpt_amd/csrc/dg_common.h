@@ -331,6 +331,85 @@ __device__ __forceinline__ void store_row(T* p, const RowRegs<T, EPL>& r) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Slice access by (re, im) pairs, for head dims whose lane slices cannot all
+// be whole vectors: the slice may run past the end of the row (D not a
+// multiple of EPL) or its operands may be aligned to a pair only.  The first
+// npairs pairs are read or written, one 4-byte (16-bit T) or 8-byte (fp32)
+// access each; the rest of the slice reads as zeros and is not written.
+// With PAIRS false the whole slice goes by vectors and npairs is unused.
+// ---------------------------------------------------------------------------
+template <typename T, int EPL, bool PAIRS>
+__device__ __forceinline__ void load_slice(RowRegs<T, EPL>& r, const T* p, int npairs) {
+  if constexpr (!PAIRS) {
+    load_row<T, EPL>(r, p);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) {
+      if constexpr (sizeof(T) == 4) {
+        u32x2_t x = {0u, 0u};
+        if (j < npairs) x = *reinterpret_cast<const u32x2_t*>(p + 2 * j);
+        r.w[2 * j] = x[0];
+        r.w[2 * j + 1] = x[1];
+      } else {
+        r.w[j] = j < npairs ? *reinterpret_cast<const uint32_t*>(p + 2 * j) : 0u;
+      }
+    }
+  }
+}
+
+template <typename T, int EPL, bool PAIRS>
+__device__ __forceinline__ void store_slice(T* p, const RowRegs<T, EPL>& r, int npairs) {
+  if constexpr (!PAIRS) {
+    store_row<T, EPL>(p, r);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) {
+      if (j >= npairs) break;
+      if constexpr (sizeof(T) == 4)
+        *reinterpret_cast<u32x2_t*>(p + 2 * j) = u32x2_t{r.w[2 * j], r.w[2 * j + 1]};
+      else
+        *reinterpret_cast<uint32_t*>(p + 2 * j) = r.w[j];
+    }
+  }
+}
+
+template <typename T, int EPL, bool PAIRS>
+__device__ __forceinline__ void load_vec_slice(const T* p, float (&out)[EPL], int npairs) {
+  if constexpr (!PAIRS) {
+    load_vec<T, EPL>(p, out);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) {
+      float v[2] = {0.f, 0.f};
+      if (j < npairs) load_vec<T, 2>(p + 2 * j, v);
+      out[2 * j] = v[0];
+      out[2 * j + 1] = v[1];
+    }
+  }
+}
+
+template <typename T, int EPL, bool PAIRS>
+__device__ __forceinline__ void store_vec_slice(T* p, const float (&in)[EPL], int npairs) {
+  if constexpr (!PAIRS) {
+    store_vec<T, EPL>(p, in);
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPL / 2; ++j) {
+      if (j >= npairs) break;
+      const float v[2] = {in[2 * j], in[2 * j + 1]};
+      store_vec<T, 2>(p + 2 * j, v);
+    }
+  }
+}
+
+// Pairs of the slice starting at element d0 that lie inside a row of D.
+template <int EPL>
+__device__ __forceinline__ int slice_pairs(int d0, int D) {
+  const int n = (D - d0) >> 1;
+  return n < 0 ? 0 : (n < EPL / 2 ? n : EPL / 2);
+}
+
 // Element e of the slice as fp32.
 template <typename T, int EPL>
 __device__ __forceinline__ float elem(const RowRegs<T, EPL>& r, int e) {
@@ -449,6 +528,24 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
 namespace dg {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+
+// Lane slices of a row of D elements of es bytes (the RoPE and vector
+// attention kernels): the row padded to DPAD = the next power of two spreads
+// over LPK = DPAD / EPL <= 64 lanes, EPL elements each.  Vector slices are
+// max(16 bytes, DPAD / 64) elements read by 16-byte loads (4 or 8 bytes for
+// rows that short); they need D to be a multiple of EPL and every operand
+// aligned to a load.  Pair slices, max(2, DPAD / 64) elements, need only
+// pair alignment: one pair per lane up to DPAD = 128, beyond that read pair
+// by pair (load_slice with PAIRS).
+constexpr int kMaxHeadDim = 1024;
+inline int vec_slice_epl(int dpad, int es) {
+  int e = 16 / es;
+  if (e > dpad) e = dpad;
+  return dpad / 64 > e ? dpad / 64 : e;
+}
+inline int pair_slice_epl(int dpad) { return dpad / 64 > 2 ? dpad / 64 : 2; }
+// Elements per load of a slice of epl elements: the operands' alignment unit.
+inline int slice_load_elems(int epl, int es) { return epl * es > 16 ? 16 / es : epl; }
 
 // A shared prefix (dg_prefix) as the kernels read it: keys t < len of row b
 // at k + (b / group) * kb + t * (the cache's t stride) + h * kh (likewise v).

@@ -20,11 +20,12 @@
 #include <mutex>
 
 // Largest key-split workspace of a decode step: up to 16 splits merge inside
-// the workgroup and need none; more happen only while B*H < 256 (they aim at
-// 4096 waves), so B*H*splits < 4096 + 255 partials of at most 256 + 2
-// floats: < 4.5 MB for any head_dim the library takes.  The check below
+// the workgroup and need none (8 for head dims past 512); more happen only
+// while B*H < 256 (512) -- they aim at 4096 waves -- so B*H*splits is below
+// 4096 + 256 (4096 + 512) partials of at most 512 + 2 (1024 + 2) floats:
+// < 9 MB (< 19 MB) for any head_dim the library takes.  The check below
 // stays as a guard.
-constexpr size_t kStaticScratchBytes = size_t(8) << 20;
+constexpr size_t kStaticScratchBytes = size_t(20) << 20;
 
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 

@@ -49,7 +49,9 @@ struct RopeArgs {
 // rows), and issues every load of them before any arithmetic: RPT times the
 // bytes in flight per wave, which a single row per lane leaves too few of to
 // keep HBM busy.  Each row's arithmetic is the same whatever RPT is.
-template <typename T, typename FT, int DPAD, int EPL, int RPT>
+// PAIRS: slices read and written pair by pair, pairs past D skipped (head
+// dims past 128 whose slices are not whole vectors).
+template <typename T, typename FT, int DPAD, int EPL, int RPT, bool PAIRS>
 __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPK = DPAD / EPL;
@@ -66,6 +68,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
   }
   const int d0 = sub * EPL;
   const bool active = d0 < a.D;
+  const int np = slice_pairs<EPL>(d0, a.D);  // PAIRS: pairs of the slice inside D
 
   // all sources of all RPT rows are read before anything is stored: the
   // destinations may alias them as far as the compiler knows, so this order
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
     if (active && live[j]) {
       const FT* f = static_cast<const FT*>(a.freqs) + pos * a.fpos + off_b[j] * a.fb + (int64_t)off_t[j] * a.ft +
                     (int64_t)off_h[j] * a.fh + d0;
-      load_row<FT, EPL>(cr[j], f);
+      load_slice<FT, EPL, PAIRS>(cr[j], f, np);
     }
 #pragma unroll
     for (int w = 0; w < 3; ++w) {
@@ -99,7 +102,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
       if (a.src[w] == nullptr || !active || !live[j]) continue;  // src: uniform over the grid
       const T* sp = static_cast<const T*>(a.src[w]) + off_b[j] * a.sb[w] + (int64_t)off_t[j] * a.st[w] +
                     (int64_t)off_h[j] * a.sh[w] + d0;
-      load_row<T, EPL>(xr[w][j], sp);
+      load_slice<T, EPL, PAIRS>(xr[w][j], sp, np);
     }
   }
 
@@ -121,7 +124,7 @@ __global__ __launch_bounds__(256) void rope_qknorm_kernel(const RopeArgs a) {
       if (active && live[j]) {
         T* d = static_cast<T*>(a.dst[w]) + pos * a.pstep[w] + off_b[j] * a.db[w] + (int64_t)off_t[j] * a.dt[w] +
                (int64_t)off_h[j] * a.dh[w] + d0;
-        store_vec<T, EPL>(d, x);
+        store_vec_slice<T, EPL, PAIRS>(d, x, np);
       }
     }
   }
@@ -202,46 +205,52 @@ int next_pow2(int x) {
 constexpr int kRopeRowsPerGroup = 4;
 constexpr int64_t kRopeMinBlocks = 2048;
 
-template <typename T, typename FT, int DPAD, int EPL>
+template <typename T, typename FT, int DPAD, int EPL, bool PAIRS>
 int launch_rope(const RopeArgs& a, hipStream_t s) {
   constexpr int LPK = DPAD / EPL;
   constexpr int RPB = 256 / LPK;
   DG_REQUIRE(a.rows < 0x7fffffffLL, DG_EINVAL, "rope: B*T*H = %lld rows, at most 2^31 - 1", (long long)a.rows);
-  constexpr int R = kRopeRowsPerGroup;
-  if (a.rows >= kRopeMinBlocks * RPB * R) {
+  // slices past 16 bytes hold enough bytes in flight with one row per group
+  constexpr int R = EPL * (int)sizeof(T) > 16 ? 1 : kRopeRowsPerGroup;
+  if (R > 1 && a.rows >= kRopeMinBlocks * RPB * R) {
     const int64_t blocks = (a.rows + RPB * R - 1) / (RPB * R);
-    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, R>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, R, PAIRS>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       a);
   } else {
     const int64_t blocks = (a.rows + RPB - 1) / RPB;
-    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, 1>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((rope_qknorm_kernel<T, FT, DPAD, EPL, 1, PAIRS>), dim3((unsigned)blocks), dim3(256), 0, s,
+                       a);
   }
   return check_launch("rope_qknorm_kernel");
 }
 
+// The kernel for a slice choice: vector slices (vec_slice_epl) or pair
+// slices (pair_slice_epl; read pair by pair past one pair per lane).
 template <typename T, typename FT, int DPAD>
-int rope_pick_epl(int epl, const RopeArgs& a, hipStream_t s) {
-  constexpr int PREF = (16 / (int)sizeof(T)) < DPAD ? (16 / (int)sizeof(T)) : DPAD;
-  if constexpr (PREF != 2) {
-    if (epl == PREF) return launch_rope<T, FT, DPAD, PREF>(a, s);
-  }
-  if constexpr (DPAD / 2 <= 64) {
-    if (epl == 2) return launch_rope<T, FT, DPAD, 2>(a, s);
-  }
+int rope_pick_epl(int epl, bool pairs, const RopeArgs& a, hipStream_t s) {
+  constexpr int es = (int)sizeof(T);
+  constexpr int PREF = (16 / es) < DPAD ? (16 / es) : DPAD;
+  constexpr int VEC = PREF > DPAD / 64 ? PREF : DPAD / 64;
+  constexpr int PAIR = DPAD / 64 > 2 ? DPAD / 64 : 2;
+  if (!pairs && epl == VEC) return launch_rope<T, FT, DPAD, VEC, false>(a, s);
+  if (pairs && epl == PAIR) return launch_rope<T, FT, DPAD, PAIR, (PAIR > 2)>(a, s);
   set_error("rope: no kernel for D pad %d with %d elements per lane", DPAD, epl);
   return DG_EUNSUPPORTED;
 }
 
 template <typename T, typename FT>
-int rope_pick_d(int dpad, int epl, const RopeArgs& a, hipStream_t s) {
+int rope_pick_d(int dpad, int epl, bool pairs, const RopeArgs& a, hipStream_t s) {
   switch (dpad) {
-    case 2: return rope_pick_epl<T, FT, 2>(epl, a, s);
-    case 4: return rope_pick_epl<T, FT, 4>(epl, a, s);
-    case 8: return rope_pick_epl<T, FT, 8>(epl, a, s);
-    case 16: return rope_pick_epl<T, FT, 16>(epl, a, s);
-    case 32: return rope_pick_epl<T, FT, 32>(epl, a, s);
-    case 64: return rope_pick_epl<T, FT, 64>(epl, a, s);
-    case 128: return rope_pick_epl<T, FT, 128>(epl, a, s);
-    case 256: return rope_pick_epl<T, FT, 256>(epl, a, s);
+    case 2: return rope_pick_epl<T, FT, 2>(epl, pairs, a, s);
+    case 4: return rope_pick_epl<T, FT, 4>(epl, pairs, a, s);
+    case 8: return rope_pick_epl<T, FT, 8>(epl, pairs, a, s);
+    case 16: return rope_pick_epl<T, FT, 16>(epl, pairs, a, s);
+    case 32: return rope_pick_epl<T, FT, 32>(epl, pairs, a, s);
+    case 64: return rope_pick_epl<T, FT, 64>(epl, pairs, a, s);
+    case 128: return rope_pick_epl<T, FT, 128>(epl, pairs, a, s);
+    case 256: return rope_pick_epl<T, FT, 256>(epl, pairs, a, s);
+    case 512: return rope_pick_epl<T, FT, 512>(epl, pairs, a, s);
+    case 1024: return rope_pick_epl<T, FT, 1024>(epl, pairs, a, s);
   }
   set_error("rope: head_dim %d unsupported", a.D);
   return DG_EUNSUPPORTED;
@@ -331,30 +340,35 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
   const int es = elem_size(dtype);
   const int fes = elem_size(freqs_dtype);
   const int dpad = next_pow2(D);
-  DG_REQUIRE(dpad <= 256, DG_EUNSUPPORTED, "rope: head_dim %d > 256", D);
+  DG_REQUIRE(D <= kMaxHeadDim, DG_EUNSUPPORTED, "rope: head_dim %d > %d", D, kMaxHeadDim);
 
-  // Preferred vector width: 16 bytes of data per lane when D is a power of two
-  // and every pointer / stride allows it; otherwise one (re, im) pair per lane.
-  int pref = 16 / es;
-  if (pref > dpad) pref = dpad;
-  auto fits = [&](int epl) {
-    if (epl != 2 && dpad != D) return false;
-    if (dpad / epl > 64) return false;
-    for (int w = 0; w < 3; ++w) {
-      if (!src[w]) continue;
-      if (!aligned(src[w], (int64_t)epl * es) || !aligned(dst[w], (int64_t)epl * es)) return false;
-      if (!strides_multiple(sst[w], epl) || !strides_multiple(dst_st[w], epl)) return false;
-      if (pstep[w] % epl != 0) return false;
+  // Vector slices (16 bytes of data per lane, or the whole row when it is
+  // shorter) where D is a multiple of them and every pointer / stride
+  // allows it; otherwise pair slices.
+  auto fits = [&](int epl, bool pairs) {
+    if (!pairs && D % epl != 0) return false;
+    const int w = pairs ? 2 : slice_load_elems(epl, es);        // data elements per access
+    const int wf = pairs ? 2 : slice_load_elems(epl, fes);      // table elements per access
+    for (int i = 0; i < 3; ++i) {
+      if (!src[i]) continue;
+      if (!aligned(src[i], (int64_t)w * es) || !aligned(dst[i], (int64_t)w * es)) return false;
+      if (!strides_multiple(sst[i], w) || !strides_multiple(dst_st[i], w)) return false;
+      if (pstep[i] % w != 0) return false;
     }
     if (need_freqs) {
-      if (!aligned(freqs, (int64_t)epl * fes) || !strides_multiple(f_st, epl)) return false;
-      if (fpos % epl != 0) return false;
+      if (!aligned(freqs, (int64_t)wf * fes) || !strides_multiple(f_st, wf)) return false;
+      if (fpos % wf != 0) return false;
     }
     return true;
   };
   int epl = 0;
-  if (fits(pref)) epl = pref;
-  else if (fits(2)) epl = 2;
+  bool pairs = false;
+  if (fits(vec_slice_epl(dpad, es), false)) {
+    epl = vec_slice_epl(dpad, es);
+  } else if (fits(pair_slice_epl(dpad), true)) {
+    epl = pair_slice_epl(dpad);
+    pairs = true;
+  }
   DG_REQUIRE(epl != 0, DG_EINVAL,
              "rope: pointers/strides not aligned to an element pair (D=%d); pass contiguous rows", D);
 
@@ -381,13 +395,13 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
   a.fpos = fpos;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  if (dtype == DG_F32) return rope_pick_d<float, float>(dpad, epl, a, s);
+  if (dtype == DG_F32) return rope_pick_d<float, float>(dpad, epl, pairs, a, s);
   if (dtype == DG_BF16) {
-    if (freqs_dtype == DG_F32) return rope_pick_d<bf16_t, float>(dpad, epl, a, s);
-    return rope_pick_d<bf16_t, bf16_t>(dpad, epl, a, s);
+    if (freqs_dtype == DG_F32) return rope_pick_d<bf16_t, float>(dpad, epl, pairs, a, s);
+    return rope_pick_d<bf16_t, bf16_t>(dpad, epl, pairs, a, s);
   }
-  if (freqs_dtype == DG_F32) return rope_pick_d<f16_t, float>(dpad, epl, a, s);
-  return rope_pick_d<f16_t, f16_t>(dpad, epl, a, s);
+  if (freqs_dtype == DG_F32) return rope_pick_d<f16_t, float>(dpad, epl, pairs, a, s);
+  return rope_pick_d<f16_t, f16_t>(dpad, epl, pairs, a, s);
 }
 
 }  // namespace

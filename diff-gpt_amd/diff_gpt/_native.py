@@ -187,18 +187,14 @@ _SIGNATURES = {
 
 ABI_VERSION = 2
 
-# head_dim the kernels take: even sizes, up to 256 for powers of two and up to
-# 128 for others (those run with one (re, im) pair per lane, at most 64 lanes
-# per row)
-MAX_HEAD_DIM = 256
-MAX_HEAD_DIM_NON_POW2 = 128
+# head_dim the kernels take: every even size up to 1024 (a row padded to the
+# next power of two spreads over at most 64 lanes of 16 elements)
+MAX_HEAD_DIM = 1024
 
 
 def head_dim_supported(D: int) -> bool:
     """Whether every kernel of the attention path takes this head_dim."""
-    if D <= 0 or D % 2:
-        return False
-    return D <= (MAX_HEAD_DIM if D & (D - 1) == 0 else MAX_HEAD_DIM_NON_POW2)
+    return 2 <= D <= MAX_HEAD_DIM and D % 2 == 0
 
 
 def lib() -> ctypes.CDLL:

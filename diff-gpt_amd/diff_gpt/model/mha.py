@@ -59,8 +59,7 @@ class MultiHeadAttention(nn.Module):
         if not _native.head_dim_supported(self.head_dim):
             raise ValueError(
                 f"head_dim {self.head_dim} (n_embd {n_embd} / n_head {n_head}) is beyond the HIP attention "
-                f"kernels, which take even head dims up to {_native.MAX_HEAD_DIM} (powers of two) or "
-                f"{_native.MAX_HEAD_DIM_NON_POW2} (other sizes)"
+                f"kernels, which take even head dims up to {_native.MAX_HEAD_DIM}"
             )
         inner = self.n_head * self.head_dim
         # creation order fixes the parameter initialisation order (seeded RNG)

@@ -93,7 +93,9 @@ DG_API const char* dg_last_error(void);
  * broadcast dims -- and the D/2 pairs of a row are contiguous.  Pass k_out /
  * v_out as the cache page at position `pos` (e.g. &cache[l,0,0,0,pos,0] with
  * cache strides) to append.  Output dtype = input dtype (rope.py:27 type_as).
- * Supported: D even, D <= 256 (powers of two) or D <= 128 (other even D).
+ * Supported: every even D up to 1024.  Rows aligned to 16 bytes (and D a
+ * multiple of max(16 bytes, D's next power of two / 64) elements) go by
+ * 16-byte accesses; other rows need alignment to an element pair.
  */
 DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
                           const void* q, const dg_stride3* q_st,
@@ -115,14 +117,15 @@ DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
  * scale is the SDPA scale (the reference uses the default 1/sqrt(D)).
  * Prefills (Tq >= 16) at D = 64 or 128 with 16-byte aligned rows run on the
  * matrix cores: bf16 / fp16 products with fp32 accumulation, fp32 inputs on
- * fp32 products and accumulation; other shapes on the vector kernel.
+ * fp32 products and accumulation; other shapes on the vector kernel, which
+ * takes every even D up to 1024 (alignment as for dg_rope_qknorm_append).
  *
  * workspace: split-KV partials; dg_attention_workspace_size() gives the bytes
  * needed for these sizes: 0 unless a single-token decode splits the keys of
- * a (b, h) over more than 16 workgroups' waves (B*H < 256 with long rows;
- * up to 16 splits merge inside one workgroup and need none).  With
- * workspace == NULL such a launch uses 16 splits merged in the workgroup
- * (always correct, slower for very few long rows).
+ * a (b, h) over more than 16 waves of one workgroup (8 for D > 512; B*H <
+ * 256 with long rows; those merge inside the workgroup and need none).  With
+ * workspace == NULL such a launch uses as many splits as one workgroup
+ * merges (always correct, slower for very few long rows).
  */
 DG_API size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int D, int dtype);
 
@@ -309,9 +312,9 @@ DG_API int dg_decode_step(int B, int H, int D, int dtype,
  * under HIP graph capture that must not allocate, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
  * dg_decode_step; the key-split partials live in a static device array of
- * dg_decode_step_noalloc_scratch_bytes() bytes (8 MiB) that the library
+ * dg_decode_step_noalloc_scratch_bytes() bytes (20 MiB) that the library
  * holds on every GPU it runs on until the process ends.  Every size fits:
- * the split workspace (dg_decode_step_workspace_size) is at most 4.5 MB; a
+ * the split workspace (dg_decode_step_workspace_size) is at most 19 MB; a
  * size beyond the array would return DG_EWORKSPACE before any GPU work.
  * It allocates nothing and frees nothing.  All calls on one GPU share that array: calls that
  * overlap on one GPU (other streams, other host threads) race and must be

@@ -579,6 +579,12 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (1, 1, 1, 0, 200, 16, 300),
     (12, 6, 8, 600, 700, 64, 720),    # small groups, D = 64 (key splits): the vector kernel's fused step
     (1, 1, 2, 0, 4000, 64, 4100),     # 32 key splits: the fused step's partials through the workspace
+    # head dims past 128: vector slices (512), pair slices (300, 1000),
+    # a shared prefix at D = 384, the workspace at D = 1000
+    (2, 1, 2, 0, 300, 512, 320),
+    (3, 1, 2, 0, 100, 300, 130),
+    (4, 2, 2, 50, 120, 384, 140),
+    (1, 1, 2, 0, 3000, 1000, 3100),
 ]
 
 
@@ -650,7 +656,8 @@ def test_decode_step_matches_two_calls(dev, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(6, 1, 4, 0, 23, 16, 40), (3, 1, 2, 0, 70, 64, 100), (2, 1, 2, 0, 600, 128, 700)],
+@pytest.mark.parametrize("shape", [(6, 1, 4, 0, 23, 16, 40), (3, 1, 2, 0, 70, 64, 100), (2, 1, 2, 0, 600, 128, 700),
+                                   (2, 1, 2, 0, 300, 512, 320), (1, 1, 1, 0, 900, 1000, 1000)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_decode_step_ignores_old_contents_at_the_position(dev, dtype, shape):
     """The fused decode step appends the new key and value while it streams
@@ -706,6 +713,107 @@ def test_decode_step_random_shapes(dev, dtype, shape):
     """Seeded random (rows, group, heads, prefix, position, head_dim, capacity)
     through the same checks as the fixed decode-step cases."""
     test_decode_step_matches_two_calls(dev, dtype, shape)
+
+
+# ------------------------------------------------------------------ wide and odd head dims
+
+# Every even head_dim up to 1024 runs on the RoPE and vector attention
+# kernels.  A row padded to the next power of two spreads over at most 64
+# lanes: vector slices of max(16 bytes, DPAD / 64) elements where D is a
+# multiple of them and the operands are aligned to a load (96, 192, 384, 512,
+# 1024 here), else pair slices read pair by pair with the pairs past D skipped
+# (130, 300 and 1000 here; any D past 128 whose operands are aligned to a
+# pair only).
+WIDE_D = [96, 130, 192, 300, 384, 512, 1000, 1024]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("D", WIDE_D)
+def test_rope_qknorm_append_wide_head_dims(dev, dtype, D):
+    """RoPE + QK-norm + append at head dims past 128: q and k bit-exact
+    against the oracle (the norm's pairwise tree over the padded row is the
+    same whatever the slice width), v copied, the rest of the cache
+    untouched."""
+    _rope_append_case(dev, dtype, 2, 5, 3, D, 7, 16)
+
+
+def _misaligned(t: torch.Tensor) -> torch.Tensor:
+    """t's values in a view one pair into rows of D + 2 elements: aligned to
+    a pair, not to a 16-byte load, row strides not multiples of 4."""
+    buf = torch.zeros((*t.shape[:-1], t.shape[-1] + 2), dtype=t.dtype, device=t.device)
+    view = buf[..., 2:]
+    view.copy_(t)
+    return view
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("D", [256, 512, 1024])
+def test_rope_pair_slices_on_misaligned_rows(dev, dtype, D):
+    """q, k and v as views aligned to a pair only: the kernel reads and
+    writes its slices pair by pair, with the vector path's bits."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, T, H, pos, cap = 2, 4, 3, 5, 12
+    q = _randn((B, T, H, D), 11 + D, dtype, 2.0)
+    k = _randn((B, T, H, D), 21 + D, dtype, 2.0)
+    v = _randn((B, T, H, D), 31 + D, dtype)
+    fc = precompute_freqs_cis(D, 64, 10000).to(TDT[dtype])[pos:pos + T].view(1, T, 1, D // 2, 2)
+    qd, kd, vd = (_misaligned(t.to(dev)) for t in (q, k, v))
+    cd = torch.zeros((2, B, H, cap, D), dtype=TDT[dtype], device=dev)
+    q_out = _misaligned(torch.zeros_like(q).to(dev))
+    _native.ops().rope_qknorm_append(qd, kd, vd, fc.to(dev), q_out, cd[0, :, :, pos:pos + T].transpose(1, 2),
+                                     cd[1, :, :, pos:pos + T].transpose(1, 2), True)
+    torch.cuda.synchronize()
+    fcn = fc.float().numpy()
+    got = cd.cpu()
+    assert np.array_equal(_bits(q_out), on.rope_qknorm(q.float().numpy(), fcn, dtype).view(np.uint32))
+    assert np.array_equal(_bits(got[0, :, :, pos:pos + T].transpose(1, 2)),
+                          on.rope_qknorm(k.float().numpy(), fcn, dtype).view(np.uint32))
+    assert torch.equal(got[1, :, :, pos:pos + T].transpose(1, 2), v)
+    assert (got[:, :, :, :pos] == 0).all() and (got[:, :, :, pos + T:] == 0).all()
+
+
+WIDE_ATTN = [  # (B, H, Tq, Tk, D)
+    (2, 2, 1, 700, 512),    # decode, key splits merged in the workgroup
+    (1, 2, 1, 5000, 1024),  # decode, 39 key splits: workspace and combine (8 merge in a workgroup at 1024)
+    (3, 2, 1, 300, 1000),   # pair slices
+    (2, 2, 1, 1200, 300),   # pair slices with key splits
+    (2, 2, 1, 500, 130),    # pair slices of 4 elements
+    (2, 2, 1, 500, 192),    # vector slices, D below its power of two
+    (1, 2, 70, 70, 384),    # causal prefill
+    (1, 1, 33, 50, 1000),   # chunked prefill, pair slices
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", WIDE_ATTN, ids=lambda s: "x".join(map(str, s)))
+def test_attention_wide_head_dims(dev, dtype, shape):
+    """dg_attention at head dims past 128 against float64 at the north-star
+    bars."""
+    B, H, Tq, Tk, D = shape
+    err = _attention_case(dev, dtype, B, H, Tq, Tk, D, cache_layout=(Tq != Tk), seed=Tk + D)
+    assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 2, 1, 600, 512), (1, 2, 40, 40, 256), (1, 1, 1, 3000, 1024)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_attention_pair_slices_on_misaligned_rows(dev, dtype, shape):
+    """q, k, v and y aligned to a pair only (power-of-two head dims that
+    would take vector slices): pair slices, within the bars of float64."""
+    from diff_gpt import _native
+
+    B, H, Tq, Tk, D = shape
+    q = _randn((B, Tq, H, D), 5 + D, dtype)
+    k = _randn((B, Tk, H, D), 6 + D, dtype)
+    v = _randn((B, Tk, H, D), 7 + D, dtype)
+    ref = on.attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    qd, kd, vd = (_misaligned(t.to(dev)) for t in (q, k, v))
+    y = _misaligned(torch.zeros_like(q).to(dev))
+    _native.attention_(qd, kd, vd, y, 1.0 / np.sqrt(D))
+    got = y.float().cpu().numpy().astype(np.float64)
+    assert np.abs(got - ref).max() <= TOL[dtype] * np.abs(ref).max()
 
 
 # ------------------------------------------------------------------ strided copy

@@ -491,6 +491,36 @@ def test_cfg0_greedy_ids_and_logits_match_oracle(dev):
     assert kv.get_pos() == 96 + 48
 
 
+@pytest.mark.parametrize("n_embd,n_head", [(1024, 2), (600, 2), (1024, 1)],
+                         ids=["head_dim512", "head_dim300", "head_dim1024"])
+def test_wide_head_dim_model_matches_oracle(dev, n_embd, n_head):
+    """A GPT whose head_dim is past 256 (the reference's SDPA takes any even
+    head_dim; the kernels take every even one up to 1024): fp32 prefill of 3
+    prompts of 20 ids and 6 teacher-forced greedy decode steps, logits within
+    1e-5 * max|ref| of the oracle at every step and the argmax equal to the
+    oracle's token wherever the top-2 margin exceeds twice that bar."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    model = _gpt(dev, vocab_size=64, n_embd=n_embd, block_size=40, n_head=n_head, n_layer=1,
+                 use_checkpoint=False)
+    params = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    cfg = tr.ModelConfig(vocab_size=64, n_embd=n_embd, block_size=40, n_head=n_head, n_layer=1)
+    prompts = torch.randint(0, 64, (3, 20), generator=torch.Generator().manual_seed(5))
+    ref_tokens, ref_logits = tr.greedy_decode(params, cfg, prompts, 6)
+    kv = KVCache(batch_size=3, num_heads=n_head, seq_len=26, head_dim=n_embd // n_head, num_layers=1)
+    with torch.no_grad():
+        logits = model(prompts.to(dev), kv_cache=kv)[0][:, -1]
+        for s in range(6):
+            ref = ref_logits[s]
+            bar = 1e-5 * ref.abs().max().item()
+            err = (logits.cpu() - ref).abs().max().item()
+            assert err <= bar, (s, err, bar)
+            top2 = ref.topk(2, dim=-1).values
+            clear = (top2[:, 0] - top2[:, 1]) > 2 * bar
+            assert torch.equal(logits.argmax(-1).cpu()[clear], ref_tokens[clear, s])
+            logits = model(ref_tokens[:, s:s + 1].to(dev), kv_cache=kv)[0][:, -1]
+
+
 def test_cfg0_kv_cache_contents_match_oracle(dev):
     """After the cfg0 prefill, the cache holds the oracle's rotated+normed K and
     raw V (same model weights; the projections differ only by GEMM rounding)."""

@@ -145,24 +145,25 @@ def test_gpt_constructor_assertions():
 
 
 @pytest.mark.parametrize("n_embd,n_head,ok", [
-    (1024, 2, False),  # head_dim 512: a power of two above 256
-    (1024, 4, True),   # 256: the largest power of two the kernels take
-    (768, 4, False),   # 192: not a power of two, above 128
-    (480, 4, True),    # 120: not a power of two, within 128
+    (2048, 1, False),  # head_dim 2048: past the largest the kernels take
+    (2052, 2, False),  # 1026: even, past 1024
+    (1024, 1, True),   # 1024: the largest
+    (1024, 2, True),   # 512
+    (768, 4, True),    # 192: not a power of two
+    (1000, 1, True),   # 1000: not a multiple of a 16-byte slice (pair slices)
     (96, 8, True),     # 12
 ])
 def test_gpt_rejects_head_dims_beyond_the_kernels(n_embd, n_head, ok):
-    """The reference's SDPA takes any even head_dim; the HIP kernels take even
-    head dims up to 256 (powers of two) or 128 (other sizes).  A model outside
-    that range is refused when it is built, with the limit in the message,
-    not at its first launch."""
+    """The reference's SDPA takes any even head_dim; the HIP kernels take every
+    even head_dim up to 1024.  A model outside that range is refused when it
+    is built, with the limit in the message, not at its first launch."""
     from diff_gpt import _native
 
     assert _native.head_dim_supported(n_embd // n_head) == ok
     if ok:
         GPT(vocab_size=64, n_embd=n_embd, block_size=8, n_layer=1, n_head=n_head)
     else:
-        with pytest.raises(ValueError, match=r"head_dim \d+ .*up to 256 \(powers of two\) or 128"):
+        with pytest.raises(ValueError, match=r"head_dim \d+ .*even head dims up to 1024"):
             GPT(vocab_size=64, n_embd=n_embd, block_size=8, n_layer=1, n_head=n_head)
 
 

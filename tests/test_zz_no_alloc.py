@@ -76,23 +76,25 @@ def test_noalloc_decode_step_equals_workspace_form(dev):
 
 
 def test_noalloc_scratch_covers_every_decode_step():
-    """Key splits beyond the 16 that one workgroup merges occur only while
-    B*H < 256, so at most 4350 partials of head_dim + 2 <= 258 floats need
-    the scratch: every decode step fits the 8 MiB array (host-side sizing,
-    so this runs without a GPU).  The workspace-size query agrees with that
-    bound over a sweep of row counts, lengths and head sizes."""
+    """Key splits beyond the 16 that one workgroup merges (8 for head dims
+    past 512) occur only while B*H < 256 (512), so at most 4351 partials of
+    padded head_dim + 2 <= 514 floats (4607 of <= 1026) need the scratch:
+    every decode step fits the 20 MiB array (host-side sizing, so this runs
+    without a GPU).  The workspace-size query agrees with that bound over a
+    sweep of row counts, lengths and head sizes."""
     from diff_gpt import _native
 
     lib = _native.lib()
     cap = lib.dg_decode_step_noalloc_scratch_bytes()
-    assert cap == 8 << 20
+    assert cap == 20 << 20
     worst = 0
-    for bh in list(range(1, 300)) + [511, 1024, 2047, 4095, 4096, 8191, 100000]:
+    for bh in list(range(1, 300)) + [383, 511, 512, 1024, 2047, 4095, 4096, 8191, 100000]:
         for max_pos in (1, 255, 256, 2175, 2176, 4096, 8192, 65536, 1 << 20):
-            for D in (16, 64, 128, 256):
+            for D in (16, 64, 128, 256, 300, 512, 1000, 1024):
                 need = lib.dg_decode_step_workspace_size(bh, 1, max_pos, D, 1)
                 assert need <= cap, (bh, max_pos, D, need)
                 if need:
-                    assert bh < 256, (bh, max_pos, D)
+                    assert bh < (256 if D <= 512 else 512), (bh, max_pos, D)
+                    assert need <= (4351 * 514 if D <= 512 else 4607 * 1026) * 4, (bh, max_pos, D, need)
                 worst = max(worst, need)
-    assert 0 < worst <= 4350 * 258 * 4
+    assert 0 < worst <= 4607 * 1026 * 4
