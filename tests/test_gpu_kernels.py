@@ -467,6 +467,8 @@ GROUPED = [  # (B, group, H, prefix, Tk, D)
     (10, 4, 2, 33, 70, 16),
     (12, 6, 8, 600, 1100, 64),
     (4, 2, 8, 1500, 2600, 128),
+    (6, 3, 2, 200, 900, 300),   # pair slices: prefix and own keys read pair by pair
+    (4, 2, 2, 100, 300, 512),
 ]
 # Groups of >= 16 rows with head_dim 16 / 32 take the matrix-core kernel
 # (dg_attn_shared.hip) whenever the vector kernel would not split the keys
@@ -584,6 +586,7 @@ DECODE_STEP = [  # (B, group, H, prefix, pos, D, cap)
     (2, 1, 2, 0, 300, 512, 320),
     (3, 1, 2, 0, 100, 300, 130),
     (4, 2, 2, 50, 120, 384, 140),
+    (4, 2, 2, 50, 120, 300, 140),
     (1, 1, 2, 0, 3000, 1000, 3100),
 ]
 
