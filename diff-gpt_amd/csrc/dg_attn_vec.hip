@@ -526,10 +526,8 @@ int launch_attn(AttnArgs a, hipStream_t s) {
 // slices (pair_slice_epl; read pair by pair past one pair per lane).
 template <typename T, int DPAD, bool FUSED>
 int attn_pick_epl(int epl, bool pairs, const AttnArgs& a, hipStream_t s) {
-  constexpr int es = (int)sizeof(T);
-  constexpr int VEC = ((16 / es) < DPAD ? (16 / es) : DPAD) > DPAD / 64 ? ((16 / es) < DPAD ? (16 / es) : DPAD)
-                                                                        : DPAD / 64;
-  constexpr int PAIR = DPAD / 64 > 2 ? DPAD / 64 : 2;
+  constexpr int VEC = vec_slice_epl(DPAD, (int)sizeof(T));
+  constexpr int PAIR = pair_slice_epl(DPAD);
   if (!pairs && epl == VEC) return launch_attn<T, DPAD, VEC, FUSED, false>(a, s);
   if (pairs && epl == PAIR) return launch_attn<T, DPAD, PAIR, FUSED, (PAIR > 2)>(a, s);
   set_error("attention: no kernel for D pad %d with %d elements per lane", DPAD, epl);

@@ -538,14 +538,13 @@ int check_launch(const char* what);
 // pair alignment: one pair per lane up to DPAD = 128, beyond that read pair
 // by pair (load_slice with PAIRS).
 constexpr int kMaxHeadDim = 1024;
-inline int vec_slice_epl(int dpad, int es) {
-  int e = 16 / es;
-  if (e > dpad) e = dpad;
+constexpr int vec_slice_epl(int dpad, int es) {
+  const int e = 16 / es < dpad ? 16 / es : dpad;
   return dpad / 64 > e ? dpad / 64 : e;
 }
-inline int pair_slice_epl(int dpad) { return dpad / 64 > 2 ? dpad / 64 : 2; }
+constexpr int pair_slice_epl(int dpad) { return dpad / 64 > 2 ? dpad / 64 : 2; }
 // Elements per load of a slice of epl elements: the operands' alignment unit.
-inline int slice_load_elems(int epl, int es) { return epl * es > 16 ? 16 / es : epl; }
+constexpr int slice_load_elems(int epl, int es) { return epl * es > 16 ? 16 / es : epl; }
 
 // A shared prefix (dg_prefix) as the kernels read it: keys t < len of row b
 // at k + (b / group) * kb + t * (the cache's t stride) + h * kh (likewise v).

@@ -228,10 +228,8 @@ int launch_rope(const RopeArgs& a, hipStream_t s) {
 // slices (pair_slice_epl; read pair by pair past one pair per lane).
 template <typename T, typename FT, int DPAD>
 int rope_pick_epl(int epl, bool pairs, const RopeArgs& a, hipStream_t s) {
-  constexpr int es = (int)sizeof(T);
-  constexpr int PREF = (16 / es) < DPAD ? (16 / es) : DPAD;
-  constexpr int VEC = PREF > DPAD / 64 ? PREF : DPAD / 64;
-  constexpr int PAIR = DPAD / 64 > 2 ? DPAD / 64 : 2;
+  constexpr int VEC = vec_slice_epl(DPAD, (int)sizeof(T));
+  constexpr int PAIR = pair_slice_epl(DPAD);
   if (!pairs && epl == VEC) return launch_rope<T, FT, DPAD, VEC, false>(a, s);
   if (pairs && epl == PAIR) return launch_rope<T, FT, DPAD, PAIR, (PAIR > 2)>(a, s);
   set_error("rope: no kernel for D pad %d with %d elements per lane", DPAD, epl);
