@@ -265,33 +265,39 @@ class Engine:
             columns.append(column)
             masks.append(mask)
         T, steps = len(prompts[0]), len(columns)
-        # the token columns reach the host in one copy; the mask of a step that
-        # samples or forces every row is known on the host already, and when
-        # every step is such a step all rows share one mask list
+        # the mask of a step that samples or forces every row is known on the
+        # host already; when every step is such a step all rows share one mask
         on_device = [s for s, m in enumerate(masks) if isinstance(m, torch.Tensor)]
-        mask_np = None
-        if on_device:
-            mask_np = np.empty((rows, steps), dtype=np.int64)
-            for s, m in enumerate(masks):
-                if not isinstance(m, torch.Tensor):
-                    mask_np[:, s] = m
-            mask_np[:, on_device] = torch.stack([masks[s] for s in on_device], dim=1).cpu().numpy()
-        gen_np = torch.stack(columns, dim=1).cpu().numpy() if columns else np.empty((rows, 0), dtype=np.int64)
         # about 2 * rows lists of Python ints are built here: with the garbage
         # collector running, a full collection triggered meanwhile walks every
         # list already built (measured: 100+ ms on a 6400-row call)
         gc_enabled = gc.isenabled()
         gc.disable()
         try:
-            generated = gen_np.tolist()
-            results = [prompts[r // num_samples] + generated[r] for r in range(rows)]
-            if mask_np is None:
+            # the lists that need nothing from the device are built first,
+            # while it still runs the steps enqueued above
+            results = [prompts[r // num_samples].copy() for r in range(rows)]
+            if not on_device:
                 shared = [0] * T + [int(m) for m in masks]
                 out_masks = [shared.copy() for _ in range(rows)]
             else:
-                mask_rows = mask_np.tolist()
+                mask_np = np.empty((rows, steps), dtype=np.int64)
+                for s, m in enumerate(masks):
+                    if not isinstance(m, torch.Tensor):
+                        mask_np[:, s] = m
+                mask_np[:, on_device] = torch.stack([masks[s] for s in on_device], dim=1).cpu().numpy()
                 zeros = [0] * T
-                out_masks = [zeros + mask_rows[r] for r in range(rows)]
+                out_masks = [zeros + row for row in mask_np.tolist()]
+            if gc_enabled:
+                # the youngest generation's collection, which these lists
+                # would trigger once the collector runs again, happens now:
+                # while the device may still work, and over the rows before
+                # the generated tokens lengthen them
+                gc.collect(0)
+            # the token columns reach the host in one copy
+            if columns:
+                for row, gen in zip(results, torch.stack(columns, dim=1).cpu().numpy().tolist()):
+                    row += gen
         finally:
             if gc_enabled:
                 gc.enable()
@@ -427,6 +433,8 @@ class Engine:
                         column = torch.where(scheduled, forced, column)
                         mask = (~scheduled).long()
                 yield column, mask
+                if step == steps - 1:
+                    break  # the last column's logits would go unused
 
                 # 3) one decode forward for the column just emitted
                 step_ids = column.unsqueeze(1)

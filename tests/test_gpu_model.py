@@ -631,6 +631,44 @@ def test_engine_graph_replay_equals_eager(dev, dtype):
         assert a == b, kw
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_engine_kept_graph_equals_eager_across_calls(dev, dtype):
+    """One Engine over several generate_multi_batch calls with the same rows,
+    prompt length and budget (the captured step kept and replayed again):
+    other seeds and temperatures, forced and per-row mixed steps between
+    sampled ones -- tokens and masks equal to the eager engine's every time."""
+    import numpy as np
+
+    from diff_gpt.model.engine import Engine
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=256, n_embd=64, block_size=138, n_head=4, n_layer=2,
+                use_checkpoint=False).eval().to(dev).to(dtype)
+    g = torch.Generator().manual_seed(11)
+    prompts = [torch.randint(0, 256, (30,), generator=g).tolist() for _ in range(3)]
+    rows, steps = 3 * 8, 12
+    table = np.random.default_rng(5).integers(0, 256, (rows, steps))
+    table[np.random.default_rng(6).random((rows, steps)) < 0.6] = -1  # sampled where negative
+    table[:, 3] = 17  # every row forced
+    cases = [dict(sampler=TemperatureSampler(1.0), seed=1),
+             dict(sampler=TemperatureSampler(1.0), seed=2),
+             dict(sampler=TemperatureSampler(0.7), seed=3),
+             dict(sampler=None, seed=4),
+             dict(sampler=TemperatureSampler(0.0)),
+             dict(sampler=TemperatureSampler(1.0), seed=5, force_schedule=[None, 5, None, None, 9] + [None] * 7),
+             dict(sampler=TemperatureSampler(1.3), seed=6, force_schedule=table)]
+    e = Engine(model)
+    kept = None
+    for kw in cases:
+        got = e.generate_multi_batch(prompts, num_samples=8, max_tokens=steps, **kw)
+        ref = Engine(model, use_graph=False).generate_multi_batch(prompts, num_samples=8, max_tokens=steps, **kw)
+        assert got == ref, kw
+        assert kept is None or e._kept[2] is kept  # one capture, replayed by every later call
+        kept = e._kept[2]
+
+
 def test_engine_reuses_the_captured_step_across_calls(dev):
     """A second call with the same rows, prompt length and budget replays the
     step captured by the first into the same cache, and gives a fresh Engine's
