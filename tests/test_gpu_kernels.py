@@ -799,6 +799,57 @@ def test_attention_wide_head_dims(dev, dtype, shape):
     assert err <= TOL[dtype], err
 
 
+def _random_wide(seed, n):
+    """Seeded (B, H, Tq, Tk, D, misaligned): any even D from 2 to 1024,
+    decode, causal or chunked, the operands aligned to a pair only in about
+    a third of the cases."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = 2 * int(rng.integers(1, 513))
+        Tk = int(rng.integers(1, 1000))
+        Tq = min(int(rng.choice([1, Tk, int(rng.integers(1, Tk + 1))])), 400)
+        Tk = max(Tk, Tq)
+        out.append((int(rng.integers(1, 4)), int(rng.integers(1, 4)), Tq, Tk, D, bool(rng.random() < 0.35)))
+    return out
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", _random_wide(31, 14), ids=lambda s: "x".join(map(str, s)))
+def test_rope_and_attention_random_head_dims(dev, dtype, shape):
+    """Seeded random even head dims up to 1024, aligned or aligned to a pair
+    only: RoPE + QK-norm bit-exact against the oracle, then attention over
+    the rotated rows within the north-star bars of float64."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    B, H, Tq, Tk, D, mis = shape
+    seed = D + Tk
+    q = _randn((B, Tq, H, D), seed, dtype, 2.0)
+    k = _randn((B, Tk, H, D), seed + 1, dtype, 2.0)
+    v = _randn((B, Tk, H, D), seed + 2, dtype)
+    fq = precompute_freqs_cis(D, 2 * Tk, 10000).to(TDT[dtype])
+    fq_q = fq[Tk - Tq:Tk].view(1, Tq, 1, D // 2, 2)
+    fq_k = fq[:Tk].view(1, Tk, 1, D // 2, 2)
+    put = _misaligned if mis else (lambda t: t)
+    qd, kd, vd = (put(t.to(dev)) for t in (q, k, v))
+    q_rot = put(torch.zeros_like(q).to(dev))
+    k_rot = put(torch.zeros_like(k).to(dev))
+    v_out = put(torch.zeros_like(v).to(dev))
+    ops = _native.ops()
+    ops.rope_qknorm_append(qd, None, None, fq_q.to(dev), q_rot, None, None, True)
+    ops.rope_qknorm_append(None, kd, vd, fq_k.to(dev), None, k_rot, v_out, True)
+    exp_q = on.rope_qknorm(q.float().numpy(), fq_q.float().numpy(), dtype)
+    exp_k = on.rope_qknorm(k.float().numpy(), fq_k.float().numpy(), dtype)
+    assert np.array_equal(_bits(q_rot), exp_q.view(np.uint32))
+    assert np.array_equal(_bits(k_rot), exp_k.view(np.uint32))
+    assert torch.equal(v_out.cpu(), v)
+    y = put(torch.zeros_like(q).to(dev))
+    _native.attention_(q_rot, k_rot, v_out, y, 1.0 / np.sqrt(D))
+    ref = on.attention_f64(exp_q.astype(np.float64), exp_k.astype(np.float64), v.float().numpy().astype(np.float64))
+    assert np.abs(y.float().cpu().numpy() - ref).max() <= TOL[dtype] * np.abs(ref).max()
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("shape", [(2, 2, 1, 600, 512), (1, 2, 40, 40, 256), (1, 1, 1, 3000, 1024)],
                          ids=lambda s: "x".join(map(str, s)))
