@@ -19,6 +19,7 @@ from oracle import numerics as on  # noqa: F401  (tests share the oracle import 
 CASES = [  # (B, H, D, dtype, max_pos, pos, group, prefix_len)
     (4, 8, 128, torch.bfloat16, 3200, 3000, 1, 0),  # configs[4]-like rows: 25 key splits
     (2, 4, 64, torch.float32, 2600, 2400, 1, 0),    # smaller second call: 20 splits
+    (1, 2, 1000, torch.bfloat16, 5000, 4800, 1, 0),  # head_dim 1000 (pair slices): 39 splits
 ]
 
 
