@@ -85,7 +85,7 @@ int mfma_prefill_rope(int B, int H, int Tq, int Tk, int D, int dtype, const void
                       const dg_stride3* y_st, float scale, hipStream_t s);
 
 // ---------------------------------------------------------------------------
-// Strided 4-D copy (exact), element size 2 or 4 bytes.
+// Strided 4-D copy (exact), element size 2, 4 or 8 bytes.
 // ---------------------------------------------------------------------------
 struct CopyArgs {
   const void* src;
@@ -154,7 +154,7 @@ int resolve_prefix(const dg_prefix* p, int limit, int dtype, const char* what, c
   if (p->k != nullptr) {
     DG_REQUIRE(p->k_st.t == k_st->t && p->v_st.t == v_st->t, DG_EINVAL,
                "%s: prefix pages must have the cache's position stride", what);
-    const int64_t es = dtype == DG_F32 ? 4 : 2;
+    const int64_t es = dtype_bytes(dtype);
     k = static_cast<const char*>(k) - (int64_t)p->own_start * k_st->t * es;
     v = static_cast<const char*>(v) - (int64_t)p->own_start * v_st->t * es;
     out = PrefixRef{p->k, p->v, p->k_st.b, p->k_st.h, p->v_st.b, p->v_st.h, p->len, p->group, p->own_start};
@@ -175,8 +175,8 @@ extern "C" int dg_abi_version(void) { return DG_ABI_VERSION; }
 extern "C" const char* dg_last_error(void) { return g_err; }
 
 extern "C" size_t dg_attention_workspace_size(int B, int H, int Tq, int Tk, int D, int dtype) {
-  (void)dtype;
-  if (B <= 0 || H <= 0 || Tq <= 0 || Tk <= 0 || D <= 0) return 0;
+  // float64 runs on a kernel without key splits
+  if (B <= 0 || H <= 0 || Tq <= 0 || Tk <= 0 || D <= 0 || dtype == DG_F64) return 0;
   return vec_attention_workspace(B, H, Tq, Tk, D);
 }
 
@@ -186,7 +186,7 @@ extern "C" int dg_attention_grouped(int B, int H, int Tq, int Tk, int D, int dty
                                     const dg_stride3* y_st, float scale, const dg_prefix* prefix,
                                     void* workspace, size_t workspace_bytes, void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0 && Tq >= 0 && Tk >= 0, DG_EINVAL, "attention: negative size");
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "attention: dtype %d unsupported", dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention: head_dim must be even (got %d)", D);
   if ((int64_t)B * H * Tq == 0) return DG_OK;
@@ -253,7 +253,7 @@ extern "C" int dg_decode_attention_at(int B, int H, int D, int dtype, const void
                                       int max_keys, void* workspace, size_t workspace_bytes,
                                       void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "attention_at: negative size");
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "attention_at: dtype %d unsupported", dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "attention_at: head_dim must be even (got %d)", D);
   DG_REQUIRE(max_keys >= 1, DG_EINVAL, "attention_at: max_keys must be >= 1 (got %d)", max_keys);
@@ -287,10 +287,10 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
                               float scale, const dg_prefix* prefix, int flags, void* workspace,
                               size_t workspace_bytes, void* stream) {
   DG_REQUIRE(B >= 0 && H >= 0, DG_EINVAL, "decode_step: negative size");
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "decode_step: dtype %d unsupported", dtype);
-  DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == DG_BF16 || freqs_dtype == DG_F16, DG_EUNSUPPORTED,
-             "decode_step: freqs dtype %d unsupported", freqs_dtype);
+  DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == dtype, DG_EUNSUPPORTED,
+             "decode_step: freqs dtype %d unsupported (fp32 or the data's dtype)", freqs_dtype);
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "decode_step: head_dim must be even (got %d)", D);
   DG_REQUIRE(max_pos >= 1, DG_EINVAL, "decode_step: max_pos must be >= 1 (got %d)", max_pos);
   DG_REQUIRE(freqs_pos_stride >= 0, DG_EINVAL, "decode_step: negative freqs_pos_stride");
@@ -350,7 +350,7 @@ extern "C" int dg_decode_step(int B, int H, int D, int dtype, const void* q, con
                : vec_attention(B, H, 1, max_pos, D, dtype, y, y_st, kw, kc_st, vw, vc_st, y, y_st, scale, pre,
                                pos_dev, workspace, workspace_bytes, max_pos, s);
   }
-  const int64_t es = dtype == DG_F32 ? 4 : 2, fes = freqs_dtype == DG_F32 ? 4 : 2;
+  const int64_t es = dtype_bytes(dtype), fes = dtype_bytes(freqs_dtype);
   const dg_stride3 f_st = {0, 0, 0};
   rc = dg_rope_qknorm_append(B, 1, H, D, dtype, q, q_st, y, y_st, k, k_st,
                              static_cast<char*>(kw) + (int64_t)pos * kc_st->t * es, kc_st, v, v_st,
@@ -380,7 +380,7 @@ extern "C" int dg_attention(int B, int H, int Tq, int Tk, int D, int dtype, cons
 
 extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const int64_t* src_st,
                          void* dst, const int64_t* dst_st, void* stream) {
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "copy4d: dtype %d unsupported", dtype);
   DG_REQUIRE(shape && src_st && dst_st, DG_EINVAL, "copy4d: NULL shape/strides");
   for (int i = 0; i < 4; ++i) DG_REQUIRE(shape[i] >= 0, DG_EINVAL, "copy4d: negative extent");
@@ -394,7 +394,7 @@ extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const
   a.s0 = src_st[0]; a.s1 = src_st[1]; a.s2 = src_st[2]; a.s3 = src_st[3];
   a.d0 = dst_st[0]; a.d1 = dst_st[1]; a.d2 = dst_st[2]; a.d3 = dst_st[3];
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t es = dtype == DG_F32 ? 4 : 2;
+  const int64_t es = dtype_bytes(dtype);
   const int64_t row_bytes = shape[3] * es;
   auto bytes16 = [&](int64_t stride) { return (stride * es) % 16 == 0; };
   if (src_st[3] == 1 && dst_st[3] == 1 && row_bytes % 16 == 0 &&
@@ -412,7 +412,9 @@ extern "C" int dg_copy4d(int dtype, const int64_t* shape, const void* src, const
   }
   int64_t blocks = (a.total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  if (dtype == DG_F32)
+  if (dtype == DG_F64)
+    hipLaunchKernelGGL(copy4d_kernel<uint64_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
+  else if (dtype == DG_F32)
     hipLaunchKernelGGL(copy4d_kernel<uint32_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);
   else
     hipLaunchKernelGGL(copy4d_kernel<uint16_t>, dim3((unsigned)blocks), dim3(256), 0, s, a);

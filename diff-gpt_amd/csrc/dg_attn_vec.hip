@@ -448,6 +448,80 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnArgs a, con
 }
 
 // ---------------------------------------------------------------------------
+// float64 attention (a GPT.double() model; SDPA in float64, mha.py:61-81):
+// one wave per (b, h, i), every key in turn, lane l holding elements
+// l, l + 64, ... of the rows (D <= 1024: at most 16); the scores, the online
+// softmax (exact running maximum) and the output in float64.  Same masks,
+// shared prefix and device position as attn_vec_kernel; no key splits.
+// ---------------------------------------------------------------------------
+constexpr int kF64Elems = 16;  // 1024 / 64
+
+__global__ __launch_bounds__(256) void attn_f64_kernel(const AttnArgs a, const double scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (unit >= a.units) return;  // whole waves leave; no barriers follow
+  int64_t r = unit;
+  const int i = (int)(r % a.Tq);
+  r /= a.Tq;
+  const int h = (int)(r % a.H);
+  const int64_t b = r / a.H;
+  int Tk = a.Tk, q_offset = a.q_offset;
+  if (a.pos_dev != nullptr) {  // uniform over the grid
+    Tk = min(*a.pos_dev + 1, a.Tk);
+    q_offset = Tk - 1;
+  }
+  const int kvis = min(Tk, i + q_offset + 1);
+  const double* qp = static_cast<const double*>(a.q) + b * a.qb + (int64_t)i * a.qt + (int64_t)h * a.qh;
+  double q[kF64Elems], acc[kF64Elems];
+#pragma unroll
+  for (int e = 0; e < kF64Elems; ++e) {
+    const int d = lane + 64 * e;
+    q[e] = d < a.D ? qp[d] : 0.0;
+    acc[e] = 0.0;
+  }
+  const double* kbase = static_cast<const double*>(a.k) + b * a.kb + (int64_t)h * a.kh;
+  const double* vbase = static_cast<const double*>(a.v) + b * a.vb + (int64_t)h * a.vh;
+  const int64_t grp = b / a.pre.group;
+  const double* kpre = static_cast<const double*>(a.pre.k) + grp * a.pre.kb + (int64_t)h * a.pre.kh;
+  const double* vpre = static_cast<const double*>(a.pre.v) + grp * a.pre.vb + (int64_t)h * a.pre.vh;
+  double m = -__builtin_huge_val(), l = 0.0;
+  for (int j = 0; j < kvis; ++j) {
+    const bool pre = j < a.pre.len;
+    const double* kr = (pre ? kpre : kbase) + (int64_t)j * a.kt;
+    const double* vr = (pre ? vpre : vbase) + (int64_t)j * a.vt;
+    double dot = 0.0;
+#pragma unroll
+    for (int e = 0; e < kF64Elems; ++e) {
+      const int d = lane + 64 * e;
+      if (d < a.D) dot += q[e] * kr[d];
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) dot += __shfl_xor(dot, off, 64);
+    const double s = dot * scale;
+    if (s > m) {  // wave-uniform: every lane holds the same sum
+      const double alpha = exp(m - s);  // 0 for the first key
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < kF64Elems; ++e) acc[e] *= alpha;
+      m = s;
+    }
+    const double p = exp(s - m);
+    l += p;
+#pragma unroll
+    for (int e = 0; e < kF64Elems; ++e) {
+      const int d = lane + 64 * e;
+      if (d < a.D) acc[e] += p * vr[d];
+    }
+  }
+  double* yp = static_cast<double*>(a.y) + b * a.yb + (int64_t)i * a.yt + (int64_t)h * a.yh;
+#pragma unroll
+  for (int e = 0; e < kF64Elems; ++e) {
+    const int d = lane + 64 * e;
+    if (d < a.D) yp[d] = acc[e] / l;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 namespace {
@@ -591,10 +665,38 @@ int vec_launch(int B, int H, int Tq, int Tk, int D, int dtype, const void* q, co
   // size_keys (>= Tk) sizes the key splits and the workspace: a decode step
   // passes its max_pos, so that the host- and device-position forms split
   // the same way and give the same bits
-  const int es = dtype == DG_F32 ? 4 : 2;
+  const int es = (int)dtype_bytes(dtype);
   const int dpad = next_pow2(D);
   DG_REQUIRE(D <= kMaxHeadDim, DG_EUNSUPPORTED, "attention: head_dim %d > %d", D, kMaxHeadDim);
   DG_REQUIRE(scale > 0.f, DG_EINVAL, "attention: scale must be positive (got %g)", (double)scale);
+  if (dtype == DG_F64) {
+    if (step != nullptr) {  // the decode step of a float64 model runs as two launches
+      *declined = true;
+      return DG_OK;
+    }
+    DG_REQUIRE(aligned(q, 8) && aligned(k, 8) && aligned(v, 8) && aligned(y, 8) && (pre.len == 0 ||
+               (aligned(pre.k, 8) && aligned(pre.v, 8))), DG_EINVAL, "attention: float64 rows must be 8-byte aligned");
+    DG_REQUIRE(k_st->t >= 0 && v_st->t >= 0, DG_EINVAL, "attention: negative key/value row stride");
+    AttnArgs a{};
+    a.q = q; a.k = k; a.v = v; a.y = y;
+    a.qb = q_st->b; a.qt = q_st->t; a.qh = q_st->h;
+    a.kb = k_st->b; a.kt = k_st->t; a.kh = k_st->h;
+    a.vb = v_st->b; a.vt = v_st->t; a.vh = v_st->h;
+    a.yb = y_st->b; a.yt = y_st->t; a.yh = y_st->h;
+    a.H = H; a.Tq = Tq; a.Tk = Tk; a.D = D;
+    a.q_offset = Tk - Tq;
+    a.pre = pre;
+    a.pos_dev = pos_dev;
+    a.nsplit = 1;
+    a.units = (int64_t)B * H * Tq;
+    DG_REQUIRE((a.units + 3) / 4 <= 0x7fffffffLL, DG_EINVAL, "attention: too many units");
+    // the ABI's scale is fp32; its rounding of SDPA's default 1/sqrt(D) stands
+    // for 1/sqrt(D) in float64, as a float64 model's SDPA applies it
+    const double d_inv = 1.0 / sqrt((double)D);
+    const double dscale = scale == (float)d_inv ? d_inv : (double)scale;
+    hipLaunchKernelGGL(attn_f64_kernel, dim3((unsigned)((a.units + 3) / 4)), dim3(256), 0, s, a, dscale);
+    return check_launch("attn_f64_kernel");
+  }
   // row offsets inside one (b, h) page are 32-bit in the kernel
   const int64_t span_k = (int64_t)Tk * (k_st->t < 0 ? -k_st->t : k_st->t);
   const int64_t span_v = (int64_t)Tk * (v_st->t < 0 ? -v_st->t : v_st->t);

@@ -182,6 +182,7 @@ struct RowsArgs {
   int64_t x_ld, g_ld, out_ld, M;
   int N;          // output columns
   float p0, p1;   // swiglu: alpha, limit;  softcap: cap
+  double d0, d1;  // the same in float64 (the float64 kernels)
 };
 
 template <typename T>
@@ -225,6 +226,95 @@ __global__ __launch_bounds__(256) void softcap_kernel(const RowsArgs a) {
   const float x = to_f32(static_cast<const T*>(a.x)[r * a.x_ld + c]);
   const float t = rt<T>(tanhf(rt<T>(x / cap)));
   static_cast<T*>(a.out)[r * a.out_ld + c] = from_f32<T>(cap * t);
+}
+
+// ---------------------------------------------------------------------------
+// float64 rows (a GPT.double() model): the same ops in float64 arithmetic, as
+// torch's float64 kernels evaluate them -- sigmoid 1 / (1 + exp(-x)), tanh,
+// the RMSNorms with DBL_EPSILON, the source softmax with its maximum
+// subtracted.  alpha, limit and cap are the ABI's float64 values.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ double sigmoid_f64(double x) { return 1.0 / (1.0 + exp(-x)); }
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// rms_norm(block_attn_res(V, w)) for one row per wave, two passes over the
+// sources (C <= 2048, lane l holding columns l, l + 64, ...): the scores
+// rms_norm(V_n) . w, their softmax over n, h = sum_n p_n V_n written out, then
+// h's RMSNorm in place (each lane rescales the columns it wrote).
+__global__ __launch_bounds__(256) void attn_res_norm_f64_kernel(const AttnResArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;  // whole waves leave; no barriers follow
+  const double* w = static_cast<const double*>(a.w);
+  double score[kMaxResSources];
+  double mx = -__builtin_huge_val();
+  for (int n = 0; n < a.nsrc; ++n) {
+    const double* x = static_cast<const double*>(a.src[n]) + row * a.ld[n];
+    double ss = 0.0;
+    for (int c = lane; c < a.N; c += 64) ss += x[c] * x[c];
+    const double r = 1.0 / sqrt(wave_sum_f64(ss) / (double)a.N + DBL_EPSILON);
+    double dot = 0.0;
+    for (int c = lane; c < a.N; c += 64) dot += (x[c] * r) * w[c];
+    score[n] = wave_sum_f64(dot);
+    mx = fmax(mx, score[n]);
+  }
+  double sum = 0.0;
+  for (int n = 0; n < a.nsrc; ++n) {
+    score[n] = exp(score[n] - mx);
+    sum += score[n];
+  }
+  double* o = static_cast<double*>(a.out) + row * a.out_ld;
+  double ss = 0.0;
+  for (int c = lane; c < a.N; c += 64) {
+    double h = 0.0;
+    for (int n = 0; n < a.nsrc; ++n) h += (score[n] / sum) * static_cast<const double*>(a.src[n])[row * a.ld[n] + c];
+    o[c] = h;
+    ss += h * h;
+  }
+  const double r = 1.0 / sqrt(wave_sum_f64(ss) / (double)a.N + DBL_EPSILON);
+  for (int c = lane; c < a.N; c += 64) o[c] = o[c] * r;
+}
+
+__global__ __launch_bounds__(256) void gate_kernel_f64(const RowsArgs a) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.M * a.N) return;
+  const int64_t r = idx / a.N;
+  const int c = (int)(idx - r * a.N);
+  const double y = static_cast<const double*>(a.x)[r * a.x_ld + c];
+  const double s = sigmoid_f64(static_cast<const double*>(a.g)[r * a.g_ld + c]);
+  static_cast<double*>(a.out)[r * a.out_ld + c] = y * s;
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel_f64(const RowsArgs a) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.M * a.N) return;
+  const int64_t r = idx / a.N;
+  const int j = (int)(idx - r * a.N);
+  const double* xr = static_cast<const double*>(a.x) + r * a.x_ld;
+  const double alpha = a.d0, limit = a.d1;
+  const double gate = fmin(xr[2 * j], limit);
+  const double lin = fmin(fmax(xr[2 * j + 1], -limit), limit);
+  const double s = sigmoid_f64(alpha * gate);
+  static_cast<double*>(a.out)[r * a.out_ld + j] = (gate * s) * (lin + 1.0);
+}
+
+__global__ __launch_bounds__(256) void softcap_kernel_f64(const RowsArgs a) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.M * a.N) return;
+  const int64_t r = idx / a.N;
+  const int c = (int)(idx - r * a.N);
+  const double cap = a.d0;
+  const double x = static_cast<const double*>(a.x)[r * a.x_ld + c];
+  static_cast<double*>(a.out)[r * a.out_ld + c] = cap * tanh(x / cap);
 }
 
 namespace {
@@ -667,7 +757,9 @@ int launch_lm_head(const LmHeadArgs& a, hipStream_t s) {
     if (n_ == 0) return DG_OK;                                                                \
     const int64_t blocks_ = (n_ + 255) / 256;                                                 \
     DG_REQUIRE(blocks_ <= 0x7fffffffLL, DG_EINVAL, #K ": too many elements (%lld)", (long long)n_); \
-    if ((dtype) == DG_F32)                                                                    \
+    if ((dtype) == DG_F64)                                                                    \
+      hipLaunchKernelGGL(K##_f64, dim3((unsigned)blocks_), dim3(256), 0, (s), (a));           \
+    else if ((dtype) == DG_F32)                                                               \
       hipLaunchKernelGGL(K<float>, dim3((unsigned)blocks_), dim3(256), 0, (s), (a));          \
     else if ((dtype) == DG_BF16)                                                              \
       hipLaunchKernelGGL(K<bf16_t>, dim3((unsigned)blocks_), dim3(256), 0, (s), (a));         \
@@ -677,6 +769,8 @@ int launch_lm_head(const LmHeadArgs& a, hipStream_t s) {
   } while (0)
 
 bool dtype_ok(int dtype) { return dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16; }
+// the row kernels with float64 forms (dg_attn_res_norm, dg_gate, dg_swiglu, dg_softcap)
+bool dtype_ok_f64(int dtype) { return dtype_ok(dtype) || dtype == DG_F64; }
 
 }  // namespace
 }  // namespace dg
@@ -688,7 +782,7 @@ extern "C" int dg_attn_res_norm(int64_t M, int C, int dtype, int nsrc, const voi
                                 void* stream) {
   DG_REQUIRE(M >= 0 && C >= 1, DG_EINVAL, "attn_res_norm: bad sizes M=%lld C=%d", (long long)M, C);
   DG_REQUIRE(C <= 2048, DG_EUNSUPPORTED, "attn_res_norm: C=%d > 2048", C);
-  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "attn_res_norm: dtype %d unsupported", dtype);
+  DG_REQUIRE(dtype_ok_f64(dtype), DG_EUNSUPPORTED, "attn_res_norm: dtype %d unsupported", dtype);
   DG_REQUIRE(nsrc >= 1 && nsrc <= kMaxResSources, DG_EINVAL, "attn_res_norm: %d sources (1..%d)", nsrc,
              kMaxResSources);
   if (M == 0) return DG_OK;
@@ -709,6 +803,11 @@ extern "C" int dg_attn_res_norm(int64_t M, int C, int dtype, int nsrc, const voi
   a.nsrc = nsrc;
   a.N = C;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == DG_F64) {
+    DG_REQUIRE((M + 3) / 4 <= 0x7fffffffLL, DG_EINVAL, "attn_res_norm: too many rows (%lld)", (long long)M);
+    hipLaunchKernelGGL(attn_res_norm_f64_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, a);
+    return check_launch("attn_res_norm_f64_kernel");
+  }
   const int npad = pow2_at_least(C);
   if (dtype == DG_F32) return res_pick<float>(npad, a, s);
   if (dtype == DG_BF16) return res_pick<bf16_t>(npad, a, s);
@@ -718,7 +817,7 @@ extern "C" int dg_attn_res_norm(int64_t M, int C, int dtype, int nsrc, const voi
 extern "C" int dg_gate(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g,
                        int64_t g_ld, void* out, int64_t out_ld, void* stream) {
   DG_REQUIRE(M >= 0 && C >= 1, DG_EINVAL, "gate: bad sizes M=%lld C=%d", (long long)M, C);
-  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "gate: dtype %d unsupported", dtype);
+  DG_REQUIRE(dtype_ok_f64(dtype), DG_EUNSUPPORTED, "gate: dtype %d unsupported", dtype);
   if (M == 0) return DG_OK;
   DG_REQUIRE(y != nullptr && g != nullptr && out != nullptr, DG_EINVAL, "gate: NULL pointer");
   DG_REQUIRE(y_ld >= C && g_ld >= C && out_ld >= C, DG_EINVAL, "gate: row stride smaller than C");
@@ -729,31 +828,33 @@ extern "C" int dg_gate(int64_t M, int C, int dtype, const void* y, int64_t y_ld,
 }
 
 extern "C" int dg_swiglu(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
-                         int64_t out_ld, float alpha, float limit, void* stream) {
+                         int64_t out_ld, double alpha, double limit, void* stream) {
   DG_REQUIRE(M >= 0 && N >= 1, DG_EINVAL, "swiglu: bad sizes M=%lld N=%d", (long long)M, N);
-  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "swiglu: dtype %d unsupported", dtype);
+  DG_REQUIRE(dtype_ok_f64(dtype), DG_EUNSUPPORTED, "swiglu: dtype %d unsupported", dtype);
   if (M == 0) return DG_OK;
   DG_REQUIRE(x != nullptr && out != nullptr, DG_EINVAL, "swiglu: NULL pointer");
   DG_REQUIRE(x_ld >= 2 * (int64_t)N && out_ld >= N, DG_EINVAL, "swiglu: row stride too small");
   RowsArgs a{};
   a.x = x; a.out = out;
   a.x_ld = x_ld; a.out_ld = out_ld; a.M = M; a.N = N;
-  a.p0 = alpha; a.p1 = limit;
+  a.p0 = (float)alpha; a.p1 = (float)limit;
+  a.d0 = alpha; a.d1 = limit;
   DG_LAUNCH_ROWS(swiglu_kernel, dtype, a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int dg_softcap(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
-                          int64_t out_ld, float cap, void* stream) {
+                          int64_t out_ld, double cap, void* stream) {
   DG_REQUIRE(M >= 0 && N >= 1, DG_EINVAL, "softcap: bad sizes M=%lld N=%d", (long long)M, N);
-  DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "softcap: dtype %d unsupported", dtype);
-  DG_REQUIRE(cap > 0.f, DG_EINVAL, "softcap: cap must be positive (got %g)", (double)cap);
+  DG_REQUIRE(dtype_ok_f64(dtype), DG_EUNSUPPORTED, "softcap: dtype %d unsupported", dtype);
+  DG_REQUIRE(cap > 0.0, DG_EINVAL, "softcap: cap must be positive (got %g)", cap);
   if (M == 0) return DG_OK;
   DG_REQUIRE(x != nullptr && out != nullptr, DG_EINVAL, "softcap: NULL pointer");
   DG_REQUIRE(x_ld >= N && out_ld >= N, DG_EINVAL, "softcap: row stride smaller than N");
   RowsArgs a{};
   a.x = x; a.out = out;
   a.x_ld = x_ld; a.out_ld = out_ld; a.M = M; a.N = N;
-  a.p0 = cap;
+  a.p0 = (float)cap;
+  a.d0 = cap;
   DG_LAUNCH_ROWS(softcap_kernel, dtype, a, static_cast<hipStream_t>(stream));
 }
 

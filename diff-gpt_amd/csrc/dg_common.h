@@ -538,6 +538,8 @@ int check_launch(const char* what);
 // pair alignment: one pair per lane up to DPAD = 128, beyond that read pair
 // by pair (load_slice with PAIRS).
 constexpr int kMaxHeadDim = 1024;
+// Bytes per element of a dg_dtype.
+inline int64_t dtype_bytes(int dtype) { return dtype == DG_F64 ? 8 : dtype == DG_F32 ? 4 : 2; }
 constexpr int vec_slice_epl(int dpad, int es) {
   const int e = 16 / es < dpad ? 16 / es : dpad;
   return dpad / 64 > e ? dpad / 64 : e;

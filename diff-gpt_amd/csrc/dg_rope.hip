@@ -180,11 +180,109 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const RowNormArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// float64 rows (a GPT.double() model).  rope.py:20-27 rounds x to fp32
+// (x.float()) and multiplies by the table in the promoted dtype of the two:
+// with a float64 table (GPT.double() converts the buffer) two rounded
+// products and a rounded sum or difference in float64; with an fp32 table the
+// same in fp32, converted exactly to float64 (type_as).  The QK-norm is
+// F.rms_norm on float64 rows: x / sqrt(mean(x^2) + DBL_EPSILON) in float64.
+// One wave per row; lane l holds pairs l, l + 64, ... (D <= 1024: at most 8),
+// so every load and store of a wave covers consecutive pairs.
+// ---------------------------------------------------------------------------
+constexpr int kF64RopePairs = 8;  // 1024 / 2 / 64
+
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <typename FT>
+__global__ __launch_bounds__(256) void rope_qknorm_f64_kernel(const RopeArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // whole waves leave; no barriers follow
+  int64_t pos = 0;
+  if (a.pos_dev != nullptr) {  // uniform over the grid
+    pos = *a.pos_dev;
+    if (pos < a.min_pos || pos >= a.max_pos) return;
+  }
+  const uint32_t r32 = (uint32_t)row;  // the host keeps B*T*H below 2^31
+  const int h = (int)(r32 % (uint32_t)a.H);
+  const uint32_t bt = r32 / (uint32_t)a.H;
+  const int t = (int)(bt % (uint32_t)a.T);
+  const int64_t b = (int64_t)(bt / (uint32_t)a.T);
+  const int npairs = a.D / 2;
+  const FT* f = static_cast<const FT*>(a.freqs) + pos * a.fpos + b * a.fb + (int64_t)t * a.ft + (int64_t)h * a.fh;
+  for (int w = 0; w < 3; ++w) {
+    if (a.src[w] == nullptr) continue;  // uniform over the grid
+    const double* sp = static_cast<const double*>(a.src[w]) + b * a.sb[w] + (int64_t)t * a.st[w] + (int64_t)h * a.sh[w];
+    double* dp = static_cast<double*>(a.dst[w]) + pos * a.pstep[w] + b * a.db[w] + (int64_t)t * a.dt[w] +
+                 (int64_t)h * a.dh[w];
+    double re[kF64RopePairs], im[kF64RopePairs];
+#pragma unroll
+    for (int j = 0; j < kF64RopePairs; ++j) {
+      const int p = lane + 64 * j;
+      re[j] = p < npairs ? sp[2 * p] : 0.0;
+      im[j] = p < npairs ? sp[2 * p + 1] : 0.0;
+    }
+    if (w < 2) {
+      double ss = 0.0;
+#pragma unroll
+      for (int j = 0; j < kF64RopePairs; ++j) {
+        const int p = lane + 64 * j;
+        // FT is the arithmetic type: float * float stays fp32, float * double
+        // promotes to float64
+        const FT c = p < npairs ? f[2 * p] : FT(0);
+        const FT sn = p < npairs ? f[2 * p + 1] : FT(0);
+        const FT xr = (FT)(float)re[j], xi = (FT)(float)im[j];
+        const FT a0 = xr * c, a1 = xi * sn, b0 = xr * sn, b1 = xi * c;
+        re[j] = (double)(a0 - a1);
+        im[j] = (double)(b0 + b1);
+        ss += re[j] * re[j] + im[j] * im[j];
+      }
+      if (a.qknorm) {
+        const double r = 1.0 / sqrt(wave_sum_f64(ss) / (double)a.D + DBL_EPSILON);
+#pragma unroll
+        for (int j = 0; j < kF64RopePairs; ++j) {
+          re[j] *= r;
+          im[j] *= r;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kF64RopePairs; ++j) {
+      const int p = lane + 64 * j;
+      if (p < npairs) {
+        dp[2 * p] = re[j];
+        dp[2 * p + 1] = im[j];
+      }
+    }
+  }
+}
+
+// Row RMSNorm in float64 (rms_norm.py:5-7 on float64 rows): one wave per row,
+// two passes over the row (N <= 8192).
+__global__ __launch_bounds__(256) void rms_norm_f64_kernel(const RowNormArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.M) return;
+  const double* x = static_cast<const double*>(a.x) + row * a.x_ld;
+  double* o = static_cast<double*>(a.out) + row * a.out_ld;
+  double ss = 0.0;
+  for (int c = lane; c < a.N; c += 64) ss += x[c] * x[c];
+  const double r = 1.0 / sqrt(wave_sum_f64(ss) / (double)a.N + DBL_EPSILON);
+  for (int c = lane; c < a.N; c += 64) o[c] = x[c] * r;
+}
+
+// ---------------------------------------------------------------------------
 // Host dispatch
 // ---------------------------------------------------------------------------
 namespace {
 
-int elem_size(int dtype) { return dtype == DG_F32 ? 4 : 2; }
+int elem_size(int dtype) { return (int)dtype_bytes(dtype); }
 
 bool aligned(const void* p, int64_t bytes) {
   return p == nullptr || (reinterpret_cast<uintptr_t>(p) % (uintptr_t)bytes) == 0;
@@ -312,7 +410,7 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
                const int64_t (&pstep)[3], int64_t fpos, void* stream) {
   DG_REQUIRE(B >= 0 && T >= 0 && H >= 0, DG_EINVAL, "rope: negative size");
   DG_REQUIRE(D >= 2 && D % 2 == 0, DG_EINVAL, "rope: head_dim must be even and >= 2 (got %d)", D);
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "rope: dtype %d unsupported", dtype);
   DG_REQUIRE(freqs_dtype == DG_F32 || freqs_dtype == dtype, DG_EUNSUPPORTED,
              "rope: freqs dtype must be fp32 or equal to the data dtype");
@@ -339,6 +437,36 @@ int rope_entry(int B, int T, int H, int D, int dtype, const void* q, const dg_st
   const int fes = elem_size(freqs_dtype);
   const int dpad = next_pow2(D);
   DG_REQUIRE(D <= kMaxHeadDim, DG_EUNSUPPORTED, "rope: head_dim %d > %d", D, kMaxHeadDim);
+  if (dtype == DG_F64) {
+    // element-aligned float64 rows, one wave per row (rope_qknorm_f64_kernel)
+    for (int w = 0; w < 3; ++w)
+      DG_REQUIRE(aligned(src[w], 8) && aligned(dst[w], 8), DG_EINVAL, "rope: float64 rows must be 8-byte aligned");
+    DG_REQUIRE(!need_freqs || aligned(freqs, fes), DG_EINVAL, "rope: freqs not aligned to its element size");
+    const int64_t rows = (int64_t)B * T * H;
+    DG_REQUIRE(rows < 0x7fffffffLL, DG_EINVAL, "rope: B*T*H = %lld rows, at most 2^31 - 1", (long long)rows);
+    RopeArgs a{};
+    for (int w = 0; w < 3; ++w) {
+      a.src[w] = src[w];
+      a.dst[w] = dst[w];
+      if (src[w]) {
+        a.sb[w] = sst[w]->b;  a.st[w] = sst[w]->t;  a.sh[w] = sst[w]->h;
+        a.db[w] = dst_st[w]->b; a.dt[w] = dst_st[w]->t; a.dh[w] = dst_st[w]->h;
+      }
+      a.pstep[w] = pstep[w];
+    }
+    a.freqs = freqs;
+    if (f_st) { a.fb = f_st->b; a.ft = f_st->t; a.fh = f_st->h; }
+    a.rows = rows;
+    a.T = T; a.H = H; a.D = D;
+    a.qknorm = (flags & DG_QKNORM) ? 1 : 0;
+    a.pos_dev = pos_dev; a.min_pos = min_pos; a.max_pos = max_pos;
+    a.fpos = fpos;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (freqs_dtype == DG_F32) hipLaunchKernelGGL(rope_qknorm_f64_kernel<float>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(rope_qknorm_f64_kernel<double>, grid, dim3(256), 0, s, a);
+    return check_launch("rope_qknorm_f64_kernel");
+  }
 
   // Vector slices (16 bytes of data per lane, or the whole row when it is
   // shorter) where D is a multiple of them and every pointer / stride
@@ -456,7 +584,7 @@ extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x
                            int64_t out_ld, void* stream) {
   DG_REQUIRE(M >= 0 && N >= 1, DG_EINVAL, "rms_norm: bad sizes M=%lld N=%d", (long long)M, N);
   DG_REQUIRE(N <= 8192, DG_EUNSUPPORTED, "rms_norm: N=%d > 8192", N);
-  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16 || dtype == DG_F64, DG_EUNSUPPORTED,
              "rms_norm: dtype %d unsupported", dtype);
   if (M == 0) return DG_OK;
   DG_REQUIRE(x != nullptr && out != nullptr, DG_EINVAL, "rms_norm: NULL pointer");
@@ -469,6 +597,11 @@ extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x
   a.M = M;
   a.N = N;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == DG_F64) {
+    DG_REQUIRE((M + 3) / 4 <= 0x7fffffffLL, DG_EINVAL, "rms_norm: too many rows (%lld)", (long long)M);
+    hipLaunchKernelGGL(rms_norm_f64_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, s, a);
+    return check_launch("rms_norm_f64_kernel");
+  }
   const int npad = next_pow2(N);
   if (dtype == DG_F32) return rms_pick<float>(npad, a, s);
   if (dtype == DG_BF16) return rms_pick<bf16_t>(npad, a, s);

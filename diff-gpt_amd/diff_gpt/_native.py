@@ -27,11 +27,11 @@ LIB_PATH = Path(
     )
 )
 
-DG_F32, DG_BF16, DG_F16 = 0, 1, 2
+DG_F32, DG_BF16, DG_F16, DG_F64 = 0, 1, 2, 3
 DG_QKNORM = 1
 DG_KEYS_NORMED = 2
 DG_EUNSUPPORTED = -2
-_DTYPE_CODE = {torch.float32: DG_F32, torch.bfloat16: DG_BF16, torch.float16: DG_F16}
+_DTYPE_CODE = {torch.float32: DG_F32, torch.bfloat16: DG_BF16, torch.float16: DG_F16, torch.float64: DG_F64}
 
 
 class Stride3(ctypes.Structure):
@@ -168,12 +168,12 @@ _SIGNATURES = {
     "dg_swiglu": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-         ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p],
+         ctypes.c_int64, ctypes.c_double, ctypes.c_double, ctypes.c_void_p],
     ),
     "dg_softcap": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
-         ctypes.c_int64, ctypes.c_float, ctypes.c_void_p],
+         ctypes.c_int64, ctypes.c_double, ctypes.c_void_p],
     ),
     "dg_block_out": (
         ctypes.c_int,
@@ -185,7 +185,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # head_dim the kernels take: every even size up to 1024 (a row padded to the
 # next power of two spreads over at most 64 lanes of 16 elements)
@@ -229,7 +229,7 @@ def _dtype_code(t: torch.Tensor) -> int:
         return _DTYPE_CODE[t.dtype]
     except KeyError:
         raise TypeError(
-            f"dgattn supports float32/bfloat16/float16 tensors, got {t.dtype}"
+            f"dgattn supports float32/bfloat16/float16/float64 tensors, got {t.dtype}"
         ) from None
 
 

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define DG_ABI_VERSION 2
+#define DG_ABI_VERSION 3
 
 #if defined(__GNUC__)
 #define DG_API __attribute__((visibility("default")))
@@ -44,8 +44,17 @@ extern "C" {
 #endif
 
 /* Element types.  The reference computes in the model's dtype (fp32, or bf16
- * after GPT.to(torch.bfloat16)); fp16 is accepted as well. */
-enum dg_dtype { DG_F32 = 0, DG_BF16 = 1, DG_F16 = 2 };
+ * after GPT.to(torch.bfloat16)); fp16 and fp64 (a GPT.double() model) are
+ * accepted as well.  fp64 runs on plain vector-ALU kernels in fp64 arithmetic
+ * (the RoPE rotation of fp32-rounded inputs, as rope.py:20 does), taken by
+ * dg_rope_qknorm_append(_at), dg_attention(_grouped), dg_decode_attention_at,
+ * dg_decode_step (two launches), dg_rms_norm, dg_attn_res_norm, dg_gate,
+ * dg_swiglu, dg_softcap and dg_copy4d; the other entry points return
+ * DG_EUNSUPPORTED for it.  The attention scale is an fp32 argument: with
+ * fp64 data its rounding of 1/sqrt(D) (SDPA's default) stands for 1/sqrt(D)
+ * in fp64, any other scale acts as its fp32 value.  ABI version 3 added
+ * DG_F64 and made dg_swiglu's alpha / limit and dg_softcap's cap double. */
+enum dg_dtype { DG_F32 = 0, DG_BF16 = 1, DG_F16 = 2, DG_F64 = 3 };
 
 enum dg_status {
   DG_OK = 0,
@@ -113,8 +122,10 @@ DG_API int dg_rope_qknorm_append(int B, int T, int H, int D, int dtype,
  * KV cache: strides b=H*Tcap*D, t=D, h=Tcap*D), y a (B,Tq,H,D) view.  Query i
  * sees key j iff j <= i + (Tk - Tq): this is is_causal=True when Tq == Tk
  * (mha.py:64), the unmasked single-query decode when Tq == 1 (mha.py:68) and
- * the bottom-right chunk mask otherwise (mha.py:69-81).  Softmax in fp32.
- * scale is the SDPA scale (the reference uses the default 1/sqrt(D)).
+ * the bottom-right chunk mask otherwise (mha.py:69-81).  Softmax in fp32
+ * (in fp64 for fp64 data).
+ * scale is the SDPA scale (the reference uses the default 1/sqrt(D); see
+ * dg_dtype for its meaning with fp64 data).
  * Prefills (Tq >= 16) at D = 64 or 128 with 16-byte aligned rows run on the
  * matrix cores: bf16 / fp16 products with fp32 accumulation, fp32 inputs on
  * fp32 products and accumulation; other shapes on the vector kernel, which
@@ -381,11 +392,11 @@ DG_API int dg_gate(int64_t M, int C, int dtype, const void* y, int64_t y_ld, con
  * out[j] = gate * sigmoid(alpha * gate) * (lin + 1).
  */
 DG_API int dg_swiglu(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
-              int64_t out_ld, float alpha, float limit, void* stream);
+              int64_t out_ld, double alpha, double limit, void* stream);
 
 /* Logit soft cap cap * tanh(x / cap) (gpt.py:182-186); out may alias x. */
 DG_API int dg_softcap(int64_t M, int N, int dtype, const void* x, int64_t x_ld, void* out,
-               int64_t out_ld, float cap, void* stream);
+               int64_t out_ld, double cap, void* stream);
 
 /*
  * lm_head + logit soft cap + greedy argmax in one launch (gpt.py:181-186 and

@@ -7,7 +7,9 @@ Floating-point conventions:
   * arrays hold float32 values; "bf16"/"f16" tensors are float32 arrays whose
     values are exactly representable in that format (round_to() produces them);
   * float32 numpy arithmetic rounds every operation (no fused multiply-add),
-    which is the RoPE / norm contract of the HIP kernels.
+    which is the RoPE / norm contract of the HIP kernels;
+  * the float64-model functions (rope_f64, rms_norm_f64) take and return
+    float64 arrays.
 """
 
 from __future__ import annotations
@@ -124,6 +126,46 @@ def rms_norm(x: np.ndarray, dtype: str) -> np.ndarray:
 def rope_qknorm(x: np.ndarray, cs: np.ndarray, dtype: str) -> np.ndarray:
     """mha.py:44-48 for one of q / k: rope, round to dtype, then rms_norm."""
     return rms_norm(rope(x, cs, dtype), dtype)
+
+
+# ---------------------------------------------------------------------------
+# float64 models (GPT.double()): rope.py:20-27 and rms_norm.py:5-7 on float64
+# ---------------------------------------------------------------------------
+
+DBL_EPS = np.finfo(np.float64).eps  # F.rms_norm eps=None for float64
+
+
+def rope_f64(x: np.ndarray, cs: np.ndarray) -> np.ndarray:
+    """apply_rotary_emb on float64 rows (rope.py:20-27): x.float() rounds x to
+    fp32; the products and the sum / difference are evaluated in the promoted
+    dtype of fp32 and the table -- float64 for a float64 table (GPT.double()
+    converts the buffer), fp32 for an fp32 one -- each operation rounded
+    (no fused multiply-add); type_as returns float64 exactly.
+
+    Pinned by: torch's own type promotion of the same expression on the CPU
+    for both table dtypes (tests/test_oracle.py), the x.float() rounding on a
+    float64 input that fp32 cannot hold, and the quarter turn (1, 0) -> (0, 1)
+    of test_rope.py:14-35."""
+    ct = np.float64 if np.asarray(cs).dtype == np.float64 else np.float32
+    x32 = np.asarray(x, dtype=np.float64).astype(np.float32).astype(ct)
+    cs = np.asarray(cs, dtype=ct)
+    pairs = x32.reshape(*x32.shape[:-1], -1, 2)
+    re, im = pairs[..., 0], pairs[..., 1]
+    c, s = cs[..., 0], cs[..., 1]
+    out = np.stack([(re * c) - (im * s), (re * s) + (im * c)], axis=-1)
+    return out.reshape(x32.shape).astype(np.float64)
+
+
+def rms_norm_f64(x: np.ndarray) -> np.ndarray:
+    """F.rms_norm(x, (N,)) on float64 rows: x / sqrt(mean(x^2) + DBL_EPSILON).
+    The summation order is numpy's, so the kernels agree within a few float64
+    ulps, not bit for bit.
+
+    Pinned by: torch.nn.functional.rms_norm in float64 on the CPU and unit RMS
+    of the result (tests/test_oracle.py)."""
+    x = np.asarray(x, dtype=np.float64)
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + DBL_EPS)
 
 
 # ---------------------------------------------------------------------------

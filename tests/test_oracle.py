@@ -155,6 +155,46 @@ def test_rms_norm_invariants():
     assert np.allclose(on.rms_norm(5 * x, "f32"), y, atol=1e-5, rtol=1e-4)
 
 
+# ---------------------------------------------------------------- float64 models
+
+
+@pytest.mark.parametrize("table", [torch.float64, torch.float32])
+def test_rope_f64_matches_torch_type_promotion(table):
+    """rope.py:20-27 on float64 rows, run by torch on the CPU: x.float() then
+    the table's promotion (float64 table: float64 products; fp32 table: fp32
+    products, widened by type_as).  Bit for bit for both table dtypes, and the
+    two differ, so a mistaken promotion fails one of them."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(3, 9, 4, 24, generator=g, dtype=torch.float64) * 3
+    theta = torch.randn(1, 9, 1, 12, generator=g, dtype=torch.float64) * 4
+    fc = torch.stack([theta.cos(), theta.sin()], dim=-1).to(table)
+    ref = tr.rope(x, fc).numpy()
+    assert tr.rope(x, fc).dtype == torch.float64
+    ours = on.rope_f64(x.numpy(), fc.numpy())
+    assert np.array_equal(ours.view(np.uint64), ref.view(np.uint64))
+    other = on.rope_f64(x.numpy(), fc.numpy().astype(np.float32 if table == torch.float64 else np.float64))
+    assert not np.array_equal(other, ours)
+
+
+def test_rope_f64_rounds_input_to_fp32_and_quarter_turn():
+    # x.float(): 1 + 2^-40 is 1.0 in fp32, so angle 0 returns exactly 1.0
+    out = on.rope_f64(np.array([1.0 + 2**-40, 0.0]), np.array([[1.0, 0.0]]))
+    assert out[0] == 1.0 and out[1] == 0.0
+    # test_rope.py:14-35: (1, 0) by pi/2 -> (cos, sin) of pi/2 in float64
+    out = on.rope_f64(np.array([1.0, 0.0]), np.array([[math.cos(math.pi / 2), math.sin(math.pi / 2)]]))
+    assert abs(out[0]) < 1e-16 and out[1] == 1.0
+
+
+@pytest.mark.parametrize("n", [6, 64, 1000])
+def test_rms_norm_f64_against_torch(n):
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(129, n, generator=g, dtype=torch.float64) * 5
+    ref = F.rms_norm(x, (n,)).numpy()
+    ours = on.rms_norm_f64(x.numpy())
+    assert np.abs(ours - ref).max() <= 8 * np.finfo(np.float64).eps * np.abs(ref).max()
+    assert np.allclose(np.sqrt((ours ** 2).mean(-1)), 1.0, rtol=0, atol=1e-14)
+
+
 # ---------------------------------------------------------------- attention
 
 
