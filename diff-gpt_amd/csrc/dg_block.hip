@@ -459,37 +459,31 @@ __device__ __forceinline__ f32x4_t layer_tile(const TileW<T, K>& f, const T* x, 
 // rms_norm(block_attn_res(V, w)) of the 16 rows into LDS xn, with
 // attn_res_norm_kernel's arithmetic; 16 lanes per row (CH = C / 16 elements
 // each).  Sources 0 .. nmem-1 are rows of global tensors; with last != null
-// the last source is that LDS matrix.  The first res_held<CH>() sources are
-// loaded into registers together, up front, and serve both passes.
-
+// the last source is that LDS matrix.  The caller has loaded the first
+// res_held<CH>() global sources (held) and the lane's slice of the
+// pseudo-query (w) into registers at the start of the kernel; they serve both
+// passes, further global sources and the LDS one are read where used.
 template <typename T, int C>
 __device__ __forceinline__ void layer_mixture(const void* const* src, const int64_t* ld, int nmem, const T* last,
-                                              const void* w_mix, int64_t row0, int64_t M, T* xn) {
+                                              const float (&held)[res_held<C / 16>()][C / 16],
+                                              const float (&w)[C / 16], int64_t row0, int64_t M, T* xn) {
 #pragma clang fp contract(off)
   constexpr int CH = C / 16;
   constexpr int G = 16;
+  constexpr int HELD = res_held<CH>();
   const int r = threadIdx.x / G, sub = threadIdx.x % G, c0 = sub * CH;
   const int64_t row = min(row0 + r, M - 1);  // rows past M: a finite copy, never stored
   const int nsrc = nmem + (last != nullptr ? 1 : 0);
-  auto load = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
-    if (n < nmem) load_vec<T, CH>(static_cast<const T*>(src[n]) + row * ld[n] + c0, x);
-    else load_vec<T, CH>(last + r * lds_ld<T, C>() + c0, x);
-  };
-  constexpr int HELD = res_held<CH>();
-  float held[HELD][CH];
-#pragma unroll
-  for (int n = 0; n < HELD; ++n)
-    if (n < nsrc) load(n, held[n]);  // uniform; no use before all are issued
   auto get = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
-    if (n < HELD) {
+    if (n < HELD && n < nmem) {
 #pragma unroll
       for (int i = 0; i < CH; ++i) x[i] = held[n][i];
+    } else if (n < nmem) {
+      load_vec<T, CH>(static_cast<const T*>(src[n]) + row * ld[n] + c0, x);
     } else {
-      load(n, x);
+      load_vec<T, CH>(last + r * lds_ld<T, C>() + c0, x);
     }
   };
-  float w[CH];
-  load_vec<T, CH>(static_cast<const T*>(w_mix) + c0, w);
   float score[kMaxResSources];
   float mx = -INFINITY;
 #pragma unroll
@@ -534,11 +528,28 @@ __device__ __forceinline__ void layer_mixture(const void* const* src, const int6
   store_vec<T, CH>(xn + r * lds_ld<T, C>() + c0, h);
 }
 
+// FFN weight fragments loaded at the start of block_out_kernel: at C = 64 in
+// 16-bit types all of a wave's up and down tiles (72 registers); otherwise
+// the first up tile, each later one fetched while the one before runs, and
+// the down tiles behind the last up tile (fp32 fragments are twice the
+// registers, and loading all of them up front measured slower).
+template <typename T, int C>
+constexpr int block_up_depth() {
+  return (C == 64 && sizeof(T) == 2) ? C / 16 : 1;
+}
+
 template <typename T, int C>
 __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
 #pragma clang fp contract(off)
   constexpr int LDC = lds_ld<T, C>(), LDH = lds_ld<T, 2 * C>();
   constexpr int CH = C / 16;
+  constexpr int NPJ = C / 64;  // c_proj tiles per wave (C / 16 tiles over 4 waves)
+  constexpr int NUP = C / 16;  // FFN-up tiles per wave (4C / 16 over 4 waves)
+  constexpr int NDN = C / 64;  // FFN-down tiles per wave
+  constexpr int UPD = block_up_depth<T, C>();
+  constexpr bool kDownAtStart = UPD == NUP;  // else the down fragments follow the up tiles
+  constexpr int NDP = kDownAtStart ? NDN : 1;
+  constexpr int HELD = res_held<CH>();
   __shared__ __attribute__((aligned(16))) T ga[kLayerRows * LDC];  // gated attention output, then xn
   __shared__ __attribute__((aligned(16))) T pm[kLayerRows * LDC];  // the partial sum after the attention
   __shared__ __attribute__((aligned(16))) T hh[kLayerRows * LDH];  // SwiGLU output
@@ -549,37 +560,59 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   const T* w_proj = static_cast<const T*>(a.w_proj);
   const T* w_up = static_cast<const T*>(a.w_up);
   const T* w_down = static_cast<const T*>(a.w_down);
-  // the wave's first c_proj and FFN-up weight fragments go out before the
-  // gate's loads
-  TileW<T, C> wp, wu;
-  load_tile_w<T, C>(wp, w_proj, a.wp_ld, wv, lane);  // C / 16 >= 4 tiles: every wave has one
-  load_tile_w<T, C>(wu, w_up, a.wu_ld, wv, lane);
-  // 1) gate (gate_kernel's arithmetic): 16 lanes per row
-  {
-    const int r = threadIdx.x / 16, c0 = (threadIdx.x % 16) * CH;
-    const int64_t row = min(row0 + r, a.M - 1);
-    float y[CH], gl[CH];
-    load_vec<T, CH>(static_cast<const T*>(a.y) + row * a.y_ld + c0, y);
-    load_vec<T, CH>(static_cast<const T*>(a.g) + row * a.g_ld + c0, gl);
+
+  // Every global operand of the wave goes out here, in the order the stages
+  // use them, so that the stages wait on LDS and the matrix cores instead of
+  // one memory round trip each: the gate's rows (16 lanes per row), the
+  // c_proj fragments and the partial sum entering the layer (matrix-core
+  // lane mapping), the mixture's committed blocks and pseudo-query (16 lanes
+  // per row), the FFN fragments.
+  const int gr = threadIdx.x / 16, gc0 = (threadIdx.x % 16) * CH;
+  const int64_t grow = min(row0 + gr, a.M - 1);  // rows past M: a finite copy, never stored
+  const int64_t crow = min(row0 + c, a.M - 1);
+  float y[CH], gl[CH];
+  load_vec<T, CH>(static_cast<const T*>(a.y) + grow * a.y_ld + gc0, y);
+  load_vec<T, CH>(static_cast<const T*>(a.g) + grow * a.g_ld + gc0, gl);
+  TileW<T, C> wp[NPJ];
 #pragma unroll
-    for (int i = 0; i < CH; ++i) y[i] = y[i] * rt<T>(sigmoid_f32(gl[i]));
-    store_vec<T, CH>(ga + r * LDC + c0, y);
+  for (int j = 0; j < NPJ; ++j) load_tile_w<T, C>(wp[j], w_proj, a.wp_ld, wv + 4 * j, lane);
+  float pin[NPJ][4];
+  if (a.pin != nullptr) {  // uniform
+#pragma unroll
+    for (int j = 0; j < NPJ; ++j)
+      load_vec<T, 4>(static_cast<const T*>(a.pin) + crow * a.pin_ld + 16 * (wv + 4 * j) + 4 * g, pin[j]);
   }
+  float held[HELD][CH];
+#pragma unroll
+  for (int n = 0; n < HELD; ++n)
+    if (n < a.nblk) load_vec<T, CH>(static_cast<const T*>(a.blk[n]) + grow * a.blk_ld[n] + gc0, held[n]);  // uniform
+  float wmix[CH];
+  load_vec<T, CH>(static_cast<const T*>(a.w_mix) + gc0, wmix);
+  TileW<T, C> wu[UPD];
+#pragma unroll
+  for (int j = 0; j < UPD; ++j) load_tile_w<T, C>(wu[j], w_up, a.wu_ld, wv + 4 * j, lane);
+  TileW<T, 2 * C> wd[NDP];
+  if constexpr (kDownAtStart) {
+#pragma unroll
+    for (int j = 0; j < NDN; ++j) load_tile_w<T, 2 * C>(wd[j], w_down, a.wd_ld, wv + 4 * j, lane);
+  }
+  // keep the scheduler from sinking the loads toward their uses
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 1) gate (gate_kernel's arithmetic)
+#pragma unroll
+  for (int i = 0; i < CH; ++i) y[i] = y[i] * rt<T>(sigmoid_f32(gl[i]));
+  store_vec<T, CH>(ga + gr * LDC + gc0, y);
   __syncthreads();
   // 2) c_proj, then the partial sum
-  const int64_t crow = min(row0 + c, a.M - 1);
-  for (int t = wv; t < C / 16; t += 4) {
-    TileW<T, C> next;
-    if (t + 4 < C / 16) load_tile_w<T, C>(next, w_proj, a.wp_ld, t + 4, lane);
-    const f32x4_t acc = layer_tile<T, C>(wp, ga, lane);
-    wp = next;
-    const int f = 16 * t + 4 * g;
+#pragma unroll
+  for (int j = 0; j < NPJ; ++j) {
+    const f32x4_t acc = layer_tile<T, C>(wp[j], ga, lane);
+    const int f = 16 * (wv + 4 * j) + 4 * g;
     float p[4];
     if (a.pin != nullptr) {
-      float pi[4];
-      load_vec<T, 4>(static_cast<const T*>(a.pin) + crow * a.pin_ld + f, pi);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) p[i] = pi[i] + rt<T>(acc[i]);
+      for (int i = 0; i < 4; ++i) p[i] = pin[j][i] + rt<T>(acc[i]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) p[i] = acc[i];
@@ -589,18 +622,20 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   __syncthreads();
   // 3) the MLP's mixture over the committed blocks and the new partial; its
   //    norm overwrites the gated rows (no longer read)
-  layer_mixture<T, C>(a.blk, a.blk_ld, a.nblk, pm, a.w_mix, row0, a.M, ga);
+  layer_mixture<T, C>(a.blk, a.blk_ld, a.nblk, pm, held, wmix, row0, a.M, ga);
   __syncthreads();
   // 4) FFN up + SwiGLU (swiglu_kernel's arithmetic on the interleaved
-  //    (gate, linear) pairs: features 2j, 2j + 1 -> hidden j); the first
-  //    FFN-down fragment goes out with the last up tile
-  TileW<T, 2 * C> wd;
-  for (int t = wv; t < 4 * C / 16; t += 4) {
+  //    (gate, linear) pairs: features 2j, 2j + 1 -> hidden j)
+#pragma unroll
+  for (int i = 0; i < NUP; ++i) {
+    const int t = wv + 4 * i;
     TileW<T, C> next;
-    if (t + 4 < 4 * C / 16) load_tile_w<T, C>(next, w_up, a.wu_ld, t + 4, lane);
-    else load_tile_w<T, 2 * C>(wd, w_down, a.wd_ld, wv, lane);
-    const f32x4_t acc = layer_tile<T, C>(wu, ga, lane);
-    wu = next;
+    if (i + UPD < NUP) load_tile_w<T, C>(next, w_up, a.wu_ld, t + 4 * UPD, lane);
+    if constexpr (!kDownAtStart) {
+      if (i + 1 == NUP) load_tile_w<T, 2 * C>(wd[0], w_down, a.wd_ld, wv, lane);
+    }
+    const f32x4_t acc = layer_tile<T, C>(wu[i % UPD], ga, lane);
+    if (i + UPD < NUP) wu[i % UPD] = next;
     float hv[2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
@@ -615,11 +650,17 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
   // 5) FFN down + residual
   const bool store = row0 + c < a.M;
   T* orow = static_cast<T*>(a.out) + (row0 + c) * a.out_ld;
-  for (int t = wv; t < C / 16; t += 4) {
+#pragma unroll
+  for (int j = 0; j < NDN; ++j) {
+    const int t = wv + 4 * j;
     TileW<T, 2 * C> next;
-    if (t + 4 < C / 16) load_tile_w<T, 2 * C>(next, w_down, a.wd_ld, t + 4, lane);
-    const f32x4_t acc = layer_tile<T, 2 * C>(wd, hh, lane);
-    wd = next;
+    if constexpr (!kDownAtStart) {
+      if (j + 1 < NDN) load_tile_w<T, 2 * C>(next, w_down, a.wd_ld, t + 4, lane);
+    }
+    const f32x4_t acc = layer_tile<T, 2 * C>(wd[kDownAtStart ? j : 0], hh, lane);
+    if constexpr (!kDownAtStart) {
+      if (j + 1 < NDN) wd[0] = next;
+    }
     const int f = 16 * t + 4 * g;
     float pmv[4], o[4];
     load_vec<T, 4>(pm + c * LDC + f, pmv);
