@@ -169,6 +169,111 @@ __global__ __launch_bounds__(256) void attn_res_norm_kernel(const AttnResArgs a,
   }
 }
 
+// attn_res_norm_kernel for few wide rows (one row per wave there, G = 64):
+// a workgroup of 4 waves takes one row, so a decode step's few hundred rows
+// keep four times the waves in flight and each wave's dependent chain of
+// per-source reductions is a quarter as long.  Wave w scores sources w,
+// w + 4, ... (each in the lane mapping, arithmetic and reduction tree of
+// attn_res_norm_kernel, so each score has its bits); the scores meet in LDS;
+// every wave takes the softmax over them in source order; wave w forms the
+// weighted sum for a quarter of the columns (each column summed over the
+// sources in source order, as before) into LDS; wave 0 normalises the row in
+// attn_res_norm_kernel's lane mapping and stores it.  Same bits throughout.
+template <int CH>
+constexpr int res_held_split() {
+  return CH <= 8 ? 8 : 64 / CH;
+}
+
+template <typename T, int NPAD, int CH>
+__global__ __launch_bounds__(256) void attn_res_norm_split_kernel(const AttnResArgs a, const int vec) {
+#pragma clang fp contract(off)
+  constexpr int G = NPAD / CH;
+  static_assert(G == 64, "one row per wave in attn_res_norm_kernel's mapping");
+  constexpr int HELD = res_held_split<CH>();  // sources a wave holds in registers
+  constexpr int CQ = CH / 4;                  // columns per lane in the weighted sum
+  static_assert(CQ >= 1 && CQ * 4 == CH, "column split");
+  __shared__ float sc[kMaxResSources];
+  __shared__ __attribute__((aligned(16))) float hrow[NPAD];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t row = blockIdx.x;  // the host launches one workgroup per row
+  const int c0 = lane * CH;
+  float w[CH];
+  load_slice<T, CH>(static_cast<const T*>(a.w) + c0, c0, a.N, vec, w);
+  auto load = [&](int n, float (&x)[CH]) __attribute__((always_inline)) {
+    load_slice<T, CH>(static_cast<const T*>(a.src[n]) + row * a.ld[n] + c0, c0, a.N, vec, x);
+  };
+  float held[HELD][CH];
+#pragma unroll
+  for (int j = 0; j < HELD; ++j)
+    if (wv + 4 * j < a.nsrc) load(wv + 4 * j, held[j]);  // wave-uniform; no use before all are issued
+  // pass 1: this wave's scores
+#pragma unroll
+  for (int j = 0; j < kMaxResSources / 4; ++j) {
+    const int n = wv + 4 * j;
+    if (n >= a.nsrc) break;  // wave-uniform
+    float x[CH];
+    if (j < HELD) {
+#pragma unroll
+      for (int i = 0; i < CH; ++i) x[i] = held[j][i];
+    } else {
+      load(n, x);
+    }
+    row_rms<CH, G>(x, a.N);
+    float prod[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) prod[i] = rt<T>(x[i]) * w[i];
+    float dot = tree_sum<CH>(prod);
+    dot = group_sum_dpp<G>(dot);
+    if (lane == 0) sc[n] = rt<T>(dot);
+  }
+  __syncthreads();
+  // softmax over the sources (fp32 inside, rounded output), in source order
+  float mx = -INFINITY;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n)
+    if (n < a.nsrc) mx = fmaxf(mx, sc[n]);
+  float e[kMaxResSources];
+  float sum = 0.f;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n) {
+    e[n] = 0.f;
+    if (n >= a.nsrc) continue;
+    e[n] = expf(sc[n] - mx);
+    sum += e[n];
+  }
+  // pass 2: columns [16 CH wv, 16 CH (wv + 1)) of the weighted sum, CQ per lane
+  const int cq = 16 * CH * wv + lane * CQ;
+  float h[CQ];
+#pragma unroll
+  for (int i = 0; i < CQ; ++i) h[i] = 0.f;
+#pragma unroll
+  for (int n = 0; n < kMaxResSources; ++n) {
+    if (n >= a.nsrc) continue;
+    const float p = rt<T>(e[n] / sum);
+    float x[CQ];
+    load_slice<T, CQ>(static_cast<const T*>(a.src[n]) + row * a.ld[n] + cq, cq, a.N, vec, x);
+#pragma unroll
+    for (int i = 0; i < CQ; ++i) h[i] = h[i] + rt<T>(p * x[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < CQ; ++i) hrow[cq + i] = (cq + i < a.N) ? rt<T>(h[i]) : 0.f;
+  __syncthreads();
+  if (wv != 0) return;  // no barrier follows
+  float hn[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) hn[i] = hrow[c0 + i];
+  row_rms<CH, G>(hn, a.N);
+  T* os = static_cast<T*>(a.out) + row * a.out_ld + c0;
+  if (vec && c0 + CH <= a.N) {
+    store_vec<T, CH>(os, hn);
+  } else {
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+      if (c0 + i < a.N) os[i] = from_f32<T>(hn[i]);
+  }
+}
+
 // sigmoid as ATen evaluates it: 1 / (1 + exp(-x)) in fp32
 __device__ __forceinline__ float sigmoid_f32(float x) {
 #pragma clang fp contract(off)
@@ -327,6 +432,9 @@ int pow2_at_least(int x) {
   return p;
 }
 
+// rows up to which wide rows (G = 64) take attn_res_norm_split_kernel
+constexpr int64_t kResSplitRows = 4096;
+
 template <typename T, int NPAD>
 int launch_res(const AttnResArgs& a, hipStream_t s) {
   // the lane mapping of rms_norm_kernel for the same row length
@@ -341,6 +449,14 @@ int launch_res(const AttnResArgs& a, hipStream_t s) {
   bool vec = (vb == 4 || vb == 8 || vb % 16 == 0) && (CH * (int)sizeof(T)) >= 4 && al(a.w, vb) &&
              al(a.out, vb) && (a.out_ld * (int64_t)sizeof(T)) % vb == 0;
   for (int n = 0; n < a.nsrc; ++n) vec = vec && al(a.src[n], vb) && (a.ld[n] * (int64_t)sizeof(T)) % vb == 0;
+  if constexpr (G == 64 && CH % 4 == 0) {
+    // few wide rows (a decode step's): one row per workgroup of four waves
+    if (a.M <= kResSplitRows) {
+      hipLaunchKernelGGL((attn_res_norm_split_kernel<T, NPAD, CH>), dim3((unsigned)a.M), dim3(256), 0, s, a,
+                         vec ? 1 : 0);
+      return check_launch("attn_res_norm_split_kernel");
+    }
+  }
   hipLaunchKernelGGL((attn_res_norm_kernel<T, NPAD, CH>), dim3((unsigned)blocks), dim3(256), 0, s, a,
                      vec ? 1 : 0);
   return check_launch("attn_res_norm_kernel");
