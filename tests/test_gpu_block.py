@@ -75,6 +75,27 @@ def test_attn_res_norm_one_source_is_rms_norm(dev, dtype):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("C,n", [(512, 9), (1024, 5), (256, 3), (1000, 13), (2048, 2)])
+def test_attn_res_norm_split_rows_equal_single_row_kernel(dev, dtype, C, n):
+    """Up to 4096 wide rows go one row per workgroup of four waves (sources
+    scored and columns summed in parallel); more rows go one row per wave.
+    Both give the same bits: 4100 rows in one launch against their first 37
+    rows and their last 512 in launches of their own."""
+    from diff_gpt import _native
+
+    M = 4100
+    srcs = [_randn((M, C), 200 + i, dtype, 1.0 + 0.3 * i).to(dev) for i in range(n)]
+    w = _randn((1, C), 8, dtype, 0.5).to(dev)
+    ops = _native.ops()
+    full = ops.attn_res_norm(srcs, w)
+    for sl in (slice(0, 37), slice(M - 512, M)):
+        part = ops.attn_res_norm([s[sl] for s in srcs], w)
+        assert torch.equal(part, full[sl])
+    one = ops.attn_res_norm([srcs[0][:64]], w)
+    assert torch.equal(one, ops.rms_norm(srcs[0][:64]))
+
+
 def test_attn_res_norm_strided_sources(dev):
     """Sources that are column slices of wider rows (row stride > C)."""
     from diff_gpt import _native
