@@ -127,6 +127,29 @@ def test_workspace_sizes():
     assert lib.dg_attention_workspace_size(1, 1, 512, 512, 64, 1) == 0
 
 
+def test_float64_declined_where_no_float64_form():
+    """dg_prefill_rope, dg_lm_head and dg_block_out have no float64 kernels:
+    they return DG_EUNSUPPORTED (the model then makes the separate calls)
+    before touching the device; an unknown dtype code is refused everywhere."""
+    from diff_gpt import _native
+
+    lib = _native.lib()
+    nul = ctypes.c_void_p(0)
+    fake = ctypes.c_void_p(0x1000)
+    st = _s3(64, 64, 64)
+    F64 = _native.DG_F64
+    assert lib.dg_prefill_rope(1, 1, 32, 32, 64, F64, fake, st, fake, st, F64, 1, fake, st, fake, st,
+                               fake, st, 0.125, nul) == -2
+    assert lib.dg_lm_head(4, 64, 256, F64, fake, 64, fake, 64, 15.0, fake, 256, nul, nul) == -2
+    ptrs = (ctypes.c_void_p * 1)(0x1000)
+    lds = (ctypes.c_int64 * 1)(64)
+    assert lib.dg_block_out(16, 64, F64, fake, 64, fake, 64, fake, 64, nul, 0, 1, ptrs, lds, fake, fake, 64,
+                            fake, 128, 1.702, 7.0, fake, 64, nul) == -2
+    assert b"dtype" in lib.dg_last_error()
+    assert lib.dg_attention_workspace_size(1, 1, 1, 4096, 64, F64) == 0
+    assert lib.dg_rms_norm(4, 64, 4, fake, 64, fake, 64, nul) == -2
+
+
 def test_block_kernel_argument_errors():
     """The decode-step neighbour kernels reject bad sizes before any launch."""
     from diff_gpt import _native
