@@ -89,7 +89,14 @@ class Block(nn.Module):
         partial_block: torch.Tensor,
         freqs_cis: torch.Tensor,
         kv_cache: KVCache | None,
+        *,
+        _last_only: bool = False,
     ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
+        """block.py:87-107.  With _last_only the attention still runs over
+        every position (its keys and values go to the cache), and the rest of
+        the layer only for the last one: the outputs are that position's
+        (B, 1, C) rows, for a last layer whose other rows only the logits of
+        their own positions would read."""
         _native.require_device("Block", partial_block)
         xn = attn_res_norm(blocks, partial_block, self.attn_res_proj)
         committed = self._at_boundary()
@@ -100,6 +107,9 @@ class Block(nn.Module):
         qkvg = F.linear(xn, sa._projection_weight())
         y = sa._attend(qkvg, freqs_cis, kv_cache)
         g = sa._gate_logits(qkvg)
+        if _last_only:
+            y, g, partial_in = y[:, -1:], g[:, -1:], partial_in[:, -1:]
+            blocks = tuple(b[:, -1:] for b in blocks)
         up, swiglu, down = self.ffwd.net
         if len(blocks) + 1 <= ATTN_RES_MAX_SOURCES:
             # gate, c_proj, the partial sum, the MLP's mixture and norm, the FFN

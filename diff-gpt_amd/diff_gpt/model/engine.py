@@ -21,7 +21,7 @@ from typing import Generator, Sequence
 import numpy as np
 import torch
 
-from diff_gpt.model.gpt import BaseGPT
+from diff_gpt.model.gpt import GPT, BaseGPT
 from diff_gpt.model.kv_cache import KVCache
 from diff_gpt.sampler.sampler import Sampler
 from diff_gpt.sampler.temperature import draw_one
@@ -367,6 +367,8 @@ class Engine:
             "head_dim": model.n_embd // model.n_head,
             "num_layers": model.n_layer,
         }
+        # the prefill's caller reads the last position's logits only
+        prefill_kw = {"_last_only": True} if isinstance(model, GPT) else {}
         use_graph = self.use_graph and steps > 1 and torch.device(device).type == "cuda"
         key = self._graph_key(S, N, T, steps) if use_graph else None
         kept, self._kept = self._kept, None  # taken: a concurrent call builds its own
@@ -385,14 +387,14 @@ class Engine:
                 cache = KVCache(batch_size=S, seq_len=T + steps, **geometry)
             pos_dev, cache.pos_dev = cache.pos_dev, None  # a prefill, not the captured step
             try:
-                logits, _ = model.forward(ids, kv_cache=cache)
+                logits, _ = model.forward(ids, kv_cache=cache, **prefill_kw)
             finally:
                 cache.pos_dev = pos_dev
             logits = logits[:, -1, :]
         else:
             # 1) batched prefill of the prompts
             prompt_cache = KVCache(batch_size=S, seq_len=T, **geometry)
-            logits, _ = model.forward(ids, kv_cache=prompt_cache)
+            logits, _ = model.forward(ids, kv_cache=prompt_cache, **prefill_kw)
             logits = logits[:, -1, :]
             logits = logits.expand(N, -1) if S == 1 else logits.repeat_interleave(N, dim=0)
             # 2) every row of a prompt starts from that prompt's cache, stored

@@ -174,11 +174,17 @@ class GPT(BaseGPT):
         kv_cache: KVCache | None = None,
         *,
         _argmax_out: torch.Tensor | None = None,
+        _last_only: bool = False,
     ) -> tuple[torch.Tensor, torch.Tensor | None]:
         """gpt.py:140-200.  _argmax_out (B, T) int64, when given, receives the
         first maximum of every logits row (greedy sampling without a separate
-        argmax launch)."""
+        argmax launch).  _last_only returns the (B, 1, V) logits of the last
+        position only (a prefill whose caller reads no others): every layer
+        still attends and caches every position, but the last layer's work
+        after its attention and the head run for that position alone."""
         B, T = idx.shape
+        assert not (_last_only and (targets is not None or _argmax_out is not None)), \
+            "_last_only returns the last position's logits alone"
         start = 0 if kv_cache is None else kv_cache.get_pos()
         end = start + T
         assert end <= self.freqs_cis.shape[0]
@@ -194,8 +200,12 @@ class GPT(BaseGPT):
         # first partial sum
         blocks: tuple[torch.Tensor, ...] = (x,)
         partial = x
-        for block in self.blocks:
-            blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache)
+        last = len(self.blocks) - 1
+        for i, block in enumerate(self.blocks):
+            blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache,
+                                    _last_only=_last_only and i == last)
+        if _last_only and not self.blocks:
+            partial = partial[:, -1:]
 
         logits = self._head(partial, _argmax_out)
 

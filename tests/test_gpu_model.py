@@ -324,6 +324,38 @@ def _gpt(dev, seed=0, **kw):
     return GPT(**kw).to(dev).eval()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n_embd,n_head,lpb", [(64, 4, 1), (128, 4, 2), (512, 8, 1), (512, 8, 3)])
+def test_prefill_last_only_equals_full_forward(dev, dtype, n_embd, n_head, lpb):
+    """GPT.forward(_last_only=True), the Engine's prefill: the cache holds the
+    same bits as after the full forward, and the logits are the full
+    forward's last position -- bit for bit where the layers' tails and the
+    head are the library's row kernels (n_embd 64, 128), within the
+    north-star bars where the tail's GEMMs are hipBLASLt's (a different row
+    count may pick another GEMM algorithm)."""
+    from diff_gpt.model.kv_cache import KVCache
+
+    model = _gpt(dev, vocab_size=128, n_embd=n_embd, block_size=64, n_head=n_head, n_layer=3,
+                 use_checkpoint=False, attn_res_layers_per_block=lpb).to(dtype)
+    ids = torch.randint(0, 128, (3, 40), generator=torch.Generator().manual_seed(2)).to(dev)
+    D = n_embd // n_head
+    kv_full = KVCache(batch_size=3, num_heads=n_head, seq_len=48, head_dim=D, num_layers=3)
+    kv_last = KVCache(batch_size=3, num_heads=n_head, seq_len=48, head_dim=D, num_layers=3)
+    with torch.no_grad():
+        full = model(ids, kv_cache=kv_full)[0][:, -1:]
+        last = model.forward(ids, kv_cache=kv_last, _last_only=True)[0]
+        nocache = model.forward(ids, _last_only=True)[0]
+    assert last.shape == (3, 1, 128)
+    assert kv_last.get_pos() == kv_full.get_pos() == 40
+    assert torch.equal(kv_last.kv_cache[..., :40, :], kv_full.kv_cache[..., :40, :])
+    if n_embd in (64, 128):
+        assert torch.equal(last, full)
+    else:
+        bar = (1e-5 if dtype == torch.float32 else 2e-2) * full.float().abs().max().item()
+        assert (last.float() - full.float()).abs().max().item() <= bar
+    assert (nocache.float() - last.float()).abs().max().item() <= 2e-2 * last.float().abs().max().item()
+
+
 def test_gpt_kv_cache_consistency(dev):
     # test_gpt.py:34-76, with two layers and a batch of 3
     from diff_gpt.model.kv_cache import KVCache
