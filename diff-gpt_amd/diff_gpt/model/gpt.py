@@ -179,12 +179,12 @@ class GPT(BaseGPT):
         """gpt.py:140-200.  _argmax_out (B, T) int64, when given, receives the
         first maximum of every logits row (greedy sampling without a separate
         argmax launch).  _last_only returns the (B, 1, V) logits of the last
-        position only (a prefill whose caller reads no others): every layer
-        still attends and caches every position, but the last layer's work
-        after its attention and the head run for that position alone."""
+        position only (a prefill whose caller reads no others; _argmax_out is
+        then (B, 1)): every layer still attends and caches every position, but
+        the last layer's work after its attention and the head run for that
+        position alone."""
         B, T = idx.shape
-        assert not (_last_only and (targets is not None or _argmax_out is not None)), \
-            "_last_only returns the last position's logits alone"
+        assert not (_last_only and targets is not None), "_last_only returns the last position's logits alone"
         start = 0 if kv_cache is None else kv_cache.get_pos()
         end = start + T
         assert end <= self.freqs_cis.shape[0]
@@ -243,12 +243,13 @@ class GPT(BaseGPT):
         greedy = type(sampler) is TemperatureSampler and sampler.temperature == 0
         for cur in range(T, T + max_new_tokens):
             window = out[:, max(0, cur - self.block_size) : cur]
+            # only the last position's logits are read
             if greedy:
-                am = torch.empty(window.shape, dtype=torch.int64, device=device)
-                self(window, _argmax_out=am)
+                am = torch.empty((B, 1), dtype=torch.int64, device=device)
+                self(window, _argmax_out=am, _last_only=True)
                 out[:, cur] = am[:, -1]
                 continue
-            logits, _ = self(window)
+            logits, _ = self(window, _last_only=True)
             last = logits[:, -1]
             if sampler is not None:
                 nxt = sampler(last, rng=rng)
