@@ -334,3 +334,42 @@ def test_engine_double_graph_equals_eager(dev):
             ids.append(nxt)
             logits = model(torch.tensor([[nxt]], device=dev), kv_cache=kv)[0][:, -1]
     assert all(r == ids for r in rows)
+
+
+def _random_f64_attn(seed, n):
+    """Seeded (B, H, Tq, Tk, D): decode, causal and chunked, D even up to 1024."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        D = 2 * int(rng.integers(1, 513))
+        B, H = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        Tk = int(rng.integers(1, 700))
+        kind = rng.integers(0, 3)
+        Tq = 1 if kind == 0 else Tk if kind == 1 else int(rng.integers(1, Tk + 1))
+        out.append((B, H, Tq, Tk, D))
+    return out
+
+
+@pytest.mark.parametrize("shape", _random_f64_attn(64, 10), ids=lambda s: "x".join(map(str, s)))
+def test_attention_f64_random_shapes(dev, shape):
+    """dg_attention in float64 at seeded random shapes against float64 brute force."""
+    test_attention_f64(dev, shape)
+
+
+@pytest.mark.parametrize("seed", [5, 6, 7])
+def test_rope_f64_random_shapes(dev, seed):
+    """Seeded random (B, T, H, D) rotations in float64 with a float64 table:
+    bit-exact against the oracle."""
+    from diff_gpt import _native
+    from diff_gpt.model.rope import precompute_freqs_cis
+
+    rng = np.random.default_rng(seed)
+    B, T, H = (int(x) for x in rng.integers(1, 9, size=3))
+    D = 2 * int(rng.integers(1, 513))
+    pos = int(rng.integers(0, 100))
+    x = _randn((B, T, H, D), seed, 2.0)
+    fc = precompute_freqs_cis(D, pos + T, 10000).double()[pos:pos + T].view(1, T, 1, D // 2, 2)
+    out = torch.empty((B, T, H, D), dtype=torch.float64, device=dev)
+    _native.ops().rope_qknorm_append(x.to(dev), None, None, fc.to(dev), out, None, None, False)
+    exp = on.rope_f64(x.numpy(), np.broadcast_to(fc.numpy(), (B, T, H, D // 2, 2)))
+    assert np.array_equal(out.cpu().numpy().view(np.uint64), exp.view(np.uint64))
