@@ -140,6 +140,13 @@ struct RowNormArgs {
   int64_t x_ld, out_ld, M;
   int N;
   int vec;  // 1 when every lane slice is aligned for CH-element vector access
+  // dg_embed_norm: row r of x is row ids[r] of the table (ids outside
+  // [0, V) give NaN rows), and out2, when set, receives the norm of the
+  // stored (rounded) out row
+  const int64_t* ids;
+  int64_t V;
+  void* out2;
+  int64_t out2_ld;
 };
 
 template <typename T, int NPAD, int CH>
@@ -152,7 +159,14 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const RowNormArgs a) {
   const int64_t row = (int64_t)blockIdx.x * ROWS_PER_BLOCK + threadIdx.x / G;
   if (row >= a.M) return;
   const int c0 = sub * CH;
-  const T* xs = static_cast<const T*>(a.x) + row * a.x_ld + c0;
+  int64_t src = row;
+  bool bad = false;
+  if (a.ids != nullptr) {  // uniform over the grid
+    const int64_t id = a.ids[row];
+    bad = id < 0 || id >= a.V;
+    src = bad ? 0 : id;
+  }
+  const T* xs = static_cast<const T*>(a.x) + src * a.x_ld + c0;
   float x[CH];
   if (a.vec && c0 + CH <= a.N) {
     load_vec<T, CH>(xs, x);
@@ -160,15 +174,37 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const RowNormArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) x[i] = (c0 + i < a.N) ? to_f32(xs[i]) : 0.f;
   }
-  float sq[CH];
+  if (bad) {
 #pragma unroll
-  for (int i = 0; i < CH; ++i) sq[i] = x[i] * x[i];
-  float ss = tree_sum<CH>(sq);
-  ss = group_sum<G>(ss);
-  const float mean = ss / (float)a.N;
-  const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+    for (int i = 0; i < CH; ++i) x[i] = __builtin_nanf("");
+  }
+  auto norm = [&](float (&v)[CH]) __attribute__((always_inline)) {
+    float sq[CH];
 #pragma unroll
-  for (int i = 0; i < CH; ++i) x[i] = x[i] * r;
+    for (int i = 0; i < CH; ++i) sq[i] = v[i] * v[i];
+    float ss = tree_sum<CH>(sq);
+    ss = group_sum<G>(ss);
+    const float mean = ss / (float)a.N;
+    const float r = 1.0f / sqrtf(mean + FLT_EPSILON);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) v[i] = v[i] * r;
+  };
+  norm(x);
+  if (a.out2 != nullptr) {  // uniform over the grid
+    // the second norm reads the first one's stored values
+    float y[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) y[i] = (c0 + i < a.N) ? to_f32(from_f32<T>(x[i])) : 0.f;
+    norm(y);
+    T* o2 = static_cast<T*>(a.out2) + row * a.out2_ld + c0;
+    if (a.vec && c0 + CH <= a.N) {
+      store_vec<T, CH>(o2, y);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+        if (c0 + i < a.N) o2[i] = from_f32<T>(y[i]);
+    }
+  }
   T* os = static_cast<T*>(a.out) + row * a.out_ld + c0;
   if (a.vec && c0 + CH <= a.N) {
     store_vec<T, CH>(os, x);
@@ -366,7 +402,8 @@ int launch_rms(const RowNormArgs& a, hipStream_t s) {
   const bool pow2_vec = (vb == 4 || vb == 8 || vb % 16 == 0);
   b.vec = pow2_vec && aligned(a.x, vb) && aligned(a.out, vb) &&
           (a.x_ld * (int64_t)sizeof(T)) % vb == 0 && (a.out_ld * (int64_t)sizeof(T)) % vb == 0 &&
-          (CH * (int)sizeof(T)) >= 4;
+          (CH * (int)sizeof(T)) >= 4 &&
+          (a.out2 == nullptr || (aligned(a.out2, vb) && (a.out2_ld * (int64_t)sizeof(T)) % vb == 0));
   hipLaunchKernelGGL((rms_norm_kernel<T, NPAD, CH>), dim3((unsigned)blocks), dim3(256), 0, s, b);
   return check_launch("rms_norm_kernel");
 }
@@ -603,6 +640,36 @@ extern "C" int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x
     return check_launch("rms_norm_f64_kernel");
   }
   const int npad = next_pow2(N);
+  if (dtype == DG_F32) return rms_pick<float>(npad, a, s);
+  if (dtype == DG_BF16) return rms_pick<bf16_t>(npad, a, s);
+  return rms_pick<f16_t>(npad, a, s);
+}
+
+extern "C" int dg_embed_norm(int64_t M, int C, int dtype, const int64_t* ids, int64_t V, const void* table,
+                             int64_t table_ld, void* x_out, int64_t x_ld, void* xn_out, int64_t xn_ld,
+                             void* stream) {
+  DG_REQUIRE(M >= 0 && C >= 1 && V >= 1, DG_EINVAL, "embed_norm: bad sizes M=%lld C=%d V=%lld", (long long)M, C,
+             (long long)V);
+  DG_REQUIRE(C <= 8192, DG_EUNSUPPORTED, "embed_norm: C=%d > 8192", C);
+  DG_REQUIRE(dtype == DG_F32 || dtype == DG_BF16 || dtype == DG_F16, DG_EUNSUPPORTED,
+             "embed_norm: dtype %d unsupported", dtype);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(ids && table && x_out, DG_EINVAL, "embed_norm: NULL pointer");
+  DG_REQUIRE(table_ld >= C && x_ld >= C && (xn_out == nullptr || xn_ld >= C), DG_EINVAL,
+             "embed_norm: row stride smaller than C");
+  RowNormArgs a{};
+  a.x = table;
+  a.out = x_out;
+  a.x_ld = table_ld;
+  a.out_ld = x_ld;
+  a.M = M;
+  a.N = C;
+  a.ids = ids;
+  a.V = V;
+  a.out2 = xn_out;
+  a.out2_ld = xn_ld;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int npad = next_pow2(C);
   if (dtype == DG_F32) return rms_pick<float>(npad, a, s);
   if (dtype == DG_BF16) return rms_pick<bf16_t>(npad, a, s);
   return rms_pick<f16_t>(npad, a, s);

@@ -148,6 +148,12 @@ _SIGNATURES = {
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
          ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
     ),
+    "dg_embed_norm": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p],
+    ),
     "dg_copy4d": (
         ctypes.c_int,
         [ctypes.c_int, ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p,
@@ -575,6 +581,35 @@ def rms_norm_(x: torch.Tensor, out: torch.Tensor) -> None:
         x2.size(0), N, _dtype_code(x2), _ptr(x2), x2.stride(0), _ptr(o2), o2.stride(0), _stream(x2)
     )
     _check(rc, "rms_norm")
+
+
+def embed_norm_(ids: torch.Tensor, table: torch.Tensor, x_out: torch.Tensor,
+                xn_out: torch.Tensor | None) -> bool:
+    """x_out = rms_norm(table[ids]) and, when given, xn_out = rms_norm(x_out)
+    in one dg_embed_norm launch (bits of the separate launches; ids outside
+    the table give NaN rows).  False, with nothing launched, for what it does
+    not take: fp64, C > 8192, a table or output without unit column stride."""
+    V, C = table.shape
+    if table.dtype not in (torch.float32, torch.bfloat16, torch.float16) or C > 8192:
+        return False
+    if table.stride(1) != 1 or ids.dtype != torch.int64:
+        return False
+    outs = [x_out] if xn_out is None else [x_out, xn_out]
+    o2 = []
+    for o in outs:
+        if o.dtype != table.dtype or not o.is_contiguous() or o.numel() != ids.numel() * C:
+            return False
+        o2.append(o.view(-1, C))
+    i1 = ids.reshape(-1)
+    if not i1.is_contiguous():
+        i1 = i1.contiguous()
+    xn2 = o2[1] if xn_out is not None else None
+    rc = lib().dg_embed_norm(
+        i1.numel(), C, _dtype_code(table), _ptr(i1), V, _ptr(table), table.stride(0),
+        _ptr(o2[0]), C, _ptr(xn2), C, _stream(table),
+    )
+    _check(rc, "embed_norm")
+    return True
 
 
 def copy4d_(src: torch.Tensor, dst: torch.Tensor) -> None:

@@ -91,14 +91,17 @@ class Block(nn.Module):
         kv_cache: KVCache | None,
         *,
         _last_only: bool = False,
+        _xn: torch.Tensor | None = None,
     ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
         """block.py:87-107.  With _last_only the attention still runs over
         every position (its keys and values go to the cache), and the rest of
         the layer only for the last one: the outputs are that position's
         (B, 1, C) rows, for a last layer whose other rows only the logits of
-        their own positions would read."""
+        their own positions would read.  _xn, when given, is the attention
+        sub-layer's input attn_res_norm(blocks, partial_block) computed by the
+        caller (layer 0's, from the embedding launch)."""
         _native.require_device("Block", partial_block)
-        xn = attn_res_norm(blocks, partial_block, self.attn_res_proj)
+        xn = attn_res_norm(blocks, partial_block, self.attn_res_proj) if _xn is None else _xn
         committed = self._at_boundary()
         partial_in = partial_block
         if committed:

@@ -167,6 +167,21 @@ class GPT(BaseGPT):
             argmax_out.copy_(torch.argmax(logits, dim=-1))
         return logits
 
+    def _embed(self, idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
+        """x = rms_norm(token_embedding_table(idx)) (gpt.py:154-155) and, when there
+        is a layer 0, rms_norm(x): one dg_embed_norm launch.  An id outside the
+        vocabulary gives a NaN row (nn.Embedding raises).  fp64 tables take
+        nn.Embedding and the RMSNorm kernel."""
+        table = self.token_embedding_table.weight
+        _native.require_device("GPT", idx, table)
+        _native.require_inference("GPT", table)
+        C = table.size(1)
+        x = torch.empty((*idx.shape, C), dtype=table.dtype, device=table.device)
+        xn0 = torch.empty_like(x) if self.blocks else None
+        if _native.embed_norm_(idx, table, x, xn0):
+            return x, xn0
+        return rms_norm(self.token_embedding_table(idx)), None
+
     def forward(
         self,
         idx: torch.Tensor,
@@ -195,7 +210,9 @@ class GPT(BaseGPT):
         else:
             freqs_cis = self.freqs_cis[start:end].view(1, T, 1, -1, 2)
 
-        x = rms_norm(self.token_embedding_table(idx))
+        # the normalised embedding and, when layer 0 reads it, layer 0's
+        # attention input rms_norm(x) (its one-block mixture) in one launch
+        x, xn0 = self._embed(idx)
         # Block-AttnRes state: the normalised embedding is block 0 and also the
         # first partial sum
         blocks: tuple[torch.Tensor, ...] = (x,)
@@ -203,7 +220,7 @@ class GPT(BaseGPT):
         last = len(self.blocks) - 1
         for i, block in enumerate(self.blocks):
             blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache,
-                                    _last_only=_last_only and i == last)
+                                    _last_only=_last_only and i == last, _xn=xn0 if i == 0 else None)
         if _last_only and not self.blocks:
             partial = partial[:, -1:]
 

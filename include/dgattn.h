@@ -354,6 +354,19 @@ DG_API int dg_rms_norm(int64_t M, int N, int dtype, const void* x, int64_t x_ld,
                 void* out, int64_t out_ld, void* stream);
 
 /*
+ * Token embedding and the RMSNorms that follow it, in one launch:
+ * x_out[r] = rms_norm(table[ids[r]]) (gpt.py:154-155, nn.Embedding then
+ * rms_norm) and, when xn_out is not NULL, xn_out[r] = rms_norm(x_out[r]) as
+ * stored, the normalised input of layer 0's attention (block.py:95-97 with
+ * the single-block short cut of block.py:27-28).  Both give dg_rms_norm's
+ * bits for the same rows.  An id outside [0, V) gives a NaN row instead of
+ * reading outside the table.  fp32 / bf16 / fp16, C <= 8192.
+ */
+DG_API int dg_embed_norm(int64_t M, int C, int dtype, const int64_t* ids, int64_t V,
+                  const void* table, int64_t table_ld, void* x_out, int64_t x_ld,
+                  void* xn_out, int64_t xn_ld, void* stream);
+
+/*
  * Strided 4-D copy dst[i0,i1,i2,i3] = src[i0,i1,i2,i3] over shape[4], element
  * strides per tensor (a 0 src stride broadcasts).  Serves KVCache.insert_kv's
  * append (kv_cache.py:108-109) and growth copy (kv_cache.py:100-106) and

@@ -148,6 +148,13 @@ def test_float64_declined_where_no_float64_form():
     assert b"dtype" in lib.dg_last_error()
     assert lib.dg_attention_workspace_size(1, 1, 1, 4096, 64, F64) == 0
     assert lib.dg_rms_norm(4, 64, 4, fake, 64, fake, 64, nul) == -2
+    assert lib.dg_embed_norm(4, 64, F64, fake, 8, fake, 64, fake, 64, nul, 64, nul) == -2
+    assert b"dtype" in lib.dg_last_error()
+    # embed_norm: empty table, row too long, stride below C; no rows is a no-op
+    assert lib.dg_embed_norm(4, 64, 0, fake, 0, fake, 64, fake, 64, nul, 64, nul) == -1
+    assert lib.dg_embed_norm(4, 10000, 0, fake, 8, fake, 10000, fake, 10000, nul, 10000, nul) == -2
+    assert lib.dg_embed_norm(4, 64, 0, fake, 8, fake, 32, fake, 64, nul, 64, nul) == -1
+    assert lib.dg_embed_norm(0, 64, 0, nul, 8, nul, 64, nul, 64, nul, 64, nul) == 0
 
 
 def test_block_kernel_argument_errors():

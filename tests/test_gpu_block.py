@@ -492,3 +492,99 @@ def test_gpt_layers_with_fused_block_out_match_separate_launches(dev, dtype, lay
         with torch.no_grad():
             ref = tr.forward(p, cfg, idx)[:, -1]
         assert _rel(fused[0], ref) <= 1e-5
+
+
+EMB = [  # (rows, C, vocab)
+    (6400, 64, 256),  # cfg1 decode step: one token per trajectory
+    (37, 64, 96),     # ragged row count
+    (512, 512, 1024),
+    (5, 1024, 64),
+    (9, 48, 33),      # C not a power of two (no vector access)
+    (3, 8192, 16),    # widest row
+    (4, 1, 8),
+]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", EMB, ids=lambda s: "x".join(map(str, s)))
+def test_embed_norm_is_embedding_then_rms_norm_bit_for_bit(dev, dtype, shape):
+    """dg_embed_norm writes rms_norm(table[ids]) and rms_norm of that row as
+    stored: the bits of nn.Embedding followed by dg_rms_norm twice, and the
+    fp32 oracle within the dtype's bar."""
+    from diff_gpt import _native
+
+    M, C, V = shape
+    table = _randn((V, C), 11, dtype, 0.7)
+    ids = torch.randint(0, V, (M,), generator=torch.Generator().manual_seed(3))
+    t, i = table.to(dev), ids.to(dev)
+    x = torch.empty((M, C), dtype=t.dtype, device=dev)
+    xn = torch.empty_like(x)
+    assert _native.embed_norm_(i, t, x, xn)
+    sep_x = _native.ops().rms_norm(torch.nn.functional.embedding(i, t))
+    sep_xn = _native.ops().rms_norm(sep_x)
+    assert torch.equal(x, sep_x) and torch.equal(xn, sep_xn)
+    ref = tr.rms(table.float()[ids])
+    assert _rel(x, ref) <= TOL[dtype]
+    assert _rel(xn, tr.rms(x.float().cpu())) <= TOL[dtype]
+    # without the second output
+    x1 = torch.empty_like(x)
+    assert _native.embed_norm_(i, t, x1, None)
+    assert torch.equal(x1, sep_x)
+
+
+def test_embed_norm_bad_ids_give_nan_rows(dev):
+    """An id outside [0, V) reads nothing outside the table: its rows are NaN,
+    the other rows are those of valid ids."""
+    from diff_gpt import _native
+
+    table = _randn((16, 64), 5, "f32").to(dev)
+    ids = torch.tensor([3, -1, 16, 15, 1 << 40, 0], device=dev)
+    x = torch.empty((6, 64), device=dev)
+    xn = torch.empty_like(x)
+    assert _native.embed_norm_(ids, table, x, xn)
+    bad = torch.tensor([False, True, True, False, True, False])
+    xc, xnc = x.cpu(), xn.cpu()
+    assert bool(xc[bad].isnan().all()) and bool(xnc[bad].isnan().all())
+    good = ids.cpu()[~bad]
+    assert torch.equal(xc[~bad], _native.ops().rms_norm(table[good.to(dev)]).cpu())
+
+
+def test_embed_norm_declines_fp64_and_strided_tables(dev):
+    from diff_gpt import _native
+
+    ids = torch.zeros(4, dtype=torch.int64, device=dev)
+    t64 = torch.randn(8, 64, dtype=torch.float64, device=dev)
+    x64 = torch.full((4, 64), 5.0, dtype=torch.float64, device=dev)
+    assert not _native.embed_norm_(ids, t64, x64, None)
+    tT = torch.randn(64, 8, device=dev).t()
+    x = torch.full((4, 64), 5.0, device=dev)
+    assert not _native.embed_norm_(ids, tT, x, None)
+    torch.cuda.synchronize()
+    assert bool((x64 == 5.0).all()) and bool((x == 5.0).all())
+
+
+def test_gpt_embedding_launch_feeds_layer_zero(dev, monkeypatch):
+    """GPT.forward gathers and normalises the embedding and layer 0's
+    attention input in one dg_embed_norm launch; with it declined (nn.Embedding,
+    then the RMSNorm kernel and layer 0's own norm) the logits are equal."""
+    from diff_gpt import _native
+    from diff_gpt.model.gpt import GPT
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=128, n_embd=64, block_size=32, n_head=4, n_layer=2,
+                use_checkpoint=False).eval().to(dev).to(torch.bfloat16)
+    idx = torch.randint(0, 128, (3, 17), generator=torch.Generator().manual_seed(4)).to(dev)
+    calls = [0]
+    real = _native.embed_norm_
+
+    def counted(*a, **k):
+        calls[0] += 1
+        return real(*a, **k)
+
+    with torch.inference_mode():
+        monkeypatch.setattr(_native, "embed_norm_", counted)
+        fused = model(idx)[0]
+        assert calls[0] == 1
+        monkeypatch.setattr(_native, "embed_norm_", lambda *a, **k: False)
+        separate = model(idx)[0]
+    assert torch.equal(fused, separate)
