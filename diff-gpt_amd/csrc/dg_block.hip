@@ -524,7 +524,8 @@ struct BlockOutArgs {
   const void* w_up;     // (4C, C)
   const void* w_down;   // (C, 2C)
   void* out;            // (M, C) partial sum leaving the layer
-  int64_t y_ld, g_ld, wp_ld, pin_ld, wu_ld, wd_ld, out_ld, M;
+  void* xn;             // (M, C) rms_norm(out) as stored, or null
+  int64_t y_ld, g_ld, wp_ld, pin_ld, wu_ld, wd_ld, out_ld, xn_ld, M;
   int nblk;
   float alpha, limit;
 };
@@ -783,6 +784,17 @@ __global__ __launch_bounds__(256) void block_out_kernel(const BlockOutArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = pmv[i] + rt<T>(acc[i]);
     if (store) store_vec<T, 4>(orow + f, o);
+    // the same lane alone reads and writes this slice of pm
+    if (a.xn != nullptr) store_vec<T, 4>(pm + c * LDC + f, o);  // uniform
+  }
+  // 6) dg_block_out_norm: the RMSNorm of the stored output rows (the head's
+  //    input after the last layer), 16 lanes per row
+  if (a.xn != nullptr) {  // uniform
+    __syncthreads();
+    float x[CH];
+    load_vec<T, CH>(pm + gr * LDC + gc0, x);
+    row_rms<CH, 16>(x, C);
+    if (row0 + gr < a.M) store_vec<T, CH>(static_cast<T*>(a.xn) + (row0 + gr) * a.xn_ld + gc0, x);
   }
 }
 
@@ -1048,11 +1060,11 @@ bool rows16(const void* p, int64_t ld, int64_t es) {
 }
 }  // namespace
 
-extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
-                            const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,
-                            const void* const* blocks, const int64_t* blocks_ld, const void* w_mix,
-                            const void* w_up, int64_t wu_ld, const void* w_down, int64_t wd_ld, float alpha,
-                            float limit, void* out, int64_t out_ld, void* stream) {
+static int block_out_impl(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
+                          const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,
+                          const void* const* blocks, const int64_t* blocks_ld, const void* w_mix, const void* w_up,
+                          int64_t wu_ld, const void* w_down, int64_t wd_ld, float alpha, float limit, void* out,
+                          int64_t out_ld, void* xn, int64_t xn_ld, void* stream) {
   DG_REQUIRE(M >= 0 && C >= 1, DG_EINVAL, "block_out: bad sizes M=%lld C=%d", (long long)M, C);
   DG_REQUIRE(dtype_ok(dtype), DG_EUNSUPPORTED, "block_out: dtype %d unsupported", dtype);
   DG_REQUIRE(C == 64 || C == 128, DG_EUNSUPPORTED, "block_out: n_embd %d unsupported (64 or 128)", C);
@@ -1066,9 +1078,9 @@ extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t 
   BlockOutArgs a{};
   bool ok = rows16(y, y_ld, es) && rows16(g, g_ld, es) && rows16(w_proj, wp_ld, es) && rows16(w_mix, 0, es) &&
             rows16(w_up, wu_ld, es) && rows16(w_down, wd_ld, es) && rows16(out, out_ld, es) &&
-            (partial_in == nullptr || rows16(partial_in, pin_ld, es));
+            (partial_in == nullptr || rows16(partial_in, pin_ld, es)) && (xn == nullptr || rows16(xn, xn_ld, es));
   DG_REQUIRE(y_ld >= C && g_ld >= C && wp_ld >= C && wu_ld >= C && wd_ld >= 2 * C && out_ld >= C &&
-                 (partial_in == nullptr || pin_ld >= C),
+                 (partial_in == nullptr || pin_ld >= C) && (xn == nullptr || xn_ld >= C),
              DG_EINVAL, "block_out: a row stride is narrower than its row");
   for (int n = 0; n < nblk; ++n) {
     DG_REQUIRE(blocks[n] != nullptr && blocks_ld[n] >= C, DG_EINVAL, "block_out: block %d is NULL or narrower than C",
@@ -1079,9 +1091,9 @@ extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t 
   }
   DG_REQUIRE(ok, DG_EUNSUPPORTED, "block_out: rows must be 16-byte aligned");
   a.y = y; a.g = g; a.w_proj = w_proj; a.pin = partial_in; a.w_mix = w_mix; a.w_up = w_up; a.w_down = w_down;
-  a.out = out;
+  a.out = out; a.xn = xn;
   a.y_ld = y_ld; a.g_ld = g_ld; a.wp_ld = wp_ld; a.pin_ld = pin_ld; a.wu_ld = wu_ld; a.wd_ld = wd_ld;
-  a.out_ld = out_ld; a.M = M; a.nblk = nblk; a.alpha = alpha; a.limit = limit;
+  a.out_ld = out_ld; a.xn_ld = xn_ld; a.M = M; a.nblk = nblk; a.alpha = alpha; a.limit = limit;
   const dim3 grid((unsigned)((M + kLayerRows - 1) / kLayerRows));
   hipStream_t s = static_cast<hipStream_t>(stream);
 #define DG_BLOCK_OUT(T)                                                                             \
@@ -1094,4 +1106,24 @@ extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t 
   else DG_BLOCK_OUT(f16_t);
 #undef DG_BLOCK_OUT
   return check_launch("block_out_kernel");
+}
+
+extern "C" int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g, int64_t g_ld,
+                            const void* w_proj, int64_t wp_ld, const void* partial_in, int64_t pin_ld, int nblk,
+                            const void* const* blocks, const int64_t* blocks_ld, const void* w_mix,
+                            const void* w_up, int64_t wu_ld, const void* w_down, int64_t wd_ld, float alpha,
+                            float limit, void* out, int64_t out_ld, void* stream) {
+  return block_out_impl(M, C, dtype, y, y_ld, g, g_ld, w_proj, wp_ld, partial_in, pin_ld, nblk, blocks, blocks_ld,
+                        w_mix, w_up, wu_ld, w_down, wd_ld, alpha, limit, out, out_ld, nullptr, 0, stream);
+}
+
+extern "C" int dg_block_out_norm(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g,
+                                 int64_t g_ld, const void* w_proj, int64_t wp_ld, const void* partial_in,
+                                 int64_t pin_ld, int nblk, const void* const* blocks, const int64_t* blocks_ld,
+                                 const void* w_mix, const void* w_up, int64_t wu_ld, const void* w_down,
+                                 int64_t wd_ld, float alpha, float limit, void* out, int64_t out_ld, void* xn,
+                                 int64_t xn_ld, void* stream) {
+  DG_REQUIRE(M == 0 || xn != nullptr, DG_EINVAL, "block_out_norm: NULL pointer");
+  return block_out_impl(M, C, dtype, y, y_ld, g, g_ld, w_proj, wp_ld, partial_in, pin_ld, nblk, blocks, blocks_ld,
+                        w_mix, w_up, wu_ld, w_down, wd_ld, alpha, limit, out, out_ld, xn, xn_ld, stream);
 }

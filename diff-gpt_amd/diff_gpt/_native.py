@@ -189,6 +189,14 @@ _SIGNATURES = {
          ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
          ctypes.c_int64, ctypes.c_void_p],
     ),
+    "dg_block_out_norm": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+         ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_int64), ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p],
+    ),
 }
 
 ABI_VERSION = 3
@@ -665,12 +673,13 @@ def _row_list(tensors: list[torch.Tensor], what: str):
 
 def block_out_(y: torch.Tensor, g: torch.Tensor, w_proj: torch.Tensor, partial_in: torch.Tensor | None,
                blocks: list[torch.Tensor], w_mix: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
-               alpha: float, limit: float, out: torch.Tensor) -> bool:
+               alpha: float, limit: float, out: torch.Tensor, xn_out: torch.Tensor | None = None) -> bool:
     """dg_block_out: from the attention output y (..., C) and the gate logits
     g, the layer's new partial sum into out: c_proj(y * sigmoid(g)), added to
     partial_in unless that is None (the layer commits its input), then plus
-    the FFN of the MLP mixture over blocks and that partial.  Returns False,
-    having done nothing, for shapes the fused kernel does not take."""
+    the FFN of the MLP mixture over blocks and that partial.  With xn_out
+    (dg_block_out_norm) also rms_norm(out) into it.  Returns False, having
+    done nothing, for shapes the fused kernel does not take."""
     C = out.size(-1)
     y2, g2, o2 = _rows(y, "block_out"), _rows(g, "block_out"), out.view(-1, C)
     p2 = None if partial_in is None else _rows(partial_in, "block_out")
@@ -678,12 +687,21 @@ def block_out_(y: torch.Tensor, g: torch.Tensor, w_proj: torch.Tensor, partial_i
     ws = (w_proj, w_up, w_down)
     if any(t.stride(1) != 1 or t.dtype != out.dtype for t in ws) or o2.stride(1) != 1:
         return False
-    rc = lib().dg_block_out(
+    x2 = None
+    if xn_out is not None:
+        if xn_out.dtype != out.dtype or xn_out.shape != out.shape or not xn_out.is_contiguous():
+            return False
+        x2 = xn_out.view(-1, C)
+    args = [
         o2.size(0), C, _dtype_code(o2), _ptr(y2), y2.stride(0), _ptr(g2), g2.stride(0), _ptr(w_proj),
         w_proj.stride(0), _ptr(p2), 0 if p2 is None else p2.stride(0), len(blocks), ptrs, lds,
         _ptr(w_mix.reshape(-1).contiguous()), _ptr(w_up), w_up.stride(0), _ptr(w_down), w_down.stride(0),
-        float(alpha), float(limit), _ptr(o2), o2.stride(0), _stream(o2),
-    )
+        float(alpha), float(limit), _ptr(o2), o2.stride(0),
+    ]
+    if x2 is None:
+        rc = lib().dg_block_out(*args, _stream(o2))
+    else:
+        rc = lib().dg_block_out_norm(*args, _ptr(x2), C, _stream(o2))
     if rc == DG_EUNSUPPORTED:
         return False
     _check(rc, "block_out")

@@ -92,6 +92,7 @@ class Block(nn.Module):
         *,
         _last_only: bool = False,
         _xn: torch.Tensor | None = None,
+        _xn_out: torch.Tensor | None = None,
     ) -> tuple[tuple[torch.Tensor, ...], torch.Tensor]:
         """block.py:87-107.  With _last_only the attention still runs over
         every position (its keys and values go to the cache), and the rest of
@@ -99,7 +100,10 @@ class Block(nn.Module):
         (B, 1, C) rows, for a last layer whose other rows only the logits of
         their own positions would read.  _xn, when given, is the attention
         sub-layer's input attn_res_norm(blocks, partial_block) computed by the
-        caller (layer 0's, from the embedding launch)."""
+        caller (layer 0's, from the embedding launch).  _xn_out, when given
+        (shaped as the returned partial sum), receives rms_norm of it: the
+        head's input after the last layer, from the same launch when
+        dg_block_out takes the layer."""
         _native.require_device("Block", partial_block)
         xn = attn_res_norm(blocks, partial_block, self.attn_res_proj) if _xn is None else _xn
         committed = self._at_boundary()
@@ -120,12 +124,15 @@ class Block(nn.Module):
             out = torch.empty_like(partial_in)
             if _native.block_out_(y, g, sa.c_proj.weight, None if committed else partial_in, list(blocks),
                                   self.mlp_res_proj.weight, up.weight, down.weight, swiglu.alpha, swiglu.limit,
-                                  out):
+                                  out, _xn_out):
                 return blocks, out
         _native.ops().gate_(y, g)  # y * sigmoid(g), mha.py:84
         attn_out = sa.c_proj(y)
         partial_block = attn_out if committed else partial_in + attn_out
-        return blocks, self._mlp(blocks, partial_block)
+        out = self._mlp(blocks, partial_block)
+        if _xn_out is not None:
+            _native.rms_norm_(out, _xn_out)
+        return blocks, out
 
     def _mlp(self, blocks: tuple[torch.Tensor, ...], partial_block: torch.Tensor) -> torch.Tensor:
         xn = attn_res_norm(blocks, partial_block, self.mlp_res_proj)

@@ -147,12 +147,14 @@ class GPT(BaseGPT):
         self.logit_softcap = logit_softcap
         self.label_smoothing_sigma = label_smoothing_sigma
 
-    def _head(self, partial: torch.Tensor, argmax_out: torch.Tensor | None) -> torch.Tensor:
-        """rms_norm -> tied lm_head -> softcap (gpt.py:181-186): one dg_lm_head
-        launch after the norm, which also writes each row's argmax into
-        argmax_out (B, T) when given; F.linear + dg_softcap (+ torch.argmax) for
-        shapes it does not take."""
-        xn = rms_norm(partial)
+    def _head(self, partial: torch.Tensor, argmax_out: torch.Tensor | None,
+              xn: torch.Tensor | None = None) -> torch.Tensor:
+        """rms_norm -> tied lm_head -> softcap (gpt.py:180-186): one dg_lm_head
+        launch after the norm (xn, when the last layer's launch wrote it),
+        which also writes each row's argmax into argmax_out (B, T) when given;
+        F.linear + dg_softcap (+ torch.argmax) for shapes it does not take."""
+        if xn is None:
+            xn = rms_norm(partial)
         B, T, C = xn.shape
         V = self.lm_head.weight.size(0)
         cap = float(self.logit_softcap)
@@ -218,13 +220,18 @@ class GPT(BaseGPT):
         blocks: tuple[torch.Tensor, ...] = (x,)
         partial = x
         last = len(self.blocks) - 1
+        # the head's input rms_norm(partial), written by the last layer
+        xn_head = None
+        if self.blocks:
+            xn_head = torch.empty((B, 1 if _last_only else T, x.size(-1)), dtype=x.dtype, device=x.device)
         for i, block in enumerate(self.blocks):
             blocks, partial = block(blocks, partial, freqs_cis=freqs_cis, kv_cache=kv_cache,
-                                    _last_only=_last_only and i == last, _xn=xn0 if i == 0 else None)
+                                    _last_only=_last_only and i == last, _xn=xn0 if i == 0 else None,
+                                    _xn_out=xn_head if i == last else None)
         if _last_only and not self.blocks:
             partial = partial[:, -1:]
 
-        logits = self._head(partial, _argmax_out)
+        logits = self._head(partial, _argmax_out, xn_head)
 
         loss = None
         if targets is not None:

@@ -451,6 +451,19 @@ DG_API int dg_block_out(int64_t M, int C, int dtype, const void* y, int64_t y_ld
                         const void* w_up, int64_t wu_ld, const void* w_down, int64_t wd_ld, float alpha,
                         float limit, void* out, int64_t out_ld, void* stream);
 
+/*
+ * dg_block_out that also writes xn = rms_norm(out) row by row, of the output
+ * as stored, with dg_rms_norm's bits: the last layer's output and the head's
+ * normalised input (gpt.py:180) from one launch.  Same support as
+ * dg_block_out; xn rows 16-byte aligned.
+ */
+DG_API int dg_block_out_norm(int64_t M, int C, int dtype, const void* y, int64_t y_ld, const void* g,
+                             int64_t g_ld, const void* w_proj, int64_t wp_ld, const void* partial_in,
+                             int64_t pin_ld, int nblk, const void* const* blocks, const int64_t* blocks_ld,
+                             const void* w_mix, const void* w_up, int64_t wu_ld, const void* w_down,
+                             int64_t wd_ld, float alpha, float limit, void* out, int64_t out_ld, void* xn,
+                             int64_t xn_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -588,3 +588,74 @@ def test_gpt_embedding_launch_feeds_layer_zero(dev, monkeypatch):
         monkeypatch.setattr(_native, "embed_norm_", lambda *a, **k: False)
         separate = model(idx)[0]
     assert torch.equal(fused, separate)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", LAYER, ids=lambda s: "x".join(map(str, s)))
+def test_block_out_norm_adds_the_head_norm_bit_for_bit(dev, dtype, shape):
+    """dg_block_out_norm writes dg_block_out's output bits and rms_norm of
+    them with dg_rms_norm's bits (the head's input after the last layer),
+    including the rows of a partial last tile."""
+    from diff_gpt import _native
+
+    M, C, nblk, committed = shape
+    blocks, pin, y, qkvg, w = _layer_case(M, C, nblk, dtype, 700 + C + nblk)
+    d = lambda t: t.to(dev)  # noqa: E731
+    args = (d(y), d(qkvg)[:, 3 * C:], d(w["proj"]), None if committed else d(pin), [d(b) for b in blocks],
+            d(w["mix_mlp"]), d(w["up"]), d(w["down"]), ALPHA, LIMIT)
+    out = torch.empty((M, C), dtype=TDT[dtype], device=dev)
+    assert _native.block_out_(*args, out)
+    out2 = torch.empty_like(out)
+    xn = torch.full_like(out, 7.0)
+    assert _native.block_out_(*args, out2, xn)
+    assert torch.equal(out, out2)
+    assert torch.equal(xn, _native.ops().rms_norm(out))
+    assert _rel(xn, tr.rms(out.float().cpu())) <= TOL[dtype]
+
+
+def test_gpt_head_norm_from_the_last_layer(dev, monkeypatch):
+    """GPT.forward takes the head's RMSNorm from the last layer's
+    dg_block_out_norm launch; with the fused layer declined (separate
+    launches, then dg_rms_norm) the logits agree within the bf16 bar, and a
+    forward with the head norm taken from dg_rms_norm instead gives equal
+    logits."""
+    from diff_gpt import _native
+    from diff_gpt.model.gpt import GPT
+    from diff_gpt.model.kv_cache import KVCache
+
+    torch.manual_seed(0)
+    model = GPT(vocab_size=128, n_embd=64, block_size=32, n_head=4, n_layer=3,
+                use_checkpoint=False).eval().to(dev).to(torch.bfloat16)
+    idx = torch.randint(0, 128, (3, 17), generator=torch.Generator().manual_seed(5)).to(dev)
+    real = _native.block_out_
+    seen = []
+
+    def counted(*a, **k):
+        seen.append(len(a) > 11 and a[11] is not None)
+        return real(*a, **k)
+
+    def without_norm(*a, **k):
+        ok = real(*a[:11], **k)
+        if ok and len(a) > 11 and a[11] is not None:
+            _native.rms_norm_(a[10], a[11])
+        return ok
+
+    def run():
+        kv = KVCache(batch_size=3, num_heads=4, seq_len=18, head_dim=16, num_layers=3)
+        with torch.inference_mode():
+            first = model(idx, kv_cache=kv)[0]
+            step = model(first[:, -1].argmax(-1, keepdim=True), kv_cache=kv)[0]
+            last = model(idx, _last_only=True)[0]
+        return first, step, last
+
+    monkeypatch.setattr(_native, "block_out_", counted)
+    fused = run()
+    assert seen == [False, False, True] * 3
+    monkeypatch.setattr(_native, "block_out_", without_norm)
+    same = run()
+    for f_, s_ in zip(fused, same):
+        assert torch.equal(f_, s_)
+    monkeypatch.setattr(_native, "block_out_", lambda *a, **k: False)
+    separate = run()
+    for f_, s_ in zip(fused, separate):
+        assert _rel(f_, s_.double().cpu()) <= TOL["bf16"]
