@@ -23,6 +23,8 @@
 // rms_norm_kernel, so they produce its bits for the same row.
 #include <float.h>
 
+#include <type_traits>
+
 #include "dg_common.h"
 
 namespace dg {
@@ -1126,4 +1128,82 @@ extern "C" int dg_block_out_norm(int64_t M, int C, int dtype, const void* y, int
   DG_REQUIRE(M == 0 || xn != nullptr, DG_EINVAL, "block_out_norm: NULL pointer");
   return block_out_impl(M, C, dtype, y, y_ld, g, g_ld, w_proj, wp_ld, partial_in, pin_ld, nblk, blocks, blocks_ld,
                         w_mix, w_up, wu_ld, w_down, wd_ld, alpha, limit, out, out_ld, xn, xn_ld, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The sampler's draw (torch.multinomial's one-sample method, temperature.py:
+// 24-25 after the softmax): ids[r] = the first maximum over j of
+// probs[r, j] / q[r, j], with q the caller's Exp(1) variates.  The quotient
+// is rounded to the storage dtype as torch's division returns it (fp32
+// arithmetic, correctly rounded; fp64 for fp64 data), and compared as
+// torch.argmax compares: a NaN is above every number, the first of equal
+// values (or of NaNs) wins.  One wave per row; lane l takes entries l,
+// l + 64, ... so each lane meets its entries in increasing order.
+// ---------------------------------------------------------------------------
+namespace dg {
+
+template <typename C>
+__device__ __forceinline__ bool draw_better(C v, int i, C bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void draw_argmax_kernel(const T* probs, int64_t p_ld, const T* q, int64_t q_ld,
+                                                          int64_t* ids, int64_t M, int V) {
+  using C = typename std::conditional<sizeof(T) == 8, double, float>::type;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // whole waves
+  const T* pr = probs + row * p_ld;
+  const T* qr = q + row * q_ld;
+  C best = (C)0;
+  int bi = 0x7fffffff;
+  for (int j = lane; j < V; j += 64) {
+    C v;
+    if constexpr (sizeof(T) == 8) {
+      v = (C)pr[j] / (C)qr[j];
+    } else {
+      v = (C)to_f32(from_f32<T>(to_f32(pr[j]) / to_f32(qr[j])));
+    }
+    if (bi == 0x7fffffff || draw_better<C>(v, j, best, bi)) {
+      best = v;
+      bi = j;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const C ov = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (oi != 0x7fffffff && (bi == 0x7fffffff || draw_better<C>(ov, oi, best, bi))) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) ids[row] = bi;
+}
+
+}  // namespace dg
+
+extern "C" int dg_draw_argmax(int64_t M, int V, int dtype, const void* probs, int64_t p_ld, const void* q,
+                              int64_t q_ld, int64_t* ids, void* stream) {
+  using namespace dg;
+  DG_REQUIRE(M >= 0 && V >= 1, DG_EINVAL, "draw_argmax: bad sizes M=%lld V=%d", (long long)M, V);
+  DG_REQUIRE(dtype_ok_f64(dtype), DG_EUNSUPPORTED, "draw_argmax: dtype %d unsupported", dtype);
+  if (M == 0) return DG_OK;
+  DG_REQUIRE(probs && q && ids, DG_EINVAL, "draw_argmax: NULL pointer");
+  DG_REQUIRE(p_ld >= V && q_ld >= V, DG_EINVAL, "draw_argmax: a row stride is narrower than its row");
+  DG_REQUIRE(M <= 4 * 0x7fffffffLL, DG_EINVAL, "draw_argmax: too many rows (%lld)", (long long)M);
+  const dim3 grid((unsigned)((M + 3) / 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define DG_DRAW(T)                                                                                 \
+  hipLaunchKernelGGL((draw_argmax_kernel<T>), grid, dim3(256), 0, s, static_cast<const T*>(probs), p_ld, \
+                     static_cast<const T*>(q), q_ld, ids, M, V)
+  if (dtype == DG_F32) DG_DRAW(float);
+  else if (dtype == DG_BF16) DG_DRAW(bf16_t);
+  else if (dtype == DG_F16) DG_DRAW(f16_t);
+  else DG_DRAW(double);
+#undef DG_DRAW
+  return check_launch("draw_argmax_kernel");
 }

@@ -189,6 +189,11 @@ _SIGNATURES = {
          ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64, ctypes.c_float, ctypes.c_float, ctypes.c_void_p,
          ctypes.c_int64, ctypes.c_void_p],
     ),
+    "dg_draw_argmax": (
+        ctypes.c_int,
+        [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p],
+    ),
     "dg_block_out_norm": (
         ctypes.c_int,
         [ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
@@ -617,6 +622,24 @@ def embed_norm_(ids: torch.Tensor, table: torch.Tensor, x_out: torch.Tensor,
         _ptr(o2[0]), C, _ptr(xn2), C, _stream(table),
     )
     _check(rc, "embed_norm")
+    return True
+
+
+def draw_argmax_(probs: torch.Tensor, q: torch.Tensor, ids: torch.Tensor) -> bool:
+    """ids (..., 1) int64 = torch.argmax(probs / q, dim=-1, keepdim=True) in one
+    dg_draw_argmax launch.  False, with nothing launched, for operands it
+    does not take (rows without unit column stride, mixed dtypes)."""
+    V = probs.size(-1)
+    if q.shape != probs.shape or q.dtype != probs.dtype or probs.dtype not in _DTYPE_CODE:
+        return False
+    if ids.dtype != torch.int64 or not ids.is_contiguous() or ids.numel() * V != probs.numel():
+        return False
+    p2, q2 = probs.reshape(-1, V), q.reshape(-1, V)
+    if p2.stride(-1) != 1 or q2.stride(-1) != 1:
+        return False
+    rc = lib().dg_draw_argmax(p2.size(0), V, _dtype_code(p2), _ptr(p2), p2.stride(0), _ptr(q2), q2.stride(0),
+                              _ptr(ids), _stream(p2))
+    _check(rc, "draw_argmax")
     return True
 
 

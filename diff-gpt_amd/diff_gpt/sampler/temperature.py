@@ -2,7 +2,9 @@
 
 T == 0 is argmax (first maximum wins); otherwise one multinomial draw from
 softmax(logits / T) with the caller's generator, on the logits' device.
-Kept on torch so the RNG stream is torch's.
+The softmax and the Exp(1) variates stay torch's, so the RNG stream is
+torch's; on the device the quotient and its argmax are one dg_draw_argmax
+launch.
 """
 
 import torch
@@ -20,6 +22,13 @@ def draw_one(probs: torch.Tensor, rng: torch.Generator | None = None) -> torch.T
     with inf, nan or negative entries, or summing to 0, which multinomial
     would reject, get an id here."""
     q = torch.empty_like(probs).exponential_(1, generator=rng)
+    if probs.is_cuda:
+        # the quotient and its first maximum in one launch (dg_draw_argmax)
+        from diff_gpt import _native
+
+        ids = torch.empty((*probs.shape[:-1], 1), dtype=torch.int64, device=probs.device)
+        if _native.draw_argmax_(probs, q, ids):
+            return ids
     return torch.argmax(probs / q, dim=-1, keepdim=True)
 
 

@@ -464,6 +464,18 @@ DG_API int dg_block_out_norm(int64_t M, int C, int dtype, const void* y, int64_t
                              int64_t wd_ld, float alpha, float limit, void* out, int64_t out_ld, void* xn,
                              int64_t xn_ld, void* stream);
 
+/*
+ * The sampler's draw (temperature.py:24-25, torch.multinomial with one
+ * sample, by its Exp(1) method): ids[r] = the first index of the maximum of
+ * probs[r, j] / q[r, j] over j < V, q the caller's Exp(1) variates (torch's
+ * exponential_ on the caller's generator, so the random stream stays
+ * torch's).  The quotient is rounded to the data dtype and compared as
+ * torch.argmax does (NaN above every number, first of equals wins): the
+ * ids of torch.argmax(probs / q, -1).  fp32 / bf16 / fp16 / fp64.
+ */
+DG_API int dg_draw_argmax(int64_t M, int V, int dtype, const void* probs, int64_t p_ld, const void* q,
+                   int64_t q_ld, int64_t* ids, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

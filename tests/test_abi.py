@@ -151,6 +151,9 @@ def test_float64_declined_where_no_float64_form():
     assert b"NULL" in lib.dg_last_error()
     assert lib.dg_block_out_norm(16, 96, 0, fake, 96, fake, 96, fake, 96, nul, 0, 1, ptrs, lds, fake, fake, 96,
                                  fake, 192, 1.702, 7.0, fake, 96, fake, 96, nul) == -2
+    assert lib.dg_draw_argmax(4, 256, 5, fake, 256, fake, 256, fake, nul) == -2
+    assert lib.dg_draw_argmax(4, 256, 0, fake, 128, fake, 256, fake, nul) == -1
+    assert lib.dg_draw_argmax(0, 256, 0, nul, 256, nul, 256, nul, nul) == 0
     assert lib.dg_attention_workspace_size(1, 1, 1, 4096, 64, F64) == 0
     assert lib.dg_rms_norm(4, 64, 4, fake, 64, fake, 64, nul) == -2
     assert lib.dg_embed_norm(4, 64, F64, fake, 8, fake, 64, fake, 64, nul, 64, nul) == -2

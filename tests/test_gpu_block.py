@@ -659,3 +659,50 @@ def test_gpt_head_norm_from_the_last_layer(dev, monkeypatch):
     separate = run()
     for f_, s_ in zip(fused, separate):
         assert _rel(f_, s_.double().cpu()) <= TOL["bf16"]
+
+
+DRAW = [(6400, 256), (37, 96), (5, 1), (3, 1000), (2, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16", "f64"])
+@pytest.mark.parametrize("shape", DRAW, ids=lambda s: "x".join(map(str, s)))
+def test_draw_argmax_equals_torch_argmax_of_quotient(dev, dtype, shape):
+    """dg_draw_argmax gives torch.argmax(probs / q, -1)'s ids on the device,
+    with ties (repeated probabilities and variates), zeros, an infinite
+    quotient and NaN rows planted."""
+    from diff_gpt import _native
+
+    M, V = shape
+    dt = torch.float64 if dtype == "f64" else TDT[dtype]
+    g = torch.Generator().manual_seed(9 + V)
+    probs = torch.softmax(torch.randn((M, V), generator=g, dtype=torch.float64) * 2, -1)
+    q = torch.empty((M, V), dtype=torch.float64).exponential_(1, generator=g)
+    if V >= 4:
+        probs[0, :4] = 0.25  # ties
+        q[0, :4] = 1.0
+        probs[1 % M, 2] = 0.0
+        q[min(2, M - 1), 3] = 0.0  # an infinite quotient (or 0/0)
+        probs[M - 1, V // 2] = float("nan")
+        probs[M - 1, V - 1] = float("nan")
+    p, qq = probs.to(dt).to(dev), q.to(dt).to(dev)
+    ids = torch.empty((M, 1), dtype=torch.int64, device=dev)
+    assert _native.draw_argmax_(p, qq, ids)
+    assert torch.equal(ids, torch.argmax(p / qq, dim=-1, keepdim=True))
+    # the oracle's statement on the host
+    assert torch.equal(ids.cpu(), torch.argmax(p.cpu() / qq.cpu(), dim=-1, keepdim=True))
+
+
+def test_temperature_sampler_draw_is_multinomial(dev):
+    """The sampler's one-launch draw gives torch.multinomial's ids on the same
+    generator state (its one-sample method) for a temperature-1 step."""
+    from diff_gpt.sampler.temperature import TemperatureSampler
+
+    logits = torch.randn((640, 256), generator=torch.Generator().manual_seed(3)).to(dev)
+    s = TemperatureSampler(1.0)
+    g1 = torch.Generator(device=dev)
+    g1.manual_seed(11)
+    got = s(logits, rng=g1)
+    g2 = torch.Generator(device=dev)
+    g2.manual_seed(11)
+    ref = torch.multinomial(torch.softmax(logits, -1), 1, generator=g2)
+    assert torch.equal(got, ref)
